@@ -1,0 +1,141 @@
+/*
+ * tropnn_hip.h -- C ABI of libtropnn_hip.so, the MI355X (gfx950) PairwiseLinear
+ * hot path: comparator route, LUT row gather-sum, min-margin STE backward.
+ *
+ * Conventions (the precedent is the reference's Zig C ABI, kernels/src/lut.zig:248-318,
+ * bound with ctypes at backends/pairwise_zig.py:19-32):
+ *   - the caller owns every buffer; all tensor pointers are DEVICE pointers to
+ *     contiguous row-major arrays; the library never allocates;
+ *   - dims are passed by value; anchors are int64 [tables, comparisons, 2]
+ *     (the torch buffer's dtype, layers/pairwise.py:57);
+ *   - every call is asynchronous on `stream` (a hipStream_t; NULL = the null
+ *     stream) and never synchronises the device;
+ *   - every entry point returns TROPNN_OK (0) or an error code, and
+ *     tropnn_hip_last_error() returns the calling thread's last message
+ *     (the reference's Zig ABI has no error channel; its Python wrappers
+ *     validate first, and so does this library, before any launch);
+ *   - stateless and re-entrant: calls on different streams may overlap as
+ *     long as they write disjoint buffers.
+ */
+#ifndef TROPNN_HIP_H
+#define TROPNN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TROPNN_HIP_ABI_VERSION 1
+
+/* status codes */
+#define TROPNN_OK 0
+#define TROPNN_ERR_INVALID_ARGUMENT 1 /* bad shape, pointer, enum or size */
+#define TROPNN_ERR_UNSUPPORTED 2      /* valid for the reference, not implemented here */
+#define TROPNN_ERR_HIP 3              /* a HIP runtime call failed */
+
+/* element type of the LUT the kernels read */
+#define TROPNN_LUT_F32 0
+#define TROPNN_LUT_F16 1 /* IEEE binary16, rows converted to f32, f32 accumulation */
+
+/* surrogate gradient of the Heaviside step (layers/surrogate.py:9-25) */
+#define TROPNN_SURROGATE_FAST_SIGMOID_ODD 0
+#define TROPNN_SURROGATE_IZHIKEVICH 1
+
+/* which comparisons carry the STE gradient (layers/pairwise.py:137-200) */
+#define TROPNN_STE_MIN_MARGIN 0
+#define TROPNN_STE_FULL 1
+
+/* Largest `comparisons` the kernels take (LUT rows per table = 2^comparisons). */
+#define TROPNN_MAX_COMPARISONS 8
+
+/* Route record: one 8-byte entry per (table, item), laid out [tables][items].
+ * Written by the training forward, read by the backward.
+ *   bytes 0-3  float    u     the margin with the smallest |margin| (first on ties)
+ *   bytes 4-5  uint16   code  the LUT row index (bit c = [margin_c > 0])
+ *   byte  6    uint8    r     the comparison index of u
+ *   byte  7    uint8    0
+ */
+typedef struct tropnn_route_record {
+    float u;
+    uint16_t code;
+    uint8_t r;
+    uint8_t reserved;
+} tropnn_route_record;
+
+typedef void *tropnn_stream_t; /* hipStream_t */
+
+/* ABI version of the loaded library; callers compare with TROPNN_HIP_ABI_VERSION. */
+int tropnn_hip_abi_version(void);
+
+/* Last error message of the calling thread ("" after a successful call). */
+const char *tropnn_hip_last_error(void);
+
+/*
+ * Eval forward with f32 / f16 weights. Replaces the Zig exports
+ * lut_forward_batch_with_offsets_no_cache and lut_forward_batch_f16_no_cache
+ * (kernels/src/lut.zig:255-285, 288-318): same argument order and meaning
+ * (weights [tables, 2^comparisons, output_dim], anchors [tables, comparisons, 2],
+ * offsets = thresholds [tables, comparisons], inputs [batch, input_dim],
+ * outputs [batch, output_dim], fully overwritten), plus the output scale the
+ * module applies afterwards (layers/base.py:76-77) and the stream.
+ */
+int tropnn_hip_lut_forward_batch_f32(size_t batch, size_t tables, size_t comparisons, size_t input_dim,
+                                     size_t output_dim, const float *weights, const int64_t *anchors,
+                                     const float *offsets, const float *inputs, float *outputs, float output_scale,
+                                     tropnn_stream_t stream);
+int tropnn_hip_lut_forward_batch_f16(size_t batch, size_t tables, size_t comparisons, size_t input_dim,
+                                     size_t output_dim, const uint16_t *weights_f16, const int64_t *anchors,
+                                     const float *offsets, const float *inputs, float *outputs, float output_scale,
+                                     tropnn_stream_t stream);
+
+/*
+ * Forward of the training / debug path. Replaces the TileLang route and
+ * forward kernels with their launcher _run_forward
+ * (backends/pairwise_tilelang.py:17-115, 413-457), fused into one launch:
+ *   output[b,:]       = output_scale * sum_t lut[t, code[b,t], :]      [items, out_features]
+ *   route_record      = per (table, item) record above, or NULL         [tables, items]
+ *   indices[b,t]      = code as int64, or NULL                          [items, tables]
+ *   margins[b,t,c]    = (x[b,a] - x[b,b']) - thr[t,c], or NULL          [items, tables, comparisons]
+ * lut_dtype selects float (TROPNN_LUT_F32) or binary16 (TROPNN_LUT_F16) rows.
+ */
+int tropnn_hip_pairwise_forward(int64_t items, int64_t in_features, int64_t out_features, int64_t tables,
+                                int64_t comparisons, const float *latent, const int64_t *anchors,
+                                const float *thresholds, const void *lut, int lut_dtype, float output_scale,
+                                float *output, tropnn_route_record *route_record, int64_t *indices, float *margins,
+                                tropnn_stream_t stream);
+
+/* Bytes of device workspace tropnn_hip_pairwise_backward needs for these dims. */
+size_t tropnn_hip_pairwise_backward_workspace_size(int64_t items, int64_t in_features, int64_t out_features,
+                                                   int64_t tables, int64_t comparisons, int lut_dtype);
+
+/*
+ * Backward of the training forward with the min-margin STE. Replaces
+ * _PairwiseTileLangFunction.backward and its LUT-scatter and min-STE kernels
+ * (backends/pairwise_tilelang.py:118-288, 481-534); the math is the autograd
+ * of the torch path (layers/pairwise.py:137-166, layers/surrogate.py:16-38):
+ *   g[b,:]            = output_scale * grad_output[b,:]
+ *   grad_lut[t,r,:]   = sum_{b: code[b,t]=r} g[b,:]                      (fully overwritten)
+ *   D[b,t]            = sum_o g[b,o] * (lut[t,nb,o] - lut[t,code,o]),   nb = code ^ (1 << r)
+ *   gu[b,t]           = D[b,t] * surrogate'(u[b,t])
+ *   grad_latent[b,i]  = sum_t gu[b,t] * ([i = a(t,r)] - [i = b'(t,r)])   (fully overwritten)
+ *   grad_thresholds[t,c] = -sum_b [r[b,t] = c] * gu[b,t]                (fully overwritten)
+ * Any of the three gradient pointers may be NULL to skip that gradient.
+ * Only ste_mode = TROPNN_STE_MIN_MARGIN and surrogate =
+ * TROPNN_SURROGATE_FAST_SIGMOID_ODD are implemented; the others return
+ * TROPNN_ERR_UNSUPPORTED. workspace: device memory of at least
+ * tropnn_hip_pairwise_backward_workspace_size() bytes, 256-byte aligned.
+ */
+int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out_features, int64_t tables,
+                                 int64_t comparisons, const float *grad_output, const int64_t *anchors,
+                                 const void *lut, int lut_dtype, const tropnn_route_record *route_record,
+                                 float output_scale, int ste_mode, int surrogate, float *grad_latent,
+                                 float *grad_thresholds, float *grad_lut, void *workspace, size_t workspace_bytes,
+                                 tropnn_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TROPNN_HIP_H */

@@ -1,0 +1,375 @@
+"""GPU parity: the HIP path (through libtropnn_hip.so's C ABI) against the CPU
+oracle on the same seeded inputs and parameters.
+
+Bars:
+  * route codes and margins: bit-exact (torch.equal on int64 codes and on the
+    f32 margin bit patterns);
+  * f32 LUT: forward output and every gradient within 1e-5 relative error,
+    measured norm-wise as max|hip - oracle| / max|oracle|;
+  * f16 LUT reads: within 1e-3 relative of the f32-LUT oracle.
+The reference's own parity tests (test_backend_parity.py:348-369) use
+allclose(atol=1e-6); test_reference_case repeats that case and bar.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import pairwise_torch as orc
+from oracle import routing_np
+from tropnn_amd import PairwiseLinear, pairwise_hip_forward
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+F32_TOL = 1e-5
+F16_TOL = 1e-3
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    yield
+    torch.cuda.synchronize()
+
+
+def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
+    a = a.detach().float().cpu()
+    b = b.detach().float().cpu()
+    assert a.shape == b.shape, (a.shape, b.shape)
+    if b.numel() == 0:
+        return 0.0
+    scale = float(b.abs().max())
+    diff = float((a - b).abs().max())
+    return diff / scale if scale > 0 else diff
+
+
+def make_pair(i, o, t, c, *, seed=0, thr_std=0.0, lut_dtype="f32", gen_seed=1234):
+    ref = orc.OraclePairwiseLinear(i, o, tables=t, comparisons=c, seed=seed)
+    hip = PairwiseLinear(i, o, tables=t, comparisons=c, seed=seed, device_lut_dtype=lut_dtype)
+    with torch.no_grad():
+        if thr_std:
+            g = torch.Generator().manual_seed(gen_seed)
+            ref.thresholds.copy_(thr_std * torch.randn(ref.thresholds.shape, generator=g))
+        hip.anchors.copy_(ref.anchors)
+        hip.thresholds.copy_(ref.thresholds)
+        hip.lut.copy_(ref.lut)
+    return ref, hip.to(DEV)
+
+
+def seeded(shape, seed):
+    return torch.randn(*shape, generator=torch.Generator().manual_seed(seed))
+
+
+def train_step(ref, hip, x, g, *, x_grad=True):
+    ref.train()
+    hip.train()
+    x_ref = x.clone().requires_grad_(x_grad)
+    x_hip = x.to(DEV).requires_grad_(x_grad)
+    y_ref = ref(x_ref)
+    y_hip = hip(x_hip)
+    y_ref.backward(g)
+    y_hip.backward(g.to(DEV))
+    torch.cuda.synchronize()
+    return (y_ref, x_ref), (y_hip, x_hip)
+
+
+def assert_train_parity(ref, hip, yx_ref, yx_hip, tol=F32_TOL, x_grad=True):
+    (y_ref, x_ref), (y_hip, x_hip) = yx_ref, yx_hip
+    assert torch.equal(hip._last_indices.cpu(), ref._last_indices), "route codes differ"
+    errs = {
+        "output": rel_err(y_hip, y_ref),
+        "grad_thresholds": rel_err(hip.thresholds.grad, ref.thresholds.grad),
+        "grad_lut": rel_err(hip.lut.grad, ref.lut.grad),
+    }
+    if x_grad:
+        errs["grad_x"] = rel_err(x_hip.grad, x_ref.grad)
+    else:
+        assert x_hip.grad is None and x_ref.grad is None
+    bad = {k: v for k, v in errs.items() if not v <= tol}
+    assert not bad, f"beyond {tol}: {bad} (all: {errs})"
+    return errs
+
+
+# ---------------------------------------------------------------- route codes
+@pytest.mark.parametrize(
+    "i,t,c,b",
+    [(8, 3, 3, 4), (16, 1, 1, 7), (33, 5, 2, 9), (128, 136, 6, 512), (64, 17, 8, 40), (300, 70, 7, 33), (1024, 64, 5, 3)],
+)
+def test_codes_and_margins_bit_exact(i, t, c, b):
+    ref, hip = make_pair(i, 4, t, c, seed=t + c, thr_std=0.5)
+    x = seeded((b, i), seed=i + b)
+    with torch.no_grad():
+        hip.eval()(x.to(DEV))
+    torch.cuda.synchronize()
+    codes = routing_np.route_codes(x.numpy(), ref.anchors.numpy(), ref.thresholds.detach().numpy())
+    margins = routing_np.margins_f32(x.numpy(), ref.anchors.numpy(), ref.thresholds.detach().numpy())
+    got_codes = hip._last_indices.cpu().reshape(b, t).numpy()
+    got_margins = hip._last_margins.cpu().reshape(b, t, c).numpy()
+    np.testing.assert_array_equal(got_codes, codes)
+    np.testing.assert_array_equal(got_margins.view(np.uint32), margins.view(np.uint32))
+
+
+def test_codes_edge_values():
+    """Subnormal, signed-zero, NaN and infinite margins: bit c is set iff the
+    f32 margin is > 0, with no denormal flushing."""
+    tiny = np.float32(1.4e-45)  # smallest positive subnormal
+    x = np.array(
+        [
+            [tiny, 0.0, -tiny, np.nan, np.inf, -np.inf, 1.0, 1.0],
+            [0.0, tiny, 0.0, -0.0, 2.0, np.nan, np.inf, np.inf],
+        ],
+        dtype=np.float32,
+    )
+    anchors = torch.tensor(
+        [[[0, 1], [1, 0], [2, 1], [3, 0]], [[4, 5], [5, 4], [6, 7], [7, 6]], [[4, 6], [6, 4], [3, 3], [0, 2]]],
+        dtype=torch.long,
+    )
+    thr = torch.zeros(3, 4)
+    ref, hip = make_pair(8, 3, 3, 4, seed=0)
+    with torch.no_grad():
+        hip.anchors.copy_(anchors.to(DEV))
+        hip.thresholds.copy_(thr.to(DEV))
+        hip.eval()(torch.from_numpy(x).to(DEV))
+    torch.cuda.synchronize()
+    expect = routing_np.route_codes(x, anchors.numpy(), thr.numpy())
+    np.testing.assert_array_equal(hip._last_indices.cpu().reshape(2, 3).numpy(), expect)
+    # the subnormal margin sets bit 0 of table 0 for item 0
+    assert expect[0, 0] & 1 == 1
+
+
+# ---------------------------------------------------------------- eval forward
+@pytest.mark.parametrize(
+    "i,o,t,c,b",
+    [(256, 512, 16, 6, 8), (128, 128, 136, 6, 512), (128, 128, 136, 6, 1), (8, 5, 3, 3, 4), (784, 128, 136, 6, 64), (128, 10, 136, 6, 33), (32, 3, 9, 8, 17)],
+)
+def test_eval_forward_f32(i, o, t, c, b):
+    ref, hip = make_pair(i, o, t, c, seed=0, thr_std=0.1)
+    x = seeded((b, i), seed=0)
+    with torch.no_grad():
+        y_ref = ref.eval()(x)
+        y_hip = hip.eval()(x.to(DEV))
+    assert torch.equal(hip._last_indices.cpu(), ref._last_indices)
+    assert rel_err(y_hip, y_ref) <= F32_TOL
+
+
+@pytest.mark.parametrize("b", [1, 64, 8192])
+def test_eval_forward_f16_lut(b):
+    """c3: same layer, LUT read as an RNE f16 copy, against the f32 oracle."""
+    ref, hip = make_pair(128, 128, 136, 6, seed=0, lut_dtype="f16")
+    x = seeded((b, 128), seed=0)
+    with torch.no_grad():
+        y_ref = ref.eval()(x)
+        y_hip = hip.eval()(x.to(DEV))
+        y_fn = pairwise_hip_forward(
+            x.to(DEV).unsqueeze(1), hip.anchors, hip.thresholds, hip.lut, lut_dtype="f16", output_scale=hip.output_scale
+        )
+    assert rel_err(y_hip, y_ref) <= F16_TOL
+    assert rel_err(y_fn, y_ref) <= F16_TOL
+
+
+def test_pairwise_hip_forward_matches_zig_restatement():
+    """The Zig-ABI-shaped entry points against the C restatement of the Zig
+    forward (f32: atol 1e-6, f16: 5e-3 as test_backend_parity.py:232, 246)."""
+    from oracle import lut_cpu
+
+    lut_cpu.build()
+    ref, hip = make_pair(8, 5, 4, 3, seed=2, thr_std=0.2)
+    x = seeded((7, 1, 8), seed=5)
+    for dt, atol in (("f32", 1e-6), ("f16", 5e-3)):
+        want = lut_cpu.forward(x, ref.anchors, ref.thresholds.detach(), ref.lut.detach(), lut_dtype=dt, threads=1)
+        got = pairwise_hip_forward(x.to(DEV), hip.anchors, hip.thresholds, hip.lut, lut_dtype=dt)
+        assert torch.allclose(got.cpu(), want, atol=atol), dt
+
+
+# ---------------------------------------------------------------- train fwd + bwd
+def test_reference_case_square_mean():
+    """test_backend_parity.py:348-369 (min-margin STE): PairwiseLinear(8, 5,
+    tables=3, comparisons=3, seed=1), x = randn(4, 8), loss = square().mean()."""
+    torch.manual_seed(0)
+    ref, hip = make_pair(8, 5, 3, 3, seed=1)
+    x = torch.randn(4, 8)
+    x_ref = x.clone().requires_grad_(True)
+    x_hip = x.to(DEV).requires_grad_(True)
+    ref.train()(x_ref).square().mean().backward()
+    hip.train()(x_hip).square().mean().backward()
+    with torch.no_grad():
+        assert torch.allclose(ref(x), hip(x.to(DEV)).cpu(), atol=1e-6)
+    assert torch.allclose(x_ref.grad, x_hip.grad.cpu(), atol=1e-6)
+    assert torch.allclose(ref.thresholds.grad, hip.thresholds.grad.cpu(), atol=1e-6)
+    assert torch.allclose(ref.lut.grad, hip.lut.grad.cpu(), atol=1e-6)
+
+
+def test_c2_north_star_config():
+    """c2: PairwiseLinear(128->128, T=136, C=6), B=512, x seed 0, G seed 1."""
+    ref, hip = make_pair(128, 128, 136, 6, seed=0)
+    x = seeded((512, 128), seed=0)
+    g = seeded((512, 1, 128), seed=1)
+    errs = assert_train_parity(ref, hip, *train_step(ref, hip, x, g))
+    print("c2 errors", errs)
+
+
+@pytest.mark.parametrize(
+    "i,o,t,c,b,thr_std",
+    [
+        (8, 5, 3, 3, 4, 0.0),
+        (128, 128, 136, 6, 1, 0.2),
+        (784, 128, 136, 6, 64, 0.0),
+        (128, 10, 136, 6, 37, 0.3),
+        (64, 64, 20, 8, 50, 0.3),
+        (16, 7, 5, 1, 19, 0.1),
+        (40, 3, 33, 4, 70, 0.5),
+        (256, 512, 16, 6, 8, 0.0),
+        (100, 96, 7, 2, 300, 0.2),
+    ],
+)
+def test_train_parity(i, o, t, c, b, thr_std):
+    ref, hip = make_pair(i, o, t, c, seed=i + t, thr_std=thr_std)
+    x = seeded((b, i), seed=b)
+    g = seeded((b, 1, o), seed=b + 1)
+    assert_train_parity(ref, hip, *train_step(ref, hip, x, g))
+
+
+def test_train_without_input_grad():
+    """The reference harness trains with an x that needs no grad
+    (tools/benchmarking/benchmark.py:105-118): thresholds and LUT grads only."""
+    ref, hip = make_pair(128, 128, 136, 6, seed=0, thr_std=0.1)
+    x = seeded((96, 128), seed=3)
+    g = seeded((96, 1, 128), seed=4)
+    assert_train_parity(ref, hip, *train_step(ref, hip, x, g, x_grad=False), x_grad=False)
+
+
+def test_sequence_input_3d():
+    """[B,S,I] input flattens to B*S items (pairwise_tilelang.py:438-441)."""
+    ref, hip = make_pair(24, 12, 10, 5, seed=4, thr_std=0.2)
+    x = seeded((6, 5, 24), seed=9)
+    g = seeded((6, 5, 12), seed=10)
+    assert_train_parity(ref, hip, *train_step(ref, hip, x, g))
+
+
+def test_eval_mode_has_no_ste_gradient():
+    """Eval mode: no STE, so x and thresholds get no gradient while the LUT
+    still does (layers/pairwise.py:245-247)."""
+    ref, hip = make_pair(32, 16, 12, 6, seed=1, thr_std=0.2)
+    x = seeded((20, 32), seed=2)
+    g = seeded((20, 1, 16), seed=3)
+    x_ref = x.clone().requires_grad_(True)
+    x_hip = x.to(DEV).requires_grad_(True)
+    ref.eval()(x_ref).backward(g)
+    hip.eval()(x_hip).backward(g.to(DEV))
+    assert x_ref.grad is None and x_hip.grad is None
+    assert ref.thresholds.grad is None and hip.thresholds.grad is None
+    assert rel_err(hip.lut.grad, ref.lut.grad) <= F32_TOL
+
+
+def test_ties_zero_margins_and_duplicate_anchors():
+    """Sparse inputs (many exact zeros) give |m| ties, resolved to the first
+    comparison, and u = 0, whose surrogate gradient is 0; an anchor pair with
+    a == b gives zero net input gradient."""
+    ref, hip = make_pair(20, 8, 6, 4, seed=7)
+    with torch.no_grad():
+        ref.anchors[0, 1] = torch.tensor([3, 3])
+        hip.anchors.copy_(ref.anchors)
+    gen = torch.Generator().manual_seed(0)
+    x = torch.rand(30, 20, generator=gen) * (torch.rand(30, 20, generator=gen) >= 0.8)
+    g = seeded((30, 1, 8), seed=2)
+    assert_train_parity(ref, hip, *train_step(ref, hip, x, g))
+
+
+def test_f16_lut_training():
+    """f16 LUT reads in training: forward and gradients within 1e-3 of the f32 oracle."""
+    ref, hip = make_pair(128, 128, 136, 6, seed=0, lut_dtype="f16", thr_std=0.1)
+    x = seeded((256, 128), seed=0)
+    g = seeded((256, 1, 128), seed=1)
+    assert_train_parity(ref, hip, *train_step(ref, hip, x, g), tol=F16_TOL)
+
+
+def test_f16_cache_follows_lut_updates():
+    _, hip = make_pair(16, 8, 4, 3, seed=0, lut_dtype="f16")
+    first = hip._lut_for_reading()
+    assert first.dtype == torch.float16
+    with torch.no_grad():
+        hip.lut.add_(1.0)
+    second = hip._lut_for_reading()
+    assert second is not first
+    assert torch.equal(second, hip.lut.detach().half())
+
+
+def test_empty_batch():
+    ref, hip = make_pair(16, 8, 4, 3, seed=0)
+    x = torch.zeros(0, 16, device=DEV, requires_grad=True)
+    y = hip.train()(x)
+    assert y.shape == (0, 1, 8)
+    y.sum().backward()
+    assert torch.count_nonzero(hip.lut.grad) == 0
+
+
+def test_route_debug_cache_off():
+    _, hip = make_pair(16, 8, 4, 3, seed=0)
+    hip.cache_route_debug = False
+    with torch.no_grad():
+        hip(seeded((5, 16), 0).to(DEV))
+    assert hip._last_indices is None and hip._last_margins is None
+
+
+def test_single_hip_runtime_in_process():
+    """libtropnn_hip.so must bind the HIP runtime torch already loaded."""
+    from tropnn_amd.backends.pairwise_hip import load_library
+
+    load_library()
+    maps = open("/proc/self/maps").read().splitlines()
+    paths = {line.split()[-1] for line in maps if "libamdhip64" in line}
+    assert len(paths) == 1, paths
+
+
+# ---------------------------------------------------------------- c4 (full size)
+def test_c4_large_layer_properties():
+    """c4: PairwiseLinear(1024->4096, T=512, C=8), f16 LUT reads, B=8192.
+
+    The full-size oracle is out of reach on the CPU, so parity is checked on
+    properties that do not depend on size:
+      * forward and input gradient of a row depend on that row only: a random
+        subset of rows is compared with the oracle run on those rows alone;
+      * every item adds its scaled grad row to exactly one row per table, so
+        sum_r grad_lut[t, r, :] = s * sum_b G[b, :] for every table t;
+      * gradients are linear in G: grad(G1 + G2) = grad(G1) + grad(G2).
+    """
+    i, o, t, c, b = 1024, 4096, 512, 8, 8192
+    ref = orc.OraclePairwiseLinear(i, o, tables=t, comparisons=c, seed=0)
+    hip = PairwiseLinear(i, o, tables=t, comparisons=c, seed=0, device_lut_dtype="f16").to(DEV)
+    assert torch.equal(hip.anchors.cpu(), ref.anchors)
+    x = seeded((b, i), seed=0).to(DEV)
+    gfull = seeded((b, 1, o), seed=1).to(DEV)
+    sub = torch.randperm(b, generator=torch.Generator().manual_seed(0))[:16]
+
+    def run(g):
+        hip.zero_grad(set_to_none=True)
+        xg = x.clone().requires_grad_(True)
+        y = hip.train()(xg)
+        y.backward(g)
+        return y.detach(), xg.grad.detach(), hip.thresholds.grad.detach().clone(), hip.lut.grad.detach().clone()
+
+    y, gx, gthr, glut = run(gfull)
+    codes = hip._last_indices.view(b, t)
+    want_codes = routing_np.route_codes(x[sub].cpu().numpy(), ref.anchors.numpy(), ref.thresholds.detach().numpy())
+    np.testing.assert_array_equal(codes[sub.to(DEV)].cpu().numpy(), want_codes)
+
+    x_sub = x[sub].cpu().requires_grad_(True)
+    y_sub = ref.train()(x_sub)
+    y_sub.backward(gfull[sub.to(DEV)].cpu())
+    assert rel_err(y[sub.to(DEV)], y_sub) <= F16_TOL
+    assert rel_err(gx[sub.to(DEV)], x_sub.grad) <= F16_TOL
+
+    s = hip.output_scale
+    row_sums = glut.sum(dim=1)  # [T, O]
+    want = (gfull.view(b, o).double().sum(0) * s).float()
+    assert rel_err(row_sums, want.expand(t, o)) <= 1e-4
+
+    mask = torch.zeros(b, 1, 1, device=DEV)
+    mask[: b // 2] = 1.0
+    _, gx1, gthr1, glut1 = run(gfull * mask)
+    _, gx2, gthr2, glut2 = run(gfull * (1 - mask))
+    assert rel_err(gx1 + gx2, gx) <= 1e-5
+    assert rel_err(gthr1 + gthr2, gthr) <= 1e-4
+    assert rel_err(glut1 + glut2, glut) <= 1e-5

@@ -1,0 +1,401 @@
+"""HIP backend of PairwiseLinear: ctypes binding of libtropnn_hip.so plus the
+autograd Function around it.
+
+Public entry points mirror the reference's backend wrappers:
+  * pairwise_hip(...)          -- like pairwise_tilelang (backends/pairwise_tilelang.py:537-549):
+                                  autograd Function, returns (output, indices, margins)
+  * pairwise_hip_forward(...)  -- like pairwise_zig_forward (backends/pairwise_zig.py:35-103):
+                                  eval-only forward with an f32 or f16 LUT
+  * has_pairwise_hip()         -- capability probe like has_pairwise_zig / has_tilelang
+                                  (backend.py:15-42)
+
+Errors follow the reference wrappers: RuntimeError when the native library or
+a GPU is missing (pairwise_tilelang.py:421-422, zig_runtime.py:81-87),
+ValueError for a non-GPU tensor or a bad shape, TypeError for a wrong dtype
+(pairwise_tilelang.py:423-436, pairwise_zig.py:43-61). There is no CPU
+fallback: every call runs the HIP kernels or raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+from typing import Any
+
+import torch
+from torch import Tensor
+
+ABI_VERSION = 1
+LUT_F32, LUT_F16 = 0, 1
+SURROGATE_IDS = {"fast_sigmoid_odd": 0, "izhikevich": 1}
+STE_MIN_MARGIN, STE_FULL = 0, 1
+MAX_COMPARISONS = 8
+ERR_NAMES = {1: "invalid argument", 2: "unsupported", 3: "HIP error"}
+
+_PKG_DIR = Path(__file__).resolve().parent.parent
+DEFAULT_LIBRARY = _PKG_DIR / "libtropnn_hip.so"
+_LOCK = threading.Lock()
+_LIB: ctypes.CDLL | None = None
+_ANCHORS_CHECKED: dict[tuple, bool] = {}
+
+EXPORTED_SYMBOLS = (
+    "tropnn_hip_abi_version",
+    "tropnn_hip_last_error",
+    "tropnn_hip_lut_forward_batch_f32",
+    "tropnn_hip_lut_forward_batch_f16",
+    "tropnn_hip_pairwise_forward",
+    "tropnn_hip_pairwise_backward_workspace_size",
+    "tropnn_hip_pairwise_backward",
+)
+
+
+def library_path() -> Path:
+    """TROPNN_HIP_LIB overrides the in-tree build location."""
+    env = os.environ.get("TROPNN_HIP_LIB")
+    return Path(env) if env else DEFAULT_LIBRARY
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    i64, sz, p, f, i = ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
+    lib.tropnn_hip_abi_version.argtypes = []
+    lib.tropnn_hip_abi_version.restype = i
+    lib.tropnn_hip_last_error.argtypes = []
+    lib.tropnn_hip_last_error.restype = ctypes.c_char_p
+    for name in ("tropnn_hip_lut_forward_batch_f32", "tropnn_hip_lut_forward_batch_f16"):
+        fn = getattr(lib, name)
+        fn.argtypes = [sz, sz, sz, sz, sz, p, p, p, p, p, f, p]
+        fn.restype = i
+    lib.tropnn_hip_pairwise_forward.argtypes = [i64, i64, i64, i64, i64, p, p, p, p, i, f, p, p, p, p, p]
+    lib.tropnn_hip_pairwise_forward.restype = i
+    lib.tropnn_hip_pairwise_backward_workspace_size.argtypes = [i64, i64, i64, i64, i64, i]
+    lib.tropnn_hip_pairwise_backward_workspace_size.restype = sz
+    lib.tropnn_hip_pairwise_backward.argtypes = [i64, i64, i64, i64, i64, p, p, p, i, p, f, i, i, p, p, p, p, sz, p]
+    lib.tropnn_hip_pairwise_backward.restype = i
+
+
+def load_library() -> ctypes.CDLL:
+    """Load libtropnn_hip.so once (under a lock), after torch's HIP runtime,
+    so both share one libamdhip64 instance. Raises RuntimeError if the file is
+    missing or its ABI version differs."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    with _LOCK:
+        if _LIB is not None:
+            return _LIB
+        path = library_path()
+        if not path.exists():
+            raise RuntimeError(
+                f"PairwiseLinear backend='hip' needs {path}, which is not built; "
+                "build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                "or `make -C tropnn_amd/csrc`"
+            )
+        try:
+            lib = ctypes.CDLL(str(path))
+        except OSError as exc:
+            raise RuntimeError(f"cannot load {path}: {exc}") from exc
+        missing = [s for s in EXPORTED_SYMBOLS if not hasattr(lib, s)]
+        if missing:
+            raise RuntimeError(f"{path} lacks symbols {missing}")
+        _declare(lib)
+        version = lib.tropnn_hip_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"{path} has ABI version {version}, this package expects {ABI_VERSION}")
+        _LIB = lib
+    return _LIB
+
+
+def has_pairwise_hip() -> bool:
+    """True when the native library loads and a GPU is visible."""
+    if not torch.cuda.is_available():
+        return False
+    try:
+        load_library()
+    except RuntimeError:
+        return False
+    return True
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == 0:
+        return
+    msg = load_library().tropnn_hip_last_error().decode(errors="replace")
+    if rc == 2:
+        raise NotImplementedError(f"{what}: {msg}")
+    if rc == 1:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {ERR_NAMES.get(rc, rc)}: {msg}")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require_gpu(*tensors: Tensor) -> None:
+    if not torch.cuda.is_available():
+        raise RuntimeError("PairwiseLinear backend='hip' requires a visible AMD GPU (torch.cuda.is_available() is False)")
+    for t in tensors:
+        if not t.is_cuda:
+            raise ValueError("PairwiseLinear backend='hip' requires GPU tensors")
+
+
+def check_anchors(anchors: Tensor, in_features: int) -> None:
+    """Every anchor must index the input row. Checked once per
+    (storage, version, in_features) because it reads the tensor back."""
+    key = (anchors.data_ptr(), anchors._version, tuple(anchors.shape), in_features, anchors.device)
+    if _ANCHORS_CHECKED.get(key):
+        return
+    if anchors.numel() > 0:
+        lo, hi = int(anchors.min().item()), int(anchors.max().item())
+        if lo < 0 or hi >= in_features:
+            raise ValueError(f"anchors must lie in [0, {in_features}), got range [{lo}, {hi}]")
+    if len(_ANCHORS_CHECKED) > 256:
+        _ANCHORS_CHECKED.clear()
+    _ANCHORS_CHECKED[key] = True
+
+
+def _validate(latent: Tensor, anchors: Tensor, thresholds: Tensor, lut: Tensor) -> tuple[int, int, int, int, int, int]:
+    if latent.ndim != 3:
+        raise ValueError(f"latent must have shape [batch, steps, in_features], got {tuple(latent.shape)}")
+    if latent.dtype != torch.float32 or thresholds.dtype != torch.float32:
+        raise TypeError(f"Pairwise HIP backend expects float32 latent and thresholds, got {latent.dtype}, {thresholds.dtype}")
+    if anchors.dtype != torch.int64:
+        raise TypeError(f"anchors must be int64, got {anchors.dtype}")
+    if lut.dtype not in (torch.float32, torch.float16):
+        raise TypeError(f"lut must be float32 or float16, got {lut.dtype}")
+    batch, steps, in_features = latent.shape
+    if anchors.ndim != 3 or anchors.shape[2] != 2:
+        raise ValueError(f"anchors must have shape [tables, comparisons, 2], got {tuple(anchors.shape)}")
+    tables, comps, _ = anchors.shape
+    if thresholds.shape != (tables, comps):
+        raise ValueError(f"thresholds must have shape {(tables, comps)}, got {tuple(thresholds.shape)}")
+    if lut.ndim != 3 or lut.shape[0] != tables or lut.shape[1] != (1 << comps):
+        raise ValueError(f"lut must have shape [{tables}, {1 << comps}, out_features], got {tuple(lut.shape)}")
+    if comps > MAX_COMPARISONS:
+        raise NotImplementedError(f"Pairwise HIP backend supports comparisons <= {MAX_COMPARISONS}, got {comps}")
+    devs = {t.device for t in (latent, anchors, thresholds, lut)}
+    if len(devs) != 1:
+        raise ValueError(f"all tensors must be on one device, got {sorted(map(str, devs))}")
+    return batch, steps, in_features, tables, comps, lut.shape[2]
+
+
+def _route_forward(
+    latent: Tensor,
+    anchors: Tensor,
+    thresholds: Tensor,
+    lut_read: Tensor,
+    *,
+    output_scale: float,
+    want_record: bool,
+    return_route: bool,
+) -> tuple[Tensor, Tensor | None, Tensor, Tensor]:
+    """One fused forward launch. Returns (output, record, indices, margins)."""
+    batch, steps, in_features, tables, comps, out_features = _validate(latent, anchors, thresholds, lut_read)
+    check_anchors(anchors, in_features)
+    items = batch * steps
+    dev = latent.device
+    x = latent.reshape(items, in_features).contiguous()
+    anc, thr, lut_c = anchors.contiguous(), thresholds.contiguous(), lut_read.contiguous()
+    out = torch.empty((items, out_features), device=dev, dtype=torch.float32)
+    record = torch.empty((tables, items), device=dev, dtype=torch.int64) if want_record else None
+    if return_route:
+        indices = torch.empty((items, tables), device=dev, dtype=torch.int64)
+        margins = torch.empty((items, tables, comps), device=dev, dtype=torch.float32)
+    else:
+        indices = torch.empty((items, 0), device=dev, dtype=torch.int64)
+        margins = torch.empty((items, 0), device=dev, dtype=torch.float32)
+    lib = load_library()
+    rc = lib.tropnn_hip_pairwise_forward(
+        items,
+        in_features,
+        out_features,
+        tables,
+        comps,
+        _ptr(x),
+        _ptr(anc),
+        _ptr(thr),
+        _ptr(lut_c),
+        LUT_F16 if lut_c.dtype == torch.float16 else LUT_F32,
+        float(output_scale),
+        _ptr(out),
+        _ptr(record),
+        _ptr(indices) if return_route else None,
+        _ptr(margins) if return_route else None,
+        _stream(dev),
+    )
+    _check(rc, "tropnn_hip_pairwise_forward")
+    if return_route:
+        idx_view = indices.view(batch, steps, tables)
+        mar_view = margins.view(batch, steps, tables, comps)
+    else:
+        idx_view = indices.view(batch, steps, 0)
+        mar_view = margins.view(batch, steps, 0)
+    return out.view(batch, steps, out_features), record, idx_view, mar_view
+
+
+class _PairwiseHipFunction(torch.autograd.Function):
+    """Forward: fused route + gather + scale. Backward: table-major LUT
+    gradient + min-margin STE, then input / threshold gradients. Contract of
+    _PairwiseTileLangFunction (backends/pairwise_tilelang.py:460-534): the
+    gradient tuple is (latent, None, thresholds, lut, None, ...), indices and
+    margins are non-differentiable."""
+
+    @staticmethod
+    def forward(  # type: ignore[override]
+        ctx: Any,
+        latent: Tensor,
+        anchors: Tensor,
+        thresholds: Tensor,
+        lut: Tensor,
+        lut_read: Tensor,
+        ste: bool,
+        surrogate: str,
+        output_scale: float,
+        return_route: bool,
+    ) -> tuple[Tensor, Tensor, Tensor]:
+        needs_lut = ctx.needs_input_grad[3]
+        needs_route = ste and (ctx.needs_input_grad[0] or ctx.needs_input_grad[2])
+        want_record = needs_lut or needs_route
+        out, record, indices, margins = _route_forward(
+            latent,
+            anchors,
+            thresholds,
+            lut_read,
+            output_scale=output_scale,
+            want_record=want_record,
+            return_route=return_route,
+        )
+        ctx.save_for_backward(record, anchors, lut_read)
+        ctx.dims = tuple(latent.shape) + (lut_read.shape[2],)
+        ctx.ste = ste
+        ctx.surrogate = surrogate
+        ctx.output_scale = float(output_scale)
+        ctx.mark_non_differentiable(indices, margins)
+        return out, indices, margins
+
+    @staticmethod
+    def backward(ctx: Any, grad_output: Tensor, grad_indices: Tensor | None, grad_margins: Tensor | None):  # type: ignore[override]
+        del grad_indices, grad_margins
+        record, anchors, lut_read = ctx.saved_tensors
+        batch, steps, in_features, out_features = ctx.dims
+        tables, comps, _ = anchors.shape
+        items = batch * steps
+        dev = grad_output.device
+        want_x = ctx.ste and ctx.needs_input_grad[0]
+        want_thr = ctx.ste and ctx.needs_input_grad[2]
+        want_lut = ctx.needs_input_grad[3]
+        if not (want_x or want_thr or want_lut):
+            return (None,) * 9
+        g = grad_output.reshape(items, out_features).to(torch.float32).contiguous()
+        grad_x = torch.empty((items, in_features), device=dev, dtype=torch.float32) if want_x else None
+        grad_thr = torch.empty((tables, comps), device=dev, dtype=torch.float32) if want_thr else None
+        grad_lut = torch.empty((tables, 1 << comps, out_features), device=dev, dtype=torch.float32) if want_lut else None
+        lib = load_library()
+        lut_dtype = LUT_F16 if lut_read.dtype == torch.float16 else LUT_F32
+        ws_bytes = lib.tropnn_hip_pairwise_backward_workspace_size(items, in_features, out_features, tables, comps, lut_dtype)
+        workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8) if (want_x or want_thr) else None
+        rc = lib.tropnn_hip_pairwise_backward(
+            items,
+            in_features,
+            out_features,
+            tables,
+            comps,
+            _ptr(g),
+            _ptr(anchors),
+            _ptr(lut_read),
+            lut_dtype,
+            _ptr(record),
+            ctx.output_scale,
+            STE_MIN_MARGIN,
+            SURROGATE_IDS[ctx.surrogate],
+            _ptr(grad_x),
+            _ptr(grad_thr),
+            _ptr(grad_lut),
+            _ptr(workspace),
+            ws_bytes,
+            _stream(dev),
+        )
+        _check(rc, "tropnn_hip_pairwise_backward")
+        gx = grad_x.view(batch, steps, in_features) if grad_x is not None else None
+        return gx, None, grad_thr, grad_lut, None, None, None, None, None
+
+
+def pairwise_hip(
+    latent: Tensor,
+    anchors: Tensor,
+    thresholds: Tensor,
+    lut: Tensor,
+    *,
+    use_min_margin_ste: bool = True,
+    surrogate: str = "fast_sigmoid_odd",
+    output_scale: float = 1.0,
+    lut_read: Tensor | None = None,
+    ste: bool = True,
+    return_route: bool = True,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """HIP counterpart of pairwise_tilelang (backends/pairwise_tilelang.py:537-549).
+
+    latent [B,S,I] f32, anchors [T,C,2] int64, thresholds [T,C] f32,
+    lut [T,2^C,O] f32 (the parameter gradients flow to). Returns
+    (output [B,S,O] = output_scale * sum_t lut[t, code], indices [B,S,T] int64,
+    margins [B,S,T,C] f32); with return_route=False the last two are empty
+    [B,S,0] tensors, as the Zig path returns (layers/pairwise.py:223-225).
+
+    lut_read: the tensor the kernels read, e.g. an f16 copy of lut (f32 by
+    default = lut itself). ste: carry the min-margin STE gradient to latent and
+    thresholds (the torch path does so only in training,
+    layers/pairwise.py:245-247). output_scale defaults to 1.0, the
+    pairwise_tilelang contract (the module scales afterwards); the package's
+    PairwiseLinear passes its 1/sqrt(T) here so the scale is fused.
+    """
+    if surrogate not in SURROGATE_IDS:
+        raise ValueError(f"Pairwise HIP backend does not support surrogate={surrogate!r}")
+    _require_gpu(latent, anchors, thresholds, lut)
+    if ste and torch.is_grad_enabled() and (latent.requires_grad or thresholds.requires_grad):
+        if not use_min_margin_ste:
+            raise NotImplementedError("Pairwise HIP backend: the full STE (use_min_margin_ste=False) is not implemented yet")
+        if surrogate != "fast_sigmoid_odd":
+            raise NotImplementedError(f"Pairwise HIP backend: the {surrogate!r} surrogate backward is not implemented yet")
+    if lut_read is None:
+        lut_read = lut
+    return _PairwiseHipFunction.apply(
+        latent, anchors, thresholds, lut, lut_read.detach(), bool(ste), surrogate, float(output_scale), bool(return_route)
+    )
+
+
+def pairwise_hip_forward(
+    latent: Tensor,
+    anchors: Tensor,
+    thresholds: Tensor,
+    lut: Tensor,
+    *,
+    lut_dtype: str = "f32",
+    output_scale: float = 1.0,
+) -> Tensor:
+    """Eval-only forward, the HIP counterpart of pairwise_zig_forward
+    (backends/pairwise_zig.py:35-103): no autograd, no route outputs, the LUT
+    read as f32 or as an RNE f16 copy. Calls the Zig-ABI-shaped entry points
+    tropnn_hip_lut_forward_batch_f32 / _f16."""
+    if lut_dtype not in ("f32", "f16"):
+        raise ValueError(f"lut_dtype must be 'f32' or 'f16', got {lut_dtype!r}")
+    _require_gpu(latent, anchors, thresholds, lut)
+    weights = lut.detach().to(torch.float16 if lut_dtype == "f16" else torch.float32)
+    batch, steps, in_features, tables, comps, out_features = _validate(latent, anchors, thresholds.detach(), weights)
+    check_anchors(anchors, in_features)
+    items = batch * steps
+    x = latent.detach().reshape(items, in_features).contiguous()
+    out = torch.empty((items, out_features), device=latent.device, dtype=torch.float32)
+    lib = load_library()
+    fn = lib.tropnn_hip_lut_forward_batch_f16 if lut_dtype == "f16" else lib.tropnn_hip_lut_forward_batch_f32
+    w = weights.contiguous()
+    thr = thresholds.detach().contiguous()
+    anc = anchors.contiguous()
+    rc = fn(items, tables, comps, in_features, out_features, _ptr(w), _ptr(anc), _ptr(thr), _ptr(x), _ptr(out),
+            float(output_scale), _stream(latent.device))
+    _check(rc, fn.__name__)
+    return out.view(batch, steps, out_features)

@@ -1,0 +1,189 @@
+// C ABI of libtropnn_hip.so (declared in include/tropnn_hip.h): argument
+// validation, the per-thread error channel, launch planning and dispatch.
+// Nothing here allocates memory or synchronises the device.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <limits>
+#include <string>
+
+#include "launch.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return TROPNN_OK;
+}
+
+int hip_fail(const char *where, hipError_t e) {
+    return fail(TROPNN_ERR_HIP, "%s: %s (%s)", where, hipGetErrorName(e), hipGetErrorString(e));
+}
+
+bool fits_int(int64_t v) { return v >= 0 && v <= std::numeric_limits<int>::max(); }
+
+// Shape checks shared by every entry point. Returns TROPNN_OK or an error code
+// (message set) and fills `d`.
+int make_dims(int64_t items, int64_t in_f, int64_t out_f, int64_t tables, int64_t comps, int lut_dtype,
+              tropnn::Dims &d) {
+    if (items < 0) return fail(TROPNN_ERR_INVALID_ARGUMENT, "items must be >= 0, got %lld", (long long)items);
+    if (in_f < 1) return fail(TROPNN_ERR_INVALID_ARGUMENT, "in_features must be >= 1, got %lld", (long long)in_f);
+    if (out_f < 1) return fail(TROPNN_ERR_INVALID_ARGUMENT, "out_features must be >= 1, got %lld", (long long)out_f);
+    if (tables < 1) return fail(TROPNN_ERR_INVALID_ARGUMENT, "tables must be >= 1, got %lld", (long long)tables);
+    if (comps < 1) return fail(TROPNN_ERR_INVALID_ARGUMENT, "comparisons must be >= 1, got %lld", (long long)comps);
+    if (comps > TROPNN_MAX_COMPARISONS)
+        return fail(TROPNN_ERR_UNSUPPORTED, "comparisons=%lld exceeds the supported maximum %d", (long long)comps,
+                    TROPNN_MAX_COMPARISONS);
+    if (lut_dtype != TROPNN_LUT_F32 && lut_dtype != TROPNN_LUT_F16)
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "lut_dtype must be TROPNN_LUT_F32 or TROPNN_LUT_F16, got %d",
+                    lut_dtype);
+    if (!fits_int(items) || !fits_int(in_f) || !fits_int(out_f) || !fits_int(tables))
+        return fail(TROPNN_ERR_UNSUPPORTED, "a dimension exceeds INT_MAX");
+    const int64_t rows = int64_t{1} << comps;
+    if (items * tables > std::numeric_limits<int>::max() || tables * rows > std::numeric_limits<int>::max())
+        return fail(TROPNN_ERR_UNSUPPORTED, "items*tables or tables*2^comparisons exceeds INT_MAX");
+    if (in_f > 8192) return fail(TROPNN_ERR_UNSUPPORTED, "in_features=%lld exceeds 8192", (long long)in_f);
+    d.items = static_cast<int>(items);
+    d.in_f = static_cast<int>(in_f);
+    d.out_f = static_cast<int>(out_f);
+    d.tables = static_cast<int>(tables);
+    d.comps = static_cast<int>(comps);
+    d.rows = static_cast<int>(rows);
+    d.lut_dtype = lut_dtype;
+    return TROPNN_OK;
+}
+
+bool misaligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) != 0; }
+
+int check_forward_ptrs(const tropnn::Dims &d, const tropnn::ForwardPlan &p, const float *x, const int64_t *anchors,
+                       const float *thr, const void *lut, const float *out) {
+    if (d.items == 0) return TROPNN_OK;
+    if (!x || !anchors || !thr || !lut || !out)
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "latent, anchors, thresholds, lut and output must be non-NULL");
+    const size_t esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
+    if (misaligned(lut, p.vec * esize) || misaligned(out, p.vec * 4) || misaligned(x, 4) || misaligned(thr, 4) ||
+        misaligned(anchors, 8))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "a device pointer is not aligned to its element/vector size");
+    return TROPNN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tropnn_hip_abi_version(void) { return TROPNN_HIP_ABI_VERSION; }
+
+const char *tropnn_hip_last_error(void) { return g_last_error.c_str(); }
+
+int tropnn_hip_pairwise_forward(int64_t items, int64_t in_features, int64_t out_features, int64_t tables,
+                                int64_t comparisons, const float *latent, const int64_t *anchors,
+                                const float *thresholds, const void *lut, int lut_dtype, float output_scale,
+                                float *output, tropnn_route_record *route_record, int64_t *indices, float *margins,
+                                tropnn_stream_t stream) {
+    tropnn::Dims d{};
+    if (int rc = make_dims(items, in_features, out_features, tables, comparisons, lut_dtype, d)) return rc;
+    const tropnn::ForwardPlan p = tropnn::plan_forward(d);
+    if (int rc = check_forward_ptrs(d, p, latent, anchors, thresholds, lut, output)) return rc;
+    if (d.items == 0) return ok();
+    if (route_record && misaligned(route_record, 8))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "route_record must be 8-byte aligned");
+    if (p.lds_bytes > 64 * 1024)
+        return fail(TROPNN_ERR_UNSUPPORTED, "forward needs %d bytes of LDS (tables too large)", p.lds_bytes);
+    hipError_t e = tropnn::launch_forward(d, p, latent, anchors, thresholds, lut, output_scale, output, route_record,
+                                          indices, margins, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail("pairwise forward launch", e);
+    return ok();
+}
+
+int tropnn_hip_lut_forward_batch_f32(size_t batch, size_t tables, size_t comparisons, size_t input_dim,
+                                     size_t output_dim, const float *weights, const int64_t *anchors,
+                                     const float *offsets, const float *inputs, float *outputs, float output_scale,
+                                     tropnn_stream_t stream) {
+    return tropnn_hip_pairwise_forward((int64_t)batch, (int64_t)input_dim, (int64_t)output_dim, (int64_t)tables,
+                                       (int64_t)comparisons, inputs, anchors, offsets, weights, TROPNN_LUT_F32,
+                                       output_scale, outputs, nullptr, nullptr, nullptr, stream);
+}
+
+int tropnn_hip_lut_forward_batch_f16(size_t batch, size_t tables, size_t comparisons, size_t input_dim,
+                                     size_t output_dim, const uint16_t *weights_f16, const int64_t *anchors,
+                                     const float *offsets, const float *inputs, float *outputs, float output_scale,
+                                     tropnn_stream_t stream) {
+    return tropnn_hip_pairwise_forward((int64_t)batch, (int64_t)input_dim, (int64_t)output_dim, (int64_t)tables,
+                                       (int64_t)comparisons, inputs, anchors, offsets, weights_f16, TROPNN_LUT_F16,
+                                       output_scale, outputs, nullptr, nullptr, nullptr, stream);
+}
+
+size_t tropnn_hip_pairwise_backward_workspace_size(int64_t items, int64_t in_features, int64_t out_features,
+                                                   int64_t tables, int64_t comparisons, int lut_dtype) {
+    tropnn::Dims d{};
+    if (make_dims(items, in_features, out_features, tables, comparisons, lut_dtype, d) != TROPNN_OK) return 0;
+    ok();
+    return tropnn::plan_backward(d).workspace_bytes;
+}
+
+int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out_features, int64_t tables,
+                                 int64_t comparisons, const float *grad_output, const int64_t *anchors,
+                                 const void *lut, int lut_dtype, const tropnn_route_record *route_record,
+                                 float output_scale, int ste_mode, int surrogate, float *grad_latent,
+                                 float *grad_thresholds, float *grad_lut, void *workspace, size_t workspace_bytes,
+                                 tropnn_stream_t stream) {
+    tropnn::Dims d{};
+    if (int rc = make_dims(items, in_features, out_features, tables, comparisons, lut_dtype, d)) return rc;
+    if (ste_mode != TROPNN_STE_MIN_MARGIN && ste_mode != TROPNN_STE_FULL)
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "ste_mode must be TROPNN_STE_MIN_MARGIN or TROPNN_STE_FULL");
+    if (surrogate != TROPNN_SURROGATE_FAST_SIGMOID_ODD && surrogate != TROPNN_SURROGATE_IZHIKEVICH)
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "surrogate must be a TROPNN_SURROGATE_* value");
+    if (ste_mode != TROPNN_STE_MIN_MARGIN)
+        return fail(TROPNN_ERR_UNSUPPORTED, "only the min-margin STE backward is implemented");
+    if (surrogate != TROPNN_SURROGATE_FAST_SIGMOID_ODD)
+        return fail(TROPNN_ERR_UNSUPPORTED, "only the fast_sigmoid_odd surrogate is implemented");
+    const tropnn::BackwardPlan p = tropnn::plan_backward(d);
+    if (d.items > 0 && (!grad_output || !anchors || !lut || !route_record))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "grad_output, anchors, lut and route_record must be non-NULL");
+    const size_t esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
+    if (misaligned(lut, p.vec * esize) || misaligned(grad_output, p.vec * 4) ||
+        (grad_lut && misaligned(grad_lut, p.vec * 4)) || misaligned(route_record, 8))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "a device pointer is not aligned to its element/vector size");
+    const bool need_ws = grad_latent != nullptr || grad_thresholds != nullptr;
+    if (need_ws && d.items > 0) {
+        if (!workspace || workspace_bytes < p.workspace_bytes)
+            return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace of %zu bytes required, got %zu", p.workspace_bytes,
+                        workspace_bytes);
+        if (misaligned(workspace, 16)) return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+    }
+    if (d.items == 0) {
+        // no items: the parameter gradients are zero (a fill kernel, not a
+        // memset, so the call stays capturable in a HIP graph)
+        hipError_t e = hipSuccess;
+        if (grad_thresholds)
+            e = tropnn::launch_fill_zero(grad_thresholds, static_cast<size_t>(d.tables) * d.comps,
+                                         static_cast<hipStream_t>(stream));
+        if (e == hipSuccess && grad_lut)
+            e = tropnn::launch_fill_zero(grad_lut, static_cast<size_t>(d.tables) * d.rows * d.out_f,
+                                         static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return hip_fail("zero fill launch", e);
+        return ok();
+    }
+    if (p.lut_lds_bytes > 64 * 1024 || p.in_lds_bytes > 64 * 1024)
+        return fail(TROPNN_ERR_UNSUPPORTED, "backward LDS plan exceeds 64 KB");
+    hipError_t e = tropnn::launch_backward(d, p, grad_output, anchors, lut, route_record, output_scale, grad_latent,
+                                           grad_thresholds, grad_lut, static_cast<float *>(workspace),
+                                           static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail("pairwise backward launch", e);
+    return ok();
+}
+
+}  // extern "C"

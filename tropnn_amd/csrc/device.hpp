@@ -1,0 +1,83 @@
+// Device-side helpers shared by the PairwiseLinear kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tropnn_hip.h"
+
+namespace tropnn {
+
+constexpr int kWave = 64;
+
+template <typename T, int V>
+using vec_t = T __attribute__((ext_vector_type(V)));
+
+// Load V consecutive LUT elements (16 bytes at most) and widen them to f32.
+// `p` must be aligned to V * sizeof(T); the host picks V so that every row
+// start and every lane offset is.
+template <typename T, int V>
+__device__ __forceinline__ void load_row(const T *__restrict__ p, float (&d)[V]) {
+    if constexpr (V == 1) {
+        d[0] = static_cast<float>(*p);
+    } else {
+        const vec_t<T, V> v = *reinterpret_cast<const vec_t<T, V> *>(p);
+#pragma unroll
+        for (int i = 0; i < V; ++i) d[i] = static_cast<float>(v[i]);
+    }
+}
+
+template <int V>
+__device__ __forceinline__ void load_f32(const float *__restrict__ p, float (&d)[V]) {
+    load_row<float, V>(p, d);
+}
+
+template <int V>
+__device__ __forceinline__ void store_f32(float *__restrict__ p, const float (&d)[V]) {
+    if constexpr (V == 1) {
+        *p = d[0];
+    } else {
+        vec_t<float, V> v;
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[i] = d[i];
+        *reinterpret_cast<vec_t<float, V> *>(p) = v;
+    }
+}
+
+// Butterfly sum over the lanes whose ids differ only in bits [lo, hi).
+// Every lane of a group ends with the group's total.
+__device__ __forceinline__ float xor_sum(float v, int lo, int hi) {
+    for (int m = lo; m < hi; m <<= 1) v += __shfl_xor(v, m, kWave);
+    return v;
+}
+
+// Preference order of torch.argmin over |margin|: a NaN beats any number
+// (argmin propagates NaN), a smaller value beats a larger one, and ties go to
+// the lower comparison index.
+__device__ __forceinline__ bool min_margin_before(float mag_a, int idx_a, float mag_b, int idx_b) {
+    const bool nan_a = mag_a != mag_a, nan_b = mag_b != mag_b;
+    if (nan_a != nan_b) return nan_a;
+    if (!nan_a && mag_a != mag_b) return mag_a < mag_b;
+    return idx_a < idx_b;
+}
+
+// torch.sign: +1, -1, or 0 for zeros and NaN.
+__device__ __forceinline__ float torch_sign(float u) { return u > 0.f ? 1.f : (u < 0.f ? -1.f : 0.f); }
+
+// fast_sigmoid_odd surrogate, -0.5 * sign(u) / (1 + |u|)^2, in the reference's
+// op order (layers/surrogate.py:16-17) so that each rounding step matches:
+// scale the sign, add one to |u|, square, then one IEEE division.
+__device__ __forceinline__ float fast_sigmoid_odd(float u) {
+    const float num = -0.5f * torch_sign(u);
+    const float base = 1.0f + fabsf(u);
+    const float den = base * base;
+    return num / den;
+}
+
+// Clamp an anchor into [0, n) so a corrupt anchor can never address memory
+// outside the staged input row; the host validates anchors before launch.
+__device__ __forceinline__ int clamp_index(int64_t a, int n) {
+    return (a >= 0 && a < n) ? static_cast<int>(a) : 0;
+}
+
+}  // namespace tropnn
