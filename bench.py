@@ -1,0 +1,243 @@
+"""PairwiseLinear fwd+bwd benchmark on one MI355X (BASELINE.json metric).
+
+Workload ("c2"): PairwiseLinear(128->128, tables=136,
+comparisons=6), f32 LUT [136, 64, 128], batch 512, x ~ N(0,1), upstream grad
+G ~ N(0,1); one step = forward + fast_sigmoid_odd min-margin STE backward
+(y = layer(x); y.backward(G)) with x, thresholds and LUT gradients. Params are
+the module's seeded init (seed 0); inputs are synthetic and already in HBM.
+
+Timed regions (both full fwd+bwd of the module API, no work skipped):
+  graph  -- the step captured once per input batch in a HIP graph
+            (torch.cuda.CUDAGraph); K replays round-robin over 4 distinct
+            resident (x, G) batches. This is `value`.
+  eager  -- K plain autograd steps; the three kernels of each step are
+            bracketed with HIP events recorded on their own launch stream
+            (library hook tropnn_hip_arm_kernel_events), giving the per-kernel
+            average durations used for `roofline`.
+cpu_baseline: the oracle's torch restatement of the reference torch path, same
+step on the host CPU for a bounded number of steps (rank 0, N=1 only).
+
+Prints ONE JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "PairwiseLinear samples/s fwd+bwd (T=136,C=6,B=512) + achieved HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+B, I, O, T, C = 512, 128, 128, 136, 6
+R = 1 << C
+E = 4  # f32 LUT element bytes
+
+
+def algorithmic_bytes() -> dict[str, int]:
+    """Per-launch algorithmic bytes (gather / embedding-bag convention: every
+    (item, table) pair moves its LUT row(s) once, streamed tensors and params
+    once). Sums to the FwdBwd figure of the c2 plan: 148,548,672 B."""
+    fwd = 4 * B * I + 20 * T * C + E * B * T * O + 4 * B * O + B * T
+    table = 4 * B * O + B * T + 2 * E * B * T * O + 4 * B * T * O + 4 * T * R * O
+    inp = 4 * B * I + 4 * B * I + 20 * T * C + 4 * T * C
+    return {"forward": fwd, "backward_table": table, "backward_input": inp}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(budget_s: float) -> dict:
+    """The oracle (torch restatement of the reference torch path) on the host
+    cores: same c2 fwd+bwd step, full batch, as many steps as fit the budget."""
+    import torch
+
+    from oracle.pairwise_torch import OraclePairwiseLinear
+
+    threads = torch.get_num_threads()
+    layer = OraclePairwiseLinear(I, O, tables=T, comparisons=C, seed=0).train()
+    x = torch.randn(B, I, generator=torch.Generator().manual_seed(0)).requires_grad_(True)
+    g = torch.randn(B, 1, O, generator=torch.Generator().manual_seed(1))
+
+    def step() -> None:
+        layer.zero_grad(set_to_none=True)
+        x.grad = None
+        layer(x).backward(g)
+
+    step()  # warmup
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": B / med,
+        "unit": "samples/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"c2 fwd+bwd, full batch {B}, {len(times)} steps (median {med * 1e3:.1f} ms/step), "
+        f"oracle/pairwise_torch.py torch-CPU restatement, torch.set_num_threads={threads}",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work (0 = skip)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(
+            "bench.py measures one GPU only: the PairwiseLinear path is built and measured on a single MI355X "
+            "(multi-GPU sharding is a design note, not part of this build). Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from tropnn_amd import PairwiseLinear
+    from tropnn_amd.backends.pairwise_hip import arm_kernel_events, library_path
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"device {torch.cuda.get_device_name(dev)}, library {library_path()}")
+
+    layer = PairwiseLinear(I, O, tables=T, comparisons=C, seed=0).to(dev).train()
+    layer.cache_route_debug = False  # route debug tensors are not part of the step
+    nb = 4
+    gen = torch.Generator().manual_seed(0)
+    xs = [torch.randn(B, I, generator=gen).to(dev).requires_grad_(True) for _ in range(nb)]
+    gs = [torch.randn(B, 1, O, generator=gen).to(dev) for _ in range(nb)]
+
+    def step(k: int) -> None:
+        layer.zero_grad(set_to_none=True)
+        xs[k].grad = None
+        layer(xs[k]).backward(gs[k])
+
+    # ---- eager warmup + per-kernel event timing
+    for w in range(args.warmup):
+        step(w % nb)
+    torch.cuda.synchronize()
+    names = ("forward", "backward_table", "backward_input")
+    evs = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)] for n in names}
+    stream = torch.cuda.current_stream(dev)
+    for n in names:  # create the event handles
+        for e0, e1 in evs[n]:
+            e0.record(stream)
+            e1.record(stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        for n in names:
+            arm_kernel_events(n, *evs[n][k])
+        step(k % nb)
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    kern_us = {n: 1e3 * sum(e0.elapsed_time(e1) for e0, e1 in evs[n]) / args.steps for n in names}
+    log(f"eager {eager_ms * 1e3:.1f} us/step; kernels (us): " + ", ".join(f"{n}={v:.2f}" for n, v in kern_us.items()))
+
+    # ---- graph capture: one graph per resident batch
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        for w in range(3):
+            step(w % nb)
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    graphs = []
+    for k in range(nb):
+        layer.zero_grad(set_to_none=True)
+        xs[k].grad = None
+        gph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gph):
+            layer(xs[k]).backward(gs[k])
+        graphs.append(gph)
+    torch.cuda.synchronize()
+    for w in range(args.warmup):
+        graphs[w % nb].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        graphs[k % nb].replay()
+    torch.cuda.synchronize()
+    graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    log(f"graph {graph_ms * 1e3:.1f} us/step")
+
+    # ---- roofline of the dominant kernel
+    algo = algorithmic_bytes()
+    dom = max(names, key=lambda n: kern_us[n])
+    achieved = algo[dom] / (kern_us[dom] * 1e-6) / 1e9
+    kernels = {
+        n: {"avg_us": round(kern_us[n], 3), "algorithmic_bytes": algo[n], "achieved_GBs": round(algo[n] / (kern_us[n] * 1e-6) / 1e9, 1)}
+        for n in names
+    }
+
+    cpu = None
+    if args.cpu_budget > 0:
+        log("timing the CPU baseline")
+        cpu = cpu_baseline(args.cpu_budget)
+        log(f"cpu baseline {cpu['value']:.0f} samples/s on {cpu['cores']} threads")
+
+    value = B / (graph_ms * 1e-3)
+    total_algo = sum(algo.values())
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(graph_ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: x, G ~ N(0,1), 4 resident batches round-robin; seeded module init (seed 0)",
+        "config": {
+            "workload": "c2: PairwiseLinear(128->128, tables=136, comparisons=6), f32 LUT [136,64,128], batch 512, "
+            "fwd + fast_sigmoid_odd min-margin STE bwd (x, thresholds, LUT grads)",
+            "batch": B,
+            "in_features": I,
+            "out_features": O,
+            "tables": T,
+            "comparisons": C,
+            "lut_dtype": "f32",
+            "mode": "hip-graph replay of the module fwd+bwd",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom,
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "step_algorithmic_GBs": round(total_algo / (graph_ms * 1e-3) / 1e9, 1),
+        "eager_ms_per_step": round(eager_ms, 6),
+        "kernels": kernels,
+    }
+    if cpu:
+        out["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

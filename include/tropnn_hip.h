@@ -111,6 +111,20 @@ size_t tropnn_hip_pairwise_backward_workspace_size(int64_t items, int64_t in_fea
                                                    int64_t tables, int64_t comparisons, int lut_dtype);
 
 /*
+ * Inverse anchor index used by the input-gradient backward: for every input
+ * feature f, offsets[f] .. offsets[f+1] delimit its entries in `entries`,
+ * each (t << 4) | (c << 1) | side for an anchors[t][c][side] equal to f, in
+ * increasing (t, c, side) order (a fixed summation order, so grad_latent is
+ * deterministic). offsets: in_features + 1 int32; entries: 2 * tables *
+ * comparisons int32. Depends on the anchors only: build once, rebuild when
+ * the anchors change. No counterpart in the reference, whose input gradient
+ * is an index_put accumulate (layers/pairwise.py:131-132) or an atomic add
+ * (backends/pairwise_tilelang.py:279-284).
+ */
+int tropnn_hip_build_anchor_index(int64_t in_features, int64_t tables, int64_t comparisons, const int64_t *anchors,
+                                  int32_t *offsets, int32_t *entries, tropnn_stream_t stream);
+
+/*
  * Backward of the training forward with the min-margin STE. Replaces
  * _PairwiseTileLangFunction.backward and its LUT-scatter and min-STE kernels
  * (backends/pairwise_tilelang.py:118-288, 481-534); the math is the autograd
@@ -121,18 +135,38 @@ size_t tropnn_hip_pairwise_backward_workspace_size(int64_t items, int64_t in_fea
  *   gu[b,t]           = D[b,t] * surrogate'(u[b,t])
  *   grad_latent[b,i]  = sum_t gu[b,t] * ([i = a(t,r)] - [i = b'(t,r)])   (fully overwritten)
  *   grad_thresholds[t,c] = -sum_b [r[b,t] = c] * gu[b,t]                (fully overwritten)
- * Any of the three gradient pointers may be NULL to skip that gradient.
+ * Every sum runs in a fixed order: the results are deterministic.
+ * Any of the three gradient pointers may be NULL to skip that gradient;
+ * grad_latent needs the anchor index (index_offsets / index_entries from
+ * tropnn_hip_build_anchor_index), the others accept NULL index pointers.
  * Only ste_mode = TROPNN_STE_MIN_MARGIN and surrogate =
  * TROPNN_SURROGATE_FAST_SIGMOID_ODD are implemented; the others return
  * TROPNN_ERR_UNSUPPORTED. workspace: device memory of at least
- * tropnn_hip_pairwise_backward_workspace_size() bytes, 256-byte aligned.
+ * tropnn_hip_pairwise_backward_workspace_size() bytes, 16-byte aligned.
  */
 int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out_features, int64_t tables,
-                                 int64_t comparisons, const float *grad_output, const int64_t *anchors,
-                                 const void *lut, int lut_dtype, const tropnn_route_record *route_record,
-                                 float output_scale, int ste_mode, int surrogate, float *grad_latent,
-                                 float *grad_thresholds, float *grad_lut, void *workspace, size_t workspace_bytes,
-                                 tropnn_stream_t stream);
+                                 int64_t comparisons, const float *grad_output, const void *lut, int lut_dtype,
+                                 const tropnn_route_record *route_record, const int32_t *index_offsets,
+                                 const int32_t *index_entries, float output_scale, int ste_mode, int surrogate,
+                                 float *grad_latent, float *grad_thresholds, float *grad_lut, void *workspace,
+                                 size_t workspace_bytes, tropnn_stream_t stream);
+
+/*
+ * Profiling hook (no counterpart in the reference, whose harness times whole
+ * calls, tools/benchmarking/benchmark.py:91-118). Arms two caller-created
+ * hipEvent_t handles to be recorded on the launch stream immediately before
+ * and after the NEXT launch of one kernel:
+ *   TROPNN_KERNEL_FORWARD         the fused route + gather + scale kernel
+ *   TROPNN_KERNEL_BACKWARD_TABLE  the table-major LUT-gradient / STE-dot kernel
+ *   TROPNN_KERNEL_BACKWARD_INPUT  the input / threshold gradient kernel
+ * One-shot and process-global (not for concurrent use from several threads).
+ * Passing NULL events disarms. Lets a benchmark time one kernel per step with
+ * events on the exact stream the kernel runs on.
+ */
+#define TROPNN_KERNEL_FORWARD 0
+#define TROPNN_KERNEL_BACKWARD_TABLE 1
+#define TROPNN_KERNEL_BACKWARD_INPUT 2
+int tropnn_hip_arm_kernel_events(int kernel, void *start_event, void *stop_event);
 
 #ifdef __cplusplus
 }

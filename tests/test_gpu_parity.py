@@ -373,3 +373,40 @@ def test_c4_large_layer_properties():
     assert rel_err(gx1 + gx2, gx) <= 1e-5
     assert rel_err(gthr1 + gthr2, gthr) <= 1e-4
     assert rel_err(glut1 + glut2, glut) <= 1e-5
+
+
+# ---------------------------------------------------------------- determinism and the anchor index
+def test_backward_is_deterministic():
+    """Every backward sum runs in a fixed order (no atomics): two runs on the
+    same inputs give bit-identical gradients."""
+    _, hip = make_pair(128, 128, 136, 6, seed=0, thr_std=0.1)
+    x = seeded((512, 128), seed=0).to(DEV)
+    g = seeded((512, 1, 128), seed=1).to(DEV)
+    grads = []
+    for _ in range(2):
+        hip.zero_grad(set_to_none=True)
+        xg = x.clone().requires_grad_(True)
+        hip.train()(xg).backward(g)
+        grads.append((xg.grad.clone(), hip.thresholds.grad.clone(), hip.lut.grad.clone()))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+
+
+def test_anchor_index_matches_numpy():
+    from tropnn_amd.backends.pairwise_hip import anchor_index
+
+    gen = torch.Generator().manual_seed(3)
+    i, t, c = 37, 29, 5
+    anchors = torch.randint(0, i, (t, c, 2), generator=gen)
+    offsets, entries = anchor_index(anchors.to(DEV), i)
+    offsets, entries = offsets.cpu().numpy(), entries.cpu().numpy()
+    flat = anchors.reshape(-1).numpy()
+    want_entries = []
+    want_offsets = [0]
+    for f in range(i):
+        for k in np.nonzero(flat == f)[0]:
+            tt, cc, side = (k // 2) // c, (k // 2) % c, k % 2
+            want_entries.append((tt << 4) | (cc << 1) | side)
+        want_offsets.append(len(want_entries))
+    np.testing.assert_array_equal(offsets, np.array(want_offsets))
+    np.testing.assert_array_equal(entries[: len(want_entries)], np.array(want_entries))

@@ -37,7 +37,12 @@ _PKG_DIR = Path(__file__).resolve().parent.parent
 DEFAULT_LIBRARY = _PKG_DIR / "libtropnn_hip.so"
 _LOCK = threading.Lock()
 _LIB: ctypes.CDLL | None = None
-_ANCHORS_CHECKED: dict[tuple, bool] = {}
+# Per-anchors-tensor caches live as attributes of the anchors tensor object
+# itself (not in a table keyed by address: the caching allocator reuses the
+# addresses of freed tensors), validated by the tensor's version counter,
+# which every in-place write bumps.
+_CHECKED_ATTR = "_tropnn_hip_checked"
+_INDEX_ATTR = "_tropnn_hip_anchor_index"
 
 EXPORTED_SYMBOLS = (
     "tropnn_hip_abi_version",
@@ -47,7 +52,10 @@ EXPORTED_SYMBOLS = (
     "tropnn_hip_pairwise_forward",
     "tropnn_hip_pairwise_backward_workspace_size",
     "tropnn_hip_pairwise_backward",
+    "tropnn_hip_build_anchor_index",
+    "tropnn_hip_arm_kernel_events",
 )
+KERNEL_IDS = {"forward": 0, "backward_table": 1, "backward_input": 2}
 
 
 def library_path() -> Path:
@@ -70,8 +78,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tropnn_hip_pairwise_forward.restype = i
     lib.tropnn_hip_pairwise_backward_workspace_size.argtypes = [i64, i64, i64, i64, i64, i]
     lib.tropnn_hip_pairwise_backward_workspace_size.restype = sz
-    lib.tropnn_hip_pairwise_backward.argtypes = [i64, i64, i64, i64, i64, p, p, p, i, p, f, i, i, p, p, p, p, sz, p]
+    lib.tropnn_hip_build_anchor_index.argtypes = [i64, i64, i64, p, p, p, p]
+    lib.tropnn_hip_build_anchor_index.restype = i
+    lib.tropnn_hip_pairwise_backward.argtypes = [i64, i64, i64, i64, i64, p, p, i, p, p, p, f, i, i, p, p, p, p, sz, p]
     lib.tropnn_hip_pairwise_backward.restype = i
+    lib.tropnn_hip_arm_kernel_events.argtypes = [i, p, p]
+    lib.tropnn_hip_arm_kernel_events.restype = i
 
 
 def load_library() -> ctypes.CDLL:
@@ -128,6 +140,16 @@ def _check(rc: int, what: str) -> None:
     raise RuntimeError(f"{what}: {ERR_NAMES.get(rc, rc)}: {msg}")
 
 
+def arm_kernel_events(kernel: str, start: "torch.cuda.Event | None", stop: "torch.cuda.Event | None") -> None:
+    """Record `start` / `stop` (torch.cuda.Event objects that have been
+    recorded once, so their handles exist) around the next launch of `kernel`
+    ("forward", "backward_table", "backward_input"); None disarms."""
+    lib = load_library()
+    h0 = None if start is None else start.cuda_event
+    h1 = None if stop is None else stop.cuda_event
+    _check(lib.tropnn_hip_arm_kernel_events(KERNEL_IDS[kernel], h0, h1), "tropnn_hip_arm_kernel_events")
+
+
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -145,18 +167,37 @@ def _require_gpu(*tensors: Tensor) -> None:
 
 
 def check_anchors(anchors: Tensor, in_features: int) -> None:
-    """Every anchor must index the input row. Checked once per
-    (storage, version, in_features) because it reads the tensor back."""
-    key = (anchors.data_ptr(), anchors._version, tuple(anchors.shape), in_features, anchors.device)
-    if _ANCHORS_CHECKED.get(key):
+    """Every anchor must index the input row. Checked once per anchors tensor
+    and version because it reads the tensor back to the host."""
+    key = (anchors._version, in_features)
+    if getattr(anchors, _CHECKED_ATTR, None) == key:
         return
     if anchors.numel() > 0:
         lo, hi = int(anchors.min().item()), int(anchors.max().item())
         if lo < 0 or hi >= in_features:
             raise ValueError(f"anchors must lie in [0, {in_features}), got range [{lo}, {hi}]")
-    if len(_ANCHORS_CHECKED) > 256:
-        _ANCHORS_CHECKED.clear()
-    _ANCHORS_CHECKED[key] = True
+    setattr(anchors, _CHECKED_ATTR, key)
+
+
+def anchor_index(anchors: Tensor, in_features: int) -> tuple[Tensor, Tensor]:
+    """(offsets [I+1], entries [2TC]) int32 inverse anchor index on the
+    anchors' device, built by tropnn_hip_build_anchor_index and cached per
+    anchors tensor and version: the anchors are a buffer that training never
+    changes, so this runs once per layer."""
+    key = (anchors._version, in_features)
+    hit = getattr(anchors, _INDEX_ATTR, None)
+    if hit is not None and hit[0] == key:
+        return hit[1], hit[2]
+    tables, comps, _ = anchors.shape
+    offsets = torch.empty(in_features + 1, device=anchors.device, dtype=torch.int32)
+    entries = torch.empty(max(2 * tables * comps, 1), device=anchors.device, dtype=torch.int32)
+    anc = anchors.contiguous()
+    rc = load_library().tropnn_hip_build_anchor_index(
+        in_features, tables, comps, _ptr(anc), _ptr(offsets), _ptr(entries), _stream(anchors.device)
+    )
+    _check(rc, "tropnn_hip_build_anchor_index")
+    setattr(anchors, _INDEX_ATTR, (key, offsets, entries))
+    return offsets, entries
 
 
 def _validate(latent: Tensor, anchors: Tensor, thresholds: Tensor, lut: Tensor) -> tuple[int, int, int, int, int, int]:
@@ -270,6 +311,9 @@ class _PairwiseHipFunction(torch.autograd.Function):
             want_record=want_record,
             return_route=return_route,
         )
+        # the anchor index is built (once per anchors version) at forward
+        # time, outside any backward-pass graph capture
+        ctx.index = anchor_index(anchors, latent.shape[2]) if (ste and ctx.needs_input_grad[0]) else None
         ctx.save_for_backward(record, anchors, lut_read)
         ctx.dims = tuple(latent.shape) + (lut_read.shape[2],)
         ctx.ste = ste
@@ -299,6 +343,7 @@ class _PairwiseHipFunction(torch.autograd.Function):
         lut_dtype = LUT_F16 if lut_read.dtype == torch.float16 else LUT_F32
         ws_bytes = lib.tropnn_hip_pairwise_backward_workspace_size(items, in_features, out_features, tables, comps, lut_dtype)
         workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8) if (want_x or want_thr) else None
+        offsets, entries = ctx.index if want_x else (None, None)
         rc = lib.tropnn_hip_pairwise_backward(
             items,
             in_features,
@@ -306,10 +351,11 @@ class _PairwiseHipFunction(torch.autograd.Function):
             tables,
             comps,
             _ptr(g),
-            _ptr(anchors),
             _ptr(lut_read),
             lut_dtype,
             _ptr(record),
+            _ptr(offsets),
+            _ptr(entries),
             ctx.output_scale,
             STE_MIN_MARGIN,
             SURROGATE_IDS[ctx.surrogate],

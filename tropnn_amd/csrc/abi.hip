@@ -5,6 +5,7 @@
 #include <stdio.h>
 
 #include <limits>
+#include <mutex>
 #include <string>
 
 #include "launch.hpp"
@@ -80,9 +81,39 @@ int check_forward_ptrs(const tropnn::Dims &d, const tropnn::ForwardPlan &p, cons
     return TROPNN_OK;
 }
 
+std::mutex g_events_mu;
+tropnn::ArmedEvents g_armed[3];
+
 }  // namespace
 
+namespace tropnn {
+
+ArmedEvents take_armed_events(int kernel) {
+    std::lock_guard<std::mutex> lock(g_events_mu);
+    ArmedEvents e = g_armed[kernel];
+    g_armed[kernel] = ArmedEvents{};
+    return e;
+}
+
+void arm_events(int kernel, hipEvent_t start, hipEvent_t stop) {
+    std::lock_guard<std::mutex> lock(g_events_mu);
+    g_armed[kernel].start = start;
+    g_armed[kernel].stop = stop;
+}
+
+}  // namespace tropnn
+
 extern "C" {
+
+int tropnn_hip_arm_kernel_events(int kernel, void *start_event, void *stop_event) {
+    if (kernel < TROPNN_KERNEL_FORWARD || kernel > TROPNN_KERNEL_BACKWARD_INPUT)
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "unknown kernel id %d", kernel);
+    if ((start_event == nullptr) != (stop_event == nullptr))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "arm both events or neither");
+    tropnn::arm_events(kernel, static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event));
+    return ok();
+}
+
 
 int tropnn_hip_abi_version(void) { return TROPNN_HIP_ABI_VERSION; }
 
@@ -134,12 +165,28 @@ size_t tropnn_hip_pairwise_backward_workspace_size(int64_t items, int64_t in_fea
     return tropnn::plan_backward(d).workspace_bytes;
 }
 
+int tropnn_hip_build_anchor_index(int64_t in_features, int64_t tables, int64_t comparisons, const int64_t *anchors,
+                                  int32_t *offsets, int32_t *entries, tropnn_stream_t stream) {
+    tropnn::Dims d{};
+    if (int rc = make_dims(0, in_features, 1, tables, comparisons, TROPNN_LUT_F32, d)) return rc;
+    if (tables * comparisons * 2 >= (int64_t{1} << 27))
+        return fail(TROPNN_ERR_UNSUPPORTED, "tables*comparisons too large for the anchor index");
+    if (!anchors || !offsets || !entries)
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "anchors, offsets and entries must be non-NULL");
+    if (misaligned(anchors, 8) || misaligned(offsets, 4) || misaligned(entries, 4))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "a device pointer is not aligned to its element size");
+    hipError_t e = tropnn::launch_anchor_index(anchors, d.in_f, d.tables, d.comps, offsets, entries,
+                                               static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail("anchor index launch", e);
+    return ok();
+}
+
 int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out_features, int64_t tables,
-                                 int64_t comparisons, const float *grad_output, const int64_t *anchors,
-                                 const void *lut, int lut_dtype, const tropnn_route_record *route_record,
-                                 float output_scale, int ste_mode, int surrogate, float *grad_latent,
-                                 float *grad_thresholds, float *grad_lut, void *workspace, size_t workspace_bytes,
-                                 tropnn_stream_t stream) {
+                                 int64_t comparisons, const float *grad_output, const void *lut, int lut_dtype,
+                                 const tropnn_route_record *route_record, const int32_t *index_offsets,
+                                 const int32_t *index_entries, float output_scale, int ste_mode, int surrogate,
+                                 float *grad_latent, float *grad_thresholds, float *grad_lut, void *workspace,
+                                 size_t workspace_bytes, tropnn_stream_t stream) {
     tropnn::Dims d{};
     if (int rc = make_dims(items, in_features, out_features, tables, comparisons, lut_dtype, d)) return rc;
     if (ste_mode != TROPNN_STE_MIN_MARGIN && ste_mode != TROPNN_STE_FULL)
@@ -151,19 +198,6 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
     if (surrogate != TROPNN_SURROGATE_FAST_SIGMOID_ODD)
         return fail(TROPNN_ERR_UNSUPPORTED, "only the fast_sigmoid_odd surrogate is implemented");
     const tropnn::BackwardPlan p = tropnn::plan_backward(d);
-    if (d.items > 0 && (!grad_output || !anchors || !lut || !route_record))
-        return fail(TROPNN_ERR_INVALID_ARGUMENT, "grad_output, anchors, lut and route_record must be non-NULL");
-    const size_t esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
-    if (misaligned(lut, p.vec * esize) || misaligned(grad_output, p.vec * 4) ||
-        (grad_lut && misaligned(grad_lut, p.vec * 4)) || misaligned(route_record, 8))
-        return fail(TROPNN_ERR_INVALID_ARGUMENT, "a device pointer is not aligned to its element/vector size");
-    const bool need_ws = grad_latent != nullptr || grad_thresholds != nullptr;
-    if (need_ws && d.items > 0) {
-        if (!workspace || workspace_bytes < p.workspace_bytes)
-            return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace of %zu bytes required, got %zu", p.workspace_bytes,
-                        workspace_bytes);
-        if (misaligned(workspace, 16)) return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
-    }
     if (d.items == 0) {
         // no items: the parameter gradients are zero (a fill kernel, not a
         // memset, so the call stays capturable in a HIP graph)
@@ -177,11 +211,25 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
         if (e != hipSuccess) return hip_fail("zero fill launch", e);
         return ok();
     }
+    if (!grad_output || !lut || !route_record)
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "grad_output, lut and route_record must be non-NULL");
+    if (grad_latent && (!index_offsets || !index_entries))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "grad_latent needs the anchor index (tropnn_hip_build_anchor_index)");
+    const size_t esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
+    if (misaligned(lut, p.vec * esize) || misaligned(grad_output, p.vec * 4) ||
+        (grad_lut && misaligned(grad_lut, p.vec * 4)) || misaligned(route_record, 8))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "a device pointer is not aligned to its element/vector size");
+    if (grad_latent || grad_thresholds) {
+        if (!workspace || workspace_bytes < p.workspace_bytes)
+            return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace of %zu bytes required, got %zu", p.workspace_bytes,
+                        workspace_bytes);
+        if (misaligned(workspace, 16)) return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+    }
     if (p.lut_lds_bytes > 64 * 1024 || p.in_lds_bytes > 64 * 1024)
-        return fail(TROPNN_ERR_UNSUPPORTED, "backward LDS plan exceeds 64 KB");
-    hipError_t e = tropnn::launch_backward(d, p, grad_output, anchors, lut, route_record, output_scale, grad_latent,
-                                           grad_thresholds, grad_lut, static_cast<float *>(workspace),
-                                           static_cast<hipStream_t>(stream));
+        return fail(TROPNN_ERR_UNSUPPORTED, "backward LDS plan exceeds 64 KB (in_features or tables too large)");
+    hipError_t e = tropnn::launch_backward(d, p, grad_output, lut, route_record, index_offsets, index_entries,
+                                           output_scale, grad_latent, grad_thresholds, grad_lut,
+                                           static_cast<float *>(workspace), static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail("pairwise backward launch", e);
     return ok();
 }

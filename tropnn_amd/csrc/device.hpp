@@ -51,6 +51,28 @@ __device__ __forceinline__ float xor_sum(float v, int lo, int hi) {
     return v;
 }
 
+// Cross-lane move inside a 16-lane DPP row (no LDS traffic).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of n consecutive lanes (n a power of two <= 64);
+// every lane ends with its group's total, bit-identical across the group
+// (each step adds a partner's partial, and IEEE addition commutes).
+// Steps: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
+// row_half_mirror (pairs the two quads of a half row), row_mirror (pairs the
+// two half rows), then cross-row shuffles (ds_bpermute) for 32 and 64.
+__device__ __forceinline__ float group_sum(float v, int n) {
+    if (n >= 2) v += dpp_mov<0xB1>(v);
+    if (n >= 4) v += dpp_mov<0x4E>(v);
+    if (n >= 8) v += dpp_mov<0x141>(v);
+    if (n >= 16) v += dpp_mov<0x140>(v);
+    if (n >= 32) v += __shfl_xor(v, 16, kWave);
+    if (n >= 64) v += __shfl_xor(v, 32, kWave);
+    return v;
+}
+
 // Preference order of torch.argmin over |margin|: a NaN beats any number
 // (argmin propagates NaN), a smaller value beats a larger one, and ties go to
 // the lower comparison index.

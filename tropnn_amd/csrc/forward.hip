@@ -7,19 +7,22 @@
 //   scale   layers/base.py:76-77
 //   min-margin selection saved for the backward: layers/pairwise.py:138-140
 //
-// Workgroup = items_per_wg items x one output tile. Phases:
-//   1. the items' input rows are staged in LDS with coalesced loads;
+// Workgroup = items_per_wg items x one output tile. The kernel is latency
+// bound at small batch, so every phase issues all of its independent global
+// loads before it waits:
+//   1. each wave loads the anchors and thresholds of its first route ballots
+//      while the workgroup stages the items' input rows in LDS (one round trip);
 //   2. route: one wave ballot evaluates 64 / P tables (P lanes per table, one
-//      comparison per lane, P = next power of two >= C); byte-aligned fields
-//      of the ballot mask are the LUT row codes, written to LDS. Training
-//      also reduces argmin |margin| inside each P-lane group and writes the
-//      route record; the debug path writes int64 codes and f32 margins;
+//      comparison per lane, P = next power of two >= C); P-bit fields of the
+//      ballot mask are the LUT row codes, written to LDS. Training also
+//      reduces argmin |margin| inside each P-lane group and writes the route
+//      record; the debug path writes int64 codes and f32 margins;
 //   3. gather: lanes cover the output tile with 16-byte row loads (float4 or
 //      8 x f16); the 64 / lanes_per_row sub-groups of a wave and the
 //      waves_per_item waves of an item take disjoint strided sets of tables,
-//      with 8 row loads in flight per lane; partial sums are combined by a
-//      lane butterfly and, across waves, through LDS in a fixed order, then
-//      scaled and stored.
+//      issuing up to 16 row loads per lane before the first add; partial sums
+//      are combined by a lane butterfly and, across waves, through LDS in a
+//      fixed order, then scaled and stored.
 #include "device.hpp"
 #include "launch.hpp"
 
@@ -41,7 +44,71 @@ struct FwdArgs {
     int codes_off, red_off;
 };
 
-constexpr int kUnroll = 8;
+constexpr int kGather = 16;   // row loads in flight per lane
+constexpr int kBallots = 4;   // ballots whose parameters a wave prefetches
+
+// One lane's comparator: anchors (clamped) and threshold of (table, comparison).
+struct Comparator {
+    int a, b;
+    float thr;
+    bool valid;
+};
+
+__device__ __forceinline__ Comparator load_comparator(const FwdArgs &p, int t, int c) {
+    Comparator q{0, 0, 0.f, false};
+    if (t < p.tables && c < p.comps) {
+        const int64_t *ap = p.anchors + (static_cast<size_t>(t) * p.comps + c) * 2;
+        q.a = clamp_index(ap[0], p.in_f);
+        q.b = clamp_index(ap[1], p.in_f);
+        q.thr = p.thr[t * p.comps + c];
+        q.valid = true;
+    }
+    return q;
+}
+
+template <bool TRAIN, bool DEBUG>
+__device__ __forceinline__ void route_ballot(const FwdArgs &p, const float *xs, uint16_t *codes, const Comparator &q,
+                                             int t, int c, int slot, int lpt, int n_items, int item0) {
+    const uint64_t field = (1ull << lpt) - 1ull;
+    for (int i = 0; i < n_items; ++i) {  // wave-uniform
+        float m = 0.f;
+        if (q.valid) m = (xs[i * p.in_f + q.a] - xs[i * p.in_f + q.b]) - q.thr;
+        const uint64_t mask = __ballot(q.valid && m > 0.f);
+        const int code = static_cast<int>((mask >> (slot * lpt)) & field);
+        const bool head = (c == 0) && (t < p.tables);
+        const size_t b = static_cast<size_t>(item0 + i);
+        if (head) codes[i * p.tables + t] = static_cast<uint16_t>(code);
+        if constexpr (DEBUG) {
+            if (p.margins != nullptr && q.valid) p.margins[(b * p.tables + t) * p.comps + c] = m;
+            if (p.indices != nullptr && head) p.indices[b * p.tables + t] = code;
+        }
+        if constexpr (TRAIN) {
+            // argmin |m| over the P lanes of this table; padding lanes
+            // (c >= C) carry +inf and index 64 so they never win.
+            float mag = q.valid ? fabsf(m) : __builtin_inff();
+            int idx = q.valid ? c : kWave;
+            float val = m;
+            for (int s = 1; s < lpt; s <<= 1) {
+                const float omag = __shfl_xor(mag, s, kWave);
+                const int oidx = __shfl_xor(idx, s, kWave);
+                const float oval = __shfl_xor(val, s, kWave);
+                if (min_margin_before(omag, oidx, mag, idx)) {
+                    mag = omag;
+                    idx = oidx;
+                    val = oval;
+                }
+            }
+            if (head) {
+                tropnn_route_record r;
+                r.u = val;
+                r.code = static_cast<uint16_t>(code);
+                r.r = static_cast<uint8_t>(idx);
+                r.reserved = 0;
+                p.rec[static_cast<size_t>(t) * p.items + b] = r;
+            }
+        }
+    }
+}
 
 template <typename T, int V, bool TRAIN, bool DEBUG>
 __global__ __launch_bounds__(512) void pairwise_forward_kernel(FwdArgs a) {
@@ -55,74 +122,38 @@ __global__ __launch_bounds__(512) void pairwise_forward_kernel(FwdArgs a) {
     const int item0 = blockIdx.x * a.items_per_wg;
     const int n_items = min(a.items_per_wg, a.items - item0);
 
-    // 1. stage the input rows (contiguous in x)
+    const int lpt = 1 << a.lpt_log2;
+    const int tpb = kWave >> a.lpt_log2;
+    const int nballot = (a.tables + tpb - 1) / tpb;
+    const int slot = lane >> a.lpt_log2;
+    const int c = lane & (lpt - 1);
+
+    // 1. prefetch this wave's first ballots, stage the input rows
+    Comparator pre[kBallots];
+#pragma unroll
+    for (int j = 0; j < kBallots; ++j) pre[j] = load_comparator(a, (wave + j * nwaves) * tpb + slot, c);
     {
         const float *src = a.x + static_cast<size_t>(item0) * a.in_f;
         const int n = n_items * a.in_f;
-        for (int k = tid; k < n; k += nthr) xs[k] = src[k];
+        if ((a.in_f & 3) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+            const int n4 = n >> 2;
+            for (int k = tid; k < n4; k += nthr)
+                reinterpret_cast<vec_t<float, 4> *>(xs)[k] = reinterpret_cast<const vec_t<float, 4> *>(src)[k];
+        } else {
+            for (int k = tid; k < n; k += nthr) xs[k] = src[k];
+        }
     }
     __syncthreads();
 
-    // 2. route: ballots of 64 / P tables
-    {
-        const int lpt = 1 << a.lpt_log2;
-        const int tpb = kWave >> a.lpt_log2;
-        const int nballot = (a.tables + tpb - 1) / tpb;
-        const int slot = lane >> a.lpt_log2;
-        const int c = lane & (lpt - 1);
-        const uint64_t field = (lpt == 64) ? ~0ull : ((1ull << lpt) - 1ull);
-        // each wave owns whole ballots: a lane's anchors and threshold are
-        // loaded once and reused for every item of the workgroup
-        for (int kb = wave; kb < nballot; kb += nwaves) {  // wave-uniform
-            const int t = kb * tpb + slot;
-            const bool valid = (t < a.tables) && (c < a.comps);
-            int ia = 0, ib = 0;
-            float th = 0.f;
-            if (valid) {
-                const int64_t *ap = a.anchors + (static_cast<size_t>(t) * a.comps + c) * 2;
-                ia = clamp_index(ap[0], a.in_f);
-                ib = clamp_index(ap[1], a.in_f);
-                th = a.thr[t * a.comps + c];
-            }
-            for (int i = 0; i < n_items; ++i) {  // wave-uniform
-                float m = 0.f;
-                if (valid) m = (xs[i * a.in_f + ia] - xs[i * a.in_f + ib]) - th;
-                const uint64_t mask = __ballot(valid && m > 0.f);
-                const int code = static_cast<int>((mask >> (slot << a.lpt_log2)) & field);
-                const bool head = (c == 0) && (t < a.tables);
-                const size_t b = static_cast<size_t>(item0 + i);
-                if (head) codes[i * a.tables + t] = static_cast<uint16_t>(code);
-                if constexpr (DEBUG) {
-                    if (a.margins != nullptr && valid) a.margins[(b * a.tables + t) * a.comps + c] = m;
-                    if (a.indices != nullptr && head) a.indices[b * a.tables + t] = code;
-                }
-                if constexpr (TRAIN) {
-                    // argmin |m| over the P lanes of this table; padding lanes
-                    // (c >= C) carry +inf and index 64 so they never win.
-                    float mag = valid ? fabsf(m) : __builtin_inff();
-                    int idx = valid ? c : kWave;
-                    float val = m;
-                    for (int s = 1; s < lpt; s <<= 1) {
-                        const float omag = __shfl_xor(mag, s, kWave);
-                        const int oidx = __shfl_xor(idx, s, kWave);
-                        const float oval = __shfl_xor(val, s, kWave);
-                        if (min_margin_before(omag, oidx, mag, idx)) {
-                            mag = omag;
-                            idx = oidx;
-                            val = oval;
-                        }
-                    }
-                    if (head) {
-                        tropnn_route_record r;
-                        r.u = val;
-                        r.code = static_cast<uint16_t>(code);
-                        r.r = static_cast<uint8_t>(idx);
-                        r.reserved = 0;
-                        a.rec[static_cast<size_t>(t) * a.items + b] = r;
-                    }
-                }
-            }
-        }
+    // 2. route
+#pragma unroll
+    for (int j = 0; j < kBallots; ++j) {
+        const int kb = wave + j * nwaves;
+        if (kb < nballot) route_ballot<TRAIN, DEBUG>(a, xs, codes, pre[j], kb * tpb + slot, c, slot, lpt, n_items, item0);
+    }
+    for (int kb = wave + kBallots * nwaves; kb < nballot; kb += nwaves) {  // many tables: rest of the ballots
+        const Comparator q = load_comparator(a, kb * tpb + slot, c);
+        route_ballot<TRAIN, DEBUG>(a, xs, codes, q, kb * tpb + slot, c, slot, lpt, n_items, item0);
     }
     __syncthreads();
 
@@ -148,24 +179,23 @@ __global__ __launch_bounds__(512) void pairwise_forward_kernel(FwdArgs a) {
         const uint16_t *my = codes + i * a.tables;
         const size_t row_stride = static_cast<size_t>(a.out_f);
         const size_t table_stride = static_cast<size_t>(a.rows) * a.out_f;
-        int t = gid;
-        for (; t + (kUnroll - 1) * gpi < a.tables; t += kUnroll * gpi) {
-            float v[kUnroll][V];
+        for (int t0 = gid; t0 < a.tables; t0 += kGather * gpi) {
+            float v[kGather][V];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                const int tt = t + u * gpi;
-                load_row<T, V>(lut + tt * table_stride + my[tt] * row_stride, v[u]);
+            for (int u = 0; u < kGather; ++u) {
+                const int tt = t0 + u * gpi;
+                const bool ok = tt < a.tables;
+                const int ts = ok ? tt : 0;  // masked lanes read row 0 of table 0
+                load_row<T, V>(lut + ts * table_stride + (ok ? my[ts] : 0) * row_stride, v[u]);
+                if (!ok) {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) v[u][e] = 0.f;
+                }
             }
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u)
+            for (int u = 0; u < kGather; ++u)
 #pragma unroll
                 for (int e = 0; e < V; ++e) acc[e] += v[u][e];
-        }
-        for (; t < a.tables; t += gpi) {
-            float v[V];
-            load_row<T, V>(lut + t * table_stride + my[t] * row_stride, v);
-#pragma unroll
-            for (int e = 0; e < V; ++e) acc[e] += v[e];
         }
     }
 
@@ -200,6 +230,8 @@ __global__ __launch_bounds__(512) void pairwise_forward_kernel(FwdArgs a) {
 template <typename T, int V>
 hipError_t launch_typed(const FwdArgs &args, const ForwardPlan &p, bool train, bool debug, hipStream_t stream) {
     const dim3 grid(p.blocks, p.o_tiles), block(p.threads);
+    const ArmedEvents ev = take_armed_events(TROPNN_KERNEL_FORWARD);
+    record_event(ev.start, stream);
     if (train && debug)
         hipLaunchKernelGGL((pairwise_forward_kernel<T, V, true, true>), grid, block, p.lds_bytes, stream, args);
     else if (train)
@@ -208,7 +240,9 @@ hipError_t launch_typed(const FwdArgs &args, const ForwardPlan &p, bool train, b
         hipLaunchKernelGGL((pairwise_forward_kernel<T, V, false, true>), grid, block, p.lds_bytes, stream, args);
     else
         hipLaunchKernelGGL((pairwise_forward_kernel<T, V, false, false>), grid, block, p.lds_bytes, stream, args);
-    return hipGetLastError();
+    const hipError_t e = hipGetLastError();
+    record_event(ev.stop, stream);
+    return e;
 }
 
 int ilog2(int v) {
@@ -235,11 +269,11 @@ ForwardPlan plan_forward(const Dims &d) {
     p.o_tiles = (d.out_f + p.o_tile - 1) / p.o_tile;
     const int sub = kWave >> p.lpr_log2;
 
-    // Fill ~2048 waves (256 CUs x 8): split an item's tables over several
-    // waves only when items x tiles alone cannot.
+    // Aim for ~4096 waves (256 CUs x 16): split an item's tables over several
+    // waves only when items x tiles alone cannot fill the chip.
     const long long units = static_cast<long long>(d.items) * p.o_tiles;
     int wpi = 1;
-    while (wpi < 8 && units * wpi < 2048 && static_cast<long long>(wpi) * 2 * sub <= d.tables) wpi <<= 1;
+    while (wpi < 8 && units * wpi < 4096 && static_cast<long long>(wpi) * 2 * sub <= d.tables) wpi <<= 1;
     int ipw = 8 / wpi;
     // keep the staged input rows within 32 KB of LDS
     while (ipw > 1 && static_cast<long long>(ipw) * d.in_f * 4 > 32 * 1024) ipw >>= 1;

@@ -43,15 +43,15 @@ struct BackwardPlan {
     int vec;            // elements per lane load of grad_output / LUT rows
     int o_chunk;        // output columns per table workgroup
     int o_chunks;       // grid.y of the table kernel
-    int lpr_log2;       // lanes per item row in the table kernel
-    int lut_threads;    // threads of a table workgroup
-    int lut_lds_bytes;  // slab + gradient slab
+    int pitch;          // LDS row pitch (floats) of the LUT slab
+    int slices_log2;    // lanes (vec-wide column slices) per gradient row
+    int lut_threads;    // threads of a table workgroup = items per sort tile
+    int lut_lds_bytes;  // slab + histograms + bucket starts + sorted tile
     int in_items_per_wg;
     int in_threads;
     int in_lds_bytes;
     size_t workspace_bytes;  // partial STE dots [o_chunks][T][B] f32
 };
-
 
 ForwardPlan plan_forward(const Dims &d);
 BackwardPlan plan_backward(const Dims &d);
@@ -60,9 +60,26 @@ hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, c
                           const float *thr, const void *lut, float scale, float *out, tropnn_route_record *rec,
                           int64_t *indices, float *margins, hipStream_t stream);
 
-hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *grad_out, const int64_t *anchors,
-                           const void *lut, const tropnn_route_record *rec, float scale, float *grad_x,
-                           float *grad_thr, float *grad_lut, float *workspace, hipStream_t stream);
+hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *grad_out, const void *lut,
+                           const tropnn_route_record *rec, const int32_t *index_offsets,
+                           const int32_t *index_entries, float scale, float *grad_x, float *grad_thr,
+                           float *grad_lut, float *workspace, hipStream_t stream);
+
+// Inverse anchor index (see tropnn_hip_build_anchor_index).
+hipError_t launch_anchor_index(const int64_t *anchors, int in_f, int tables, int comps, int32_t *offsets,
+                               int32_t *entries, hipStream_t stream);
+
+// Events armed by tropnn_hip_arm_kernel_events for the next launch of a
+// kernel; take_armed_events clears them. record_event tolerates NULL.
+struct ArmedEvents {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+ArmedEvents take_armed_events(int kernel);
+void arm_events(int kernel, hipEvent_t start, hipEvent_t stop);
+inline void record_event(hipEvent_t e, hipStream_t s) {
+    if (e != nullptr) (void)hipEventRecord(e, s);
+}
 
 // Writes n zeros with a kernel (no hipMemsetAsync node in captured graphs).
 hipError_t launch_fill_zero(float *p, size_t n, hipStream_t stream);
