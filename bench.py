@@ -54,6 +54,36 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+KERNEL_SOURCES = (
+    "tropnn_amd/csrc/forward.hip",
+    "tropnn_amd/csrc/backward.hip",
+    "tropnn_amd/csrc/abi.hip",
+    "tropnn_amd/csrc/device.hpp",
+    "tropnn_amd/csrc/launch.hpp",
+    "include/tropnn_hip.h",
+)
+
+
+def measured_traffic(kernel: str) -> int | None:
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE scaled by a
+    calibration copy), used only while the kernel sources still hash to the
+    profiled ones; otherwise None."""
+    import hashlib
+
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    rec = json.loads(path.read_text())
+    h = hashlib.sha256()
+    for src in KERNEL_SOURCES:
+        h.update((ROOT / src).read_bytes())
+    if rec.get("source_sha256") != h.hexdigest() or kernel not in rec.get("kernels", {}):
+        return None
+    k = rec["kernels"][kernel]
+    return int(k["fetch_bytes"] + k["write_bytes"])
+
+
 def cpu_baseline(budget_s: float) -> dict:
     """The oracle (torch restatement of the reference torch path) on the host
     cores: same c2 fwd+bwd step, full batch, as many steps as fit the budget."""
@@ -96,6 +126,13 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work (0 = skip)")
+    ap.add_argument(
+        "--calibrate-copy-bytes",
+        type=int,
+        default=0,
+        help="also run one plain device copy of this many bytes (the reference dispatch that scales "
+        "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)",
+    )
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
@@ -187,6 +224,16 @@ def main() -> int:
         for n in names
     }
 
+    if args.calibrate_copy_bytes > 0:
+        n = args.calibrate_copy_bytes // 4
+        src = torch.ones(n, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy of {n * 4} bytes done")
+        del src, dst
+
     cpu = None
     if args.cpu_budget > 0:
         log("timing the CPU baseline")
@@ -226,7 +273,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(dom),
         },
         "cpu_baseline": cpu,
         "step_algorithmic_GBs": round(total_algo / (graph_ms * 1e-3) / 1e9, 1),

@@ -1,0 +1,106 @@
+"""The C ABI of libtropnn_hip.so without a GPU: the library loads, exports
+exactly what include/tropnn_hip.h declares, and rejects bad arguments with
+the documented codes before any launch (these calls touch no device)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import importlib
+
+ph = importlib.import_module("tropnn_amd.backends.pairwise_hip")
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "tropnn_hip.h"
+
+
+def header_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(tropnn_hip_[a-z0-9_]+)\s*\(", text)))
+
+
+def header_define(name: str) -> int:
+    m = re.search(rf"#define {name} (\d+)", HEADER.read_text())
+    assert m, name
+    return int(m.group(1))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    path = ph.library_path()
+    if not path.exists():
+        pytest.skip("libtropnn_hip.so not built (run __graft_entry__.build())")
+    return ph.load_library()
+
+
+def test_exports_match_header(lib):
+    declared = header_functions()
+    assert sorted(ph.EXPORTED_SYMBOLS) == declared
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    assert lib.tropnn_hip_abi_version() == header_define("TROPNN_HIP_ABI_VERSION") == ph.ABI_VERSION
+
+
+def test_constants_match_header():
+    assert header_define("TROPNN_LUT_F32") == ph.LUT_F32
+    assert header_define("TROPNN_LUT_F16") == ph.LUT_F16
+    assert header_define("TROPNN_SURROGATE_FAST_SIGMOID_ODD") == ph.SURROGATE_IDS["fast_sigmoid_odd"]
+    assert header_define("TROPNN_SURROGATE_IZHIKEVICH") == ph.SURROGATE_IDS["izhikevich"]
+    assert header_define("TROPNN_MAX_COMPARISONS") == ph.MAX_COMPARISONS
+    assert header_define("TROPNN_KERNEL_FORWARD") == ph.KERNEL_IDS["forward"]
+
+
+def test_workspace_size(lib):
+    n = lib.tropnn_hip_pairwise_backward_workspace_size(512, 128, 128, 136, 6, ph.LUT_F32)
+    assert n > 0 and n % (136 * 512 * 4) == 0  # whole [chunks][T][B] f32 planes
+    assert lib.tropnn_hip_pairwise_backward_workspace_size(512, 128, 128, 136, 9, ph.LUT_F32) == 0
+
+
+def _err(lib) -> str:
+    return lib.tropnn_hip_last_error().decode()
+
+
+def test_forward_rejects_bad_arguments(lib):
+    fwd = lib.tropnn_hip_pairwise_forward
+    # tables < 1
+    assert fwd(4, 8, 5, 0, 3, 8, 8, 8, 8, 0, 1.0, 8, None, None, None, None) == 1
+    assert "tables" in _err(lib)
+    # comparisons above the supported maximum: unsupported, not invalid
+    assert fwd(4, 8, 5, 3, 9, 8, 8, 8, 8, 0, 1.0, 8, None, None, None, None) == 2
+    assert "comparisons" in _err(lib)
+    # unknown LUT dtype
+    assert fwd(4, 8, 5, 3, 3, 8, 8, 8, 8, 7, 1.0, 8, None, None, None, None) == 1
+    # NULL buffers
+    assert fwd(4, 8, 5, 3, 3, None, 8, 8, 8, 0, 1.0, 8, None, None, None, None) == 1
+    assert "non-NULL" in _err(lib)
+    # empty batch is a no-op success
+    assert fwd(0, 8, 5, 3, 3, None, None, None, None, 0, 1.0, None, None, None, None, None) == 0
+    assert _err(lib) == ""
+
+
+def test_backward_rejects_bad_arguments(lib):
+    bwd = lib.tropnn_hip_pairwise_backward
+    args = [4, 8, 5, 3, 3, 16, 16, 0, 16, 16, 16, 1.0, 0, 0, 16, 16, 16, 16, 1 << 20, None]
+    bad_mode = list(args)
+    bad_mode[12] = 1  # full STE: not implemented
+    assert bwd(*bad_mode) == 2 and "min-margin" in _err(lib)
+    bad_surr = list(args)
+    bad_surr[13] = 1  # izhikevich: not implemented
+    assert bwd(*bad_surr) == 2 and "fast_sigmoid_odd" in _err(lib)
+    no_index = list(args)
+    no_index[9] = None
+    assert bwd(*no_index) == 1 and "anchor index" in _err(lib)
+    small_ws = list(args)
+    small_ws[18] = 4
+    assert bwd(*small_ws) == 1 and "workspace" in _err(lib)
+
+
+def test_event_hook_rejects_bad_kernel(lib):
+    assert lib.tropnn_hip_arm_kernel_events(7, None, None) == 1
+    assert lib.tropnn_hip_arm_kernel_events(0, ctypes.c_void_p(8), None) == 1
+    assert lib.tropnn_hip_arm_kernel_events(0, None, None) == 0
