@@ -43,11 +43,17 @@ E = 4  # f32 LUT element bytes
 def algorithmic_bytes() -> dict[str, int]:
     """Per-launch algorithmic bytes (gather / embedding-bag convention: every
     (item, table) pair moves its LUT row(s) once, streamed tensors and params
-    once). Sums to the FwdBwd figure of the c2 plan: 148,548,672 B."""
+    once), split by the kernel that moves them. Sums to the FwdBwd figure of
+    the c2 plan: 148,548,672 B.
+      forward: x, anchors + thresholds, one row per (item, table), y, codes;
+      backward_item: G, x re-read, codes, current + neighbour rows per
+        (item, table), grad_x, anchors + thresholds;
+      backward_table: one f32 grad-row contribution per (item, table),
+        grad_lut once, grad_thr."""
     fwd = 4 * B * I + 20 * T * C + E * B * T * O + 4 * B * O + B * T
-    table = 4 * B * O + B * T + 2 * E * B * T * O + 4 * B * T * O + 4 * T * R * O
-    inp = 4 * B * I + 4 * B * I + 20 * T * C + 4 * T * C
-    return {"forward": fwd, "backward_table": table, "backward_input": inp}
+    item = 4 * B * O + 4 * B * I + B * T + 2 * E * B * T * O + 4 * B * I + 20 * T * C
+    table = 4 * B * T * O + 4 * T * R * O + 4 * T * C
+    return {"forward": fwd, "backward_item": item, "backward_table": table}
 
 
 def log(msg: str) -> None:
@@ -170,7 +176,7 @@ def main() -> int:
     for w in range(args.warmup):
         step(w % nb)
     torch.cuda.synchronize()
-    names = ("forward", "backward_table", "backward_input")
+    names = ("forward", "backward_item", "backward_table")
     evs = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)] for n in names}
     stream = torch.cuda.current_stream(dev)
     for n in names:  # create the event handles

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TROPNN_HIP_ABI_VERSION 1
+#define TROPNN_HIP_ABI_VERSION 2
 
 /* status codes */
 #define TROPNN_OK 0
@@ -113,9 +113,9 @@ size_t tropnn_hip_pairwise_backward_workspace_size(int64_t items, int64_t in_fea
 /*
  * Inverse anchor index used by the input-gradient backward: for every input
  * feature f, offsets[f] .. offsets[f+1] delimit its entries in `entries`,
- * each (t << 4) | (c << 1) | side for an anchors[t][c][side] equal to f, in
- * increasing (t, c, side) order (a fixed summation order, so grad_latent is
- * deterministic). offsets: in_features + 1 int32; entries: 2 * tables *
+ * each ((t * comparisons + c) << 1) | side, the flat position of an
+ * anchors[t][c][side] equal to f, in increasing order (a fixed summation
+ * order, so grad_latent is deterministic). offsets: in_features + 1 int32; entries: 2 * tables *
  * comparisons int32. Depends on the anchors only: build once, rebuild when
  * the anchors change. No counterpart in the reference, whose input gradient
  * is an index_put accumulate (layers/pairwise.py:131-132) or an atomic add
@@ -157,15 +157,15 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
  * hipEvent_t handles to be recorded on the launch stream immediately before
  * and after the NEXT launch of one kernel:
  *   TROPNN_KERNEL_FORWARD         the fused route + gather + scale kernel
- *   TROPNN_KERNEL_BACKWARD_TABLE  the table-major LUT-gradient / STE-dot kernel
- *   TROPNN_KERNEL_BACKWARD_INPUT  the input / threshold gradient kernel
+ *   TROPNN_KERNEL_BACKWARD_TABLE  the per-table LUT-gradient / threshold-gradient kernel
+ *   TROPNN_KERNEL_BACKWARD_ITEM   the per-item STE-dot / input-gradient kernel
  * One-shot and process-global (not for concurrent use from several threads).
  * Passing NULL events disarms. Lets a benchmark time one kernel per step with
  * events on the exact stream the kernel runs on.
  */
 #define TROPNN_KERNEL_FORWARD 0
 #define TROPNN_KERNEL_BACKWARD_TABLE 1
-#define TROPNN_KERNEL_BACKWARD_INPUT 2
+#define TROPNN_KERNEL_BACKWARD_ITEM 2
 int tropnn_hip_arm_kernel_events(int kernel, void *start_event, void *stop_event);
 
 #ifdef __cplusplus

@@ -154,6 +154,21 @@ def test_eval_forward_f32(i, o, t, c, b):
     assert rel_err(y_hip, y_ref) <= F32_TOL
 
 
+@pytest.mark.parametrize(
+    "i,o,t,c,b",
+    # f16 row loads of 1, 2, 4 and 8 halves per lane, and several output tiles
+    [(64, 9, 20, 5, 33), (64, 128, 20, 5, 33), (64, 256, 37, 4, 17), (64, 1000, 12, 8, 5), (96, 2048, 40, 7, 3)],
+)
+def test_eval_forward_f16_shapes(i, o, t, c, b):
+    ref, hip = make_pair(i, o, t, c, seed=1, thr_std=0.1, lut_dtype="f16")
+    x = seeded((b, i), seed=2)
+    with torch.no_grad():
+        y_ref = ref.eval()(x)
+        y_hip = hip.eval()(x.to(DEV))
+    assert torch.equal(hip._last_indices.cpu(), ref._last_indices)
+    assert rel_err(y_hip, y_ref) <= F16_TOL
+
+
 @pytest.mark.parametrize("b", [1, 64, 8192])
 def test_eval_forward_f16_lut(b):
     """c3: same layer, LUT read as an RNE f16 copy, against the f32 oracle."""
@@ -406,7 +421,7 @@ def test_anchor_index_matches_numpy():
     for f in range(i):
         for k in np.nonzero(flat == f)[0]:
             tt, cc, side = (k // 2) // c, (k // 2) % c, k % 2
-            want_entries.append((tt << 4) | (cc << 1) | side)
+            want_entries.append(((tt * c + cc) << 1) | side)
         want_offsets.append(len(want_entries))
     np.testing.assert_array_equal(offsets, np.array(want_offsets))
     np.testing.assert_array_equal(entries[: len(want_entries)], np.array(want_entries))

@@ -26,7 +26,7 @@ from typing import Any
 import torch
 from torch import Tensor
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 LUT_F32, LUT_F16 = 0, 1
 SURROGATE_IDS = {"fast_sigmoid_odd": 0, "izhikevich": 1}
 STE_MIN_MARGIN, STE_FULL = 0, 1
@@ -55,7 +55,7 @@ EXPORTED_SYMBOLS = (
     "tropnn_hip_build_anchor_index",
     "tropnn_hip_arm_kernel_events",
 )
-KERNEL_IDS = {"forward": 0, "backward_table": 1, "backward_input": 2}
+KERNEL_IDS = {"forward": 0, "backward_table": 1, "backward_item": 2}
 
 
 def library_path() -> Path:
@@ -143,7 +143,7 @@ def _check(rc: int, what: str) -> None:
 def arm_kernel_events(kernel: str, start: "torch.cuda.Event | None", stop: "torch.cuda.Event | None") -> None:
     """Record `start` / `stop` (torch.cuda.Event objects that have been
     recorded once, so their handles exist) around the next launch of `kernel`
-    ("forward", "backward_table", "backward_input"); None disarms."""
+    ("forward", "backward_table", "backward_item"); None disarms."""
     lib = load_library()
     h0 = None if start is None else start.cuda_event
     h1 = None if stop is None else stop.cuda_event

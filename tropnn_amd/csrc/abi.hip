@@ -106,7 +106,7 @@ void arm_events(int kernel, hipEvent_t start, hipEvent_t stop) {
 extern "C" {
 
 int tropnn_hip_arm_kernel_events(int kernel, void *start_event, void *stop_event) {
-    if (kernel < TROPNN_KERNEL_FORWARD || kernel > TROPNN_KERNEL_BACKWARD_INPUT)
+    if (kernel < TROPNN_KERNEL_FORWARD || kernel > TROPNN_KERNEL_BACKWARD_ITEM)
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "unknown kernel id %d", kernel);
     if ((start_event == nullptr) != (stop_event == nullptr))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "arm both events or neither");
@@ -133,6 +133,11 @@ int tropnn_hip_pairwise_forward(int64_t items, int64_t in_features, int64_t out_
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "route_record must be 8-byte aligned");
     if (p.lds_bytes > 64 * 1024)
         return fail(TROPNN_ERR_UNSUPPORTED, "forward needs %d bytes of LDS (tables too large)", p.lds_bytes);
+    // the gather addresses the LUT through one buffer resource with 32-bit offsets
+    const int64_t lut_bytes = int64_t{d.tables} * d.rows * d.out_f * (d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4);
+    if (lut_bytes > (int64_t{1} << 31))
+        return fail(TROPNN_ERR_UNSUPPORTED, "LUT of %lld bytes exceeds the forward's 2 GiB limit",
+                    (long long)lut_bytes);
     hipError_t e = tropnn::launch_forward(d, p, latent, anchors, thresholds, lut, output_scale, output, route_record,
                                           indices, margins, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail("pairwise forward launch", e);
@@ -216,7 +221,8 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
     if (grad_latent && (!index_offsets || !index_entries))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "grad_latent needs the anchor index (tropnn_hip_build_anchor_index)");
     const size_t esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
-    if (misaligned(lut, p.vec * esize) || misaligned(grad_output, p.vec * 4) ||
+    const size_t gvec = static_cast<size_t>(p.vec > p.item_vec ? p.vec : p.item_vec);
+    if (misaligned(lut, p.item_vec * esize) || misaligned(grad_output, gvec * 4) ||
         (grad_lut && misaligned(grad_lut, p.vec * 4)) || misaligned(route_record, 8))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "a device pointer is not aligned to its element/vector size");
     if (grad_latent || grad_thresholds) {
@@ -225,8 +231,14 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
                         workspace_bytes);
         if (misaligned(workspace, 16)) return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
     }
-    if (p.lut_lds_bytes > 64 * 1024 || p.in_lds_bytes > 64 * 1024)
-        return fail(TROPNN_ERR_UNSUPPORTED, "backward LDS plan exceeds 64 KB (in_features or tables too large)");
+    if (p.lut_lds_bytes > 160 * 1024 || p.item_lds_bytes > 64 * 1024)
+        return fail(TROPNN_ERR_UNSUPPORTED, "backward LDS plan exceeds the workgroup limit (in_features or tables too large)");
+    // grad rows and the LUT are addressed through buffer resources with 32-bit offsets
+    const int64_t lut_bytes = int64_t{d.tables} * d.rows * d.out_f * esize;
+    const int64_t g_bytes = int64_t{d.items} * d.out_f * 4;
+    if (lut_bytes > (int64_t{1} << 31) || g_bytes > (int64_t{1} << 31))
+        return fail(TROPNN_ERR_UNSUPPORTED, "LUT (%lld bytes) or grad_output (%lld bytes) exceeds the 2 GiB limit",
+                    (long long)lut_bytes, (long long)g_bytes);
     hipError_t e = tropnn::launch_backward(d, p, grad_output, lut, route_record, index_offsets, index_entries,
                                            output_scale, grad_latent, grad_thresholds, grad_lut,
                                            static_cast<float *>(workspace), static_cast<hipStream_t>(stream));

@@ -10,23 +10,34 @@
 //
 // No float atomics anywhere (LDS float atomics serialise badly on gfx950, and
 // fixed summation orders make every gradient deterministic). Two launches:
-//  (1) table kernel, one workgroup per (table, output chunk). Items are taken
-//      in tiles of blockDim items; each tile is counting-sorted by LUT row
-//      code in LDS (per-wave ballot ranking, per-wave histograms, one scan),
-//      which keeps item order inside a bucket. Each thread owns fixed
-//      (row, column-slice) units of the table's gradient and accumulates its
-//      bucket's grad rows in registers, so grad_lut is written exactly once.
-//      The same pass forms the STE partial dot
-//      sum_{o in chunk} g[o] * (L[nb,o] - L[code,o]) from the LDS LUT slab,
-//      reduced over the row's lanes with DPP, into the workspace
-//      [chunks][T][B].
-//  (2) input kernel, two roles in one grid. Role A (item tiles): gu[b,t] =
-//      D[b,t] * surrogate'(u) for the tile's items go to LDS; then one thread
-//      per (item, input feature) walks that feature's entries of the inverse
-//      anchor index (the (table, comparison, side) triples that read the
-//      feature, in increasing order) and writes grad_latent directly. Role B
-//      (one workgroup per table) reduces -gu per comparison over all items in
-//      a fixed order and writes grad_thresholds.
+//  (1) item kernel, one workgroup per item, shaped like the forward: each wave
+//      takes up to 16 consecutive tables. A lane holds the record of table
+//      lane / 4; the wave moves each table's code and min-margin comparison to
+//      scalar registers and loads the two LUT rows L[code], L[nb] (nb = code
+//      with the min-margin bit flipped) with scalar row offsets, 64 lanes
+//      spanning the row. Each lane forms its part of the 16 STE dots
+//      sum_o G[b,o] (L[nb,o] - L[code,o]); one reduce-scatter over the wave
+//      (DPP inside rows, shuffles across them) completes all 16 at once, lane
+//      4i holding table i's dot. That lane applies scale and surrogate
+//      derivative, stores gu[t][b] and expands it into the item's LDS slots
+//      (one per (table, comparison), zero except at the min-margin one). Then
+//      one thread per input feature sums the signed slots named by the
+//      feature's entries of the inverse anchor index, in entry order, and
+//      writes grad_latent.
+//  (2) table kernel, one workgroup per (table, output chunk of S * V columns).
+//      Items are taken in tiles of 1024; each tile is counting-sorted by LUT
+//      row code in LDS (C wave ballots give every item its rank among equal
+//      codes of its wave and every lane the population of one code, one DPP
+//      scan turns the per-wave counts into bucket offsets), which keeps item
+//      order inside a bucket. Row groups of S lanes (V columns each) then walk
+//      equal contiguous ranges of the sorted list, eight items per step: grad
+//      rows arrive through buffer loads (out-of-range offsets read zeros, so
+//      the walk carries no masks), are summed along runs of equal codes in
+//      registers, and each finished run goes to its LUT row (whole bucket in
+//      the range) or to one of the range's two split slots; a combine pass
+//      adds the split pieces in range order. Rows are scaled and written once.
+//      The workgroup of chunk 0 also reduces table t's threshold gradient
+//      from gu.
 //  A third, tiny kernel builds the inverse anchor index; callers rebuild it
 //  only when the anchors change.
 #include "device.hpp"
@@ -35,29 +46,228 @@
 namespace tropnn {
 namespace {
 
-constexpr int kLutThreads = 1024;
-constexpr int kInThreads = 256;
-constexpr int kBatch = 8;     // bucket items whose grad rows are loaded together
-constexpr int kUnits = 4;     // max (row, slice) units per thread in the table kernel
-constexpr int kPairs = 4;     // records per thread per batch in the input kernel
+constexpr int kLutThreads = 1024;  // items per sort tile
+constexpr int kItemTables = 16;    // tables per item-kernel wave (one reduce-scatter)
+constexpr int kEntries = 16;       // index entries a walker reads per batch
+constexpr int kIndexRegs = 2;      // index words per thread loaded ahead of the dots
 
-struct LutArgs {
+struct ItemArgs {
     const float *grad_out;
     const void *lut;
     const uint64_t *rec;
+    const int32_t *index_offsets;  // [in_f + 1]
+    const int32_t *index_entries;  // ((t * C + c) << 1) | side
+    float scale;
+    float *grad_x;
+    float *gu;  // [T][B]
+    uint32_t lut_bytes, g_bytes;
+    int items, in_f, out_f, tables, comps, rows, row_bytes, table_bytes, per_wave, o_tiles;
+};
+
+struct LutArgs {
+    const float *grad_out;
+    const uint64_t *rec;
+    const float *gu;  // [T][B], for the threshold gradient
     float scale;
     float *grad_lut;
-    float *dpart;
-    int items, out_f, tables, comps, rows, o_chunk, pitch, slices_log2;
-    int hist_off, start_off, sorted_off;  // LDS byte offsets
+    float *grad_thr;
+    uint32_t g_bytes;
+    int items, out_f, tables, comps, rows, o_chunk;
+    int hist_off, start_off, sorted_off, rowbuf_off, part_off, thr_off, wtot_off;  // LDS byte offsets
 };
 
 __device__ __forceinline__ int rec_code(uint64_t r) { return static_cast<int>((r >> 32) & 0xffffu); }
 __device__ __forceinline__ int rec_r(uint64_t r) { return static_cast<int>((r >> 48) & 0xffu); }
 __device__ __forceinline__ float rec_u(uint64_t r) { return __builtin_bit_cast(float, static_cast<uint32_t>(r)); }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// DPP controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1]
+// (lane ^ 2), row_half_mirror (lane ^ 7 inside 8), row_ror:8 (lane ^ 8 inside
+// 16).
+constexpr int kXor1 = 0xB1, kXor2 = 0x4E, kMirror8 = 0x141, kRor8 = 0x128;
+
+// The value of the lane whose id differs in bit BIT (inside a row of 16 via
+// DPP; bit 2 uses the half-row mirror, lane ^ 7, which also flips the lower
+// bits, and every step below only relies on the flipped high bit; bits 4 and 5
+// via cross-row shuffles).
+template <int BIT>
+__device__ __forceinline__ float flip(float v) {
+    if constexpr (BIT == 5) return __shfl_xor(v, 32, kWave);
+    else if constexpr (BIT == 4) return __shfl_xor(v, 16, kWave);
+    else if constexpr (BIT == 3) return dpp<kRor8>(v);
+    else if constexpr (BIT == 2) return dpp<kMirror8>(v);
+    else if constexpr (BIT == 1) return dpp<kXor2>(v);
+    else return dpp<kXor1>(v);
+}
+
+// Reduce-scatter of N values per lane over the S lanes of an aligned lane
+// group (N <= S <= 64, powers of two): lane j returns the group total of value
+// u = (j / (S / N)) & (N - 1). The first log2(N) steps pair lanes across one
+// high bit, keep half of the values and add the partner's copy of that half;
+// the remaining steps are plain butterflies. The sum tree is fixed, so every
+// total is deterministic.
+template <int BIT, int N>
+__device__ __forceinline__ void rs_select(float (&v)[N], int j) {
+    if constexpr (N > 1) {
+        constexpr int H = N / 2;
+        const bool up = ((j >> BIT) & 1) != 0;
+        float w[H];
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const float keep = up ? v[H + i] : v[i];
+            const float send = up ? v[i] : v[H + i];
+            w[i] = keep + flip<BIT>(send);
+        }
+        rs_select<BIT - 1, H>(w, j);
+        v[0] = w[0];
+    } else if constexpr (BIT >= 0) {
+        v[0] += flip<BIT>(v[0]);
+        rs_select<BIT - 1, 1>(v, j);
+    }
+}
+
+template <int S, int N>
+__device__ __forceinline__ float reduce_scatter(const float (&d)[N], int j) {
+    static_assert(S == 4 || S == 8 || S == 16 || S == 32 || S == 64, "lane groups of 4 to 64 lanes");
+    static_assert(N <= S && (N & (N - 1)) == 0, "N is a power of two <= S");
+    float v[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = d[i];
+    constexpr int kTop = S == 64 ? 5 : (S == 32 ? 4 : (S == 16 ? 3 : (S == 8 ? 2 : 1)));
+    rs_select<kTop, N>(v, j);
+    return v[0];
+}
+
+// ------------------------------------------------------------------ item kernel
+
+// At most 80 VGPRs (6 waves per SIMD): two workgroups of up to 9 waves then
+// share a CU.
+template <typename T, int N>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void pairwise_bwd_item_kernel(ItemArgs a) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    float *gud = reinterpret_cast<float *>(lds);  // [T * C] this item's gu slots
+
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = blockIdx.x;
+    const int C = a.comps, R = a.rows;
+    const int t0 = wave * a.per_wave;
+    const int nt = max(0, min(a.tables, t0 + a.per_wave) - t0);
+
+    // 0. the inverse anchor index (offsets, then entries) is staged in LDS
+    //    for the feature walk; its first loads go out with the first block's
+    const int nidx = a.grad_x != nullptr ? a.in_f + 1 + 2 * a.tables * C : 0;
+    int *idx_s = reinterpret_cast<int *>(gud + a.tables * C);  // [in_f + 1 + 2 T C]
+    int iv[kIndexRegs];
+#pragma unroll
+    for (int q = 0; q < kIndexRegs; ++q) {
+        const int k = tid + q * nthr;
+        iv[q] = k < nidx ? (k <= a.in_f ? a.index_offsets[k] : a.index_entries[k - a.in_f - 1]) : 0;
+    }
+
+    const __amdgpu_buffer_rsrc_t lut_rsrc = buffer_rsrc(a.lut, a.lut_bytes);
+    const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.grad_out, a.g_bytes);
+    constexpr int kLoaded = item_wave_tables(static_cast<int>(sizeof(T)), N);  // tables with rows in flight
+    const int ti = lane >> 2;  // lane l serves table l / 4 of a block
+    for (int tb = t0; tb < t0 + nt; tb += kLoaded) {  // blocks of kLoaded tables
+        const int ntb = min(kLoaded, t0 + nt - tb);
+        // 1. this lane's table record
+        const bool has = ti < ntb;
+        const uint64_t rr = has ? a.rec[static_cast<size_t>(tb + ti) * a.items + b] : 0ull;
+        const int code_v = rec_code(rr) & (R - 1);
+        const int r_v = rec_r(rr) & 7;
+
+        // 2. per table: both LUT rows at scalar row offsets (all in flight),
+        //    then this lane's part of each dot against the item's grad row
+        float d[kItemTables];
+#pragma unroll
+        for (int i = 0; i < kItemTables; ++i) d[i] = 0.f;
+        for (int ct = 0; ct < a.o_tiles; ++ct) {
+            const int col = ct * (kWave * N) + lane * N;
+            const bool col_ok = col < a.out_f;
+            float g[N];
+            buffer_row<float, N>(g_rsrc, col_ok ? static_cast<uint32_t>(b * a.out_f + col) * 4u : kOutOfRange, 0, g);
+            const uint32_t voff = col_ok ? static_cast<uint32_t>(col) * static_cast<uint32_t>(sizeof(T)) : kOutOfRange;
+            // all kLoaded tables' rows in flight at once (sized to 80 VGPRs)
+            {
+                constexpr int kBatch = kLoaded;
+                constexpr int i0 = 0;
+                float lk[kBatch][N], ln[kBatch][N];
+#pragma unroll
+                for (int i = 0; i < kBatch; ++i) {
+                    const bool live = i0 + i < ntb;
+                    const int code = __builtin_amdgcn_readlane(code_v, 4 * (i0 + i));
+                    const int nb = (code ^ (1 << __builtin_amdgcn_readlane(r_v, 4 * (i0 + i)))) & (R - 1);
+                    const int trow = (tb + i0 + i) * a.table_bytes;
+                    buffer_row<T, N>(lut_rsrc, live ? voff : kOutOfRange, live ? trow + code * a.row_bytes : 0, lk[i]);
+                    buffer_row<T, N>(lut_rsrc, live ? voff : kOutOfRange, live ? trow + nb * a.row_bytes : 0, ln[i]);
+                }
+#pragma unroll
+                for (int i = 0; i < kBatch; ++i)
+#pragma unroll
+                    for (int e = 0; e < N; ++e) d[i0 + i] += g[e] * (ln[i][e] - lk[i][e]);
+            }
+        }
+
+        // 3. lane 4i completes table i's dot: gu, stored and expanded into slots
+        const float dot = reduce_scatter<kWave, kItemTables>(d, lane) * a.scale;
+        if (has && (lane & 3) == 0) {
+            const float gu = dot * fast_sigmoid_odd(rec_u(rr));
+            if (a.gu != nullptr) a.gu[static_cast<size_t>(tb + ti) * a.items + b] = gu;
+            float *slot = gud + (tb + ti) * C;
+            for (int c = 0; c < C; ++c) slot[c] = c == r_v ? gu : 0.f;
+        }
+    }
+    if (a.grad_x == nullptr) return;
+#pragma unroll
+    for (int q = 0; q < kIndexRegs; ++q)
+        if (tid + q * nthr < nidx) idx_s[tid + q * nthr] = iv[q];
+    for (int k = tid + kIndexRegs * nthr; k < nidx; k += nthr)
+        idx_s[k] = k <= a.in_f ? a.index_offsets[k] : a.index_entries[k - a.in_f - 1];
+    __syncthreads();
+
+    // 4. one thread per input feature: its signed slots in entry order
+    const int *off_s = idx_s, *ent_s = idx_s + a.in_f + 1;
+    for (int f = tid; f < a.in_f; f += nthr) {
+        const int f0 = off_s[f], f1 = off_s[f + 1];
+        float gx = 0.f;
+        for (int eb = f0; eb < f1; eb += kEntries) {
+            int en[kEntries];
+#pragma unroll
+            for (int q = 0; q < kEntries; ++q) en[q] = eb + q < f1 ? ent_s[eb + q] : 0;
+            float v[kEntries];
+#pragma unroll
+            for (int q = 0; q < kEntries; ++q) v[q] = eb + q < f1 ? gud[en[q] >> 1] : 0.f;
+#pragma unroll
+            for (int q = 0; q < kEntries; ++q)
+                if (eb + q < f1) gx = (en[q] & 1) ? gx - v[q] : gx + v[q];
+        }
+        a.grad_x[static_cast<size_t>(b) * a.in_f + f] = gx;
+    }
+}
+
+// ------------------------------------------------------------------ table kernel
+
+// Inclusive prefix sum over the 64 lanes of a wave: DPP shifts inside rows of
+// 16, then the row broadcasts of lanes 15 and 31. All lanes must be active.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);   // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+    return v;
+}
+
 // Exclusive prefix sum over n <= 1024 ints in LDS, in place, by the first
-// wave (serial across 64-wide chunks, shuffle scan inside a chunk).
+// wave (serial across 64-wide chunks, shuffle scan inside a chunk); v[n]
+// receives the total.
 __device__ void wave_exclusive_scan(int *v, int n, int lane) {
     int carry = 0;
     for (int base = 0; base < n; base += kWave) {
@@ -74,261 +284,279 @@ __device__ void wave_exclusive_scan(int *v, int n, int lane) {
     if (lane == 0) v[n] = carry;
 }
 
-template <typename T, int V>
+// Sorted-list entry: item in the tile (10 bits), code (8), whether the item's
+// bucket lies inside the walk range of its position (1), and else which of
+// that range's two split slots its segment uses (1).
+__device__ __forceinline__ uint32_t pack_entry(int item, int code, bool inside, int slot) {
+    return static_cast<uint32_t>(item) | (static_cast<uint32_t>(code) << 10) | (static_cast<uint32_t>(inside) << 18) |
+           (static_cast<uint32_t>(slot) << 19);
+}
+__device__ __forceinline__ int entry_item(uint32_t e) { return static_cast<int>(e & 0x3ffu); }
+__device__ __forceinline__ int entry_code(uint32_t e) { return static_cast<int>((e >> 10) & 0xffu); }
+__device__ __forceinline__ bool entry_inside(uint32_t e) { return ((e >> 18) & 1u) != 0; }
+__device__ __forceinline__ int entry_slot(uint32_t e) { return static_cast<int>((e >> 19) & 1u); }
+
+template <int V, int S>
 __global__ __launch_bounds__(kLutThreads) void pairwise_bwd_table_kernel(LutArgs a) {
+    constexpr int kK = 8;  // sorted positions per walk step
+    constexpr int kWaves = kLutThreads / kWave;
+    constexpr int nthr = kLutThreads;
+    constexpr int NG = nthr / S;  // row groups
     extern __shared__ __align__(16) unsigned char lds[];
-    float *slab = reinterpret_cast<float *>(lds);                // [rows][pitch] LUT chunk as f32
-    int *hist = reinterpret_cast<int *>(lds + a.hist_off);       // [waves][rows] counts, then bases
-    int *start = reinterpret_cast<int *>(lds + a.start_off);     // [rows + 1] bucket starts
-    uint32_t *sorted = reinterpret_cast<uint32_t *>(lds + a.sorted_off);  // [tile] item | nb << 16
+    int *hist = reinterpret_cast<int *>(lds + a.hist_off);                   // [R][waves] counts -> offsets
+    int *start = reinterpret_cast<int *>(lds + a.start_off);                 // [R + 1] bucket starts
+    uint32_t *sorted = reinterpret_cast<uint32_t *>(lds + a.sorted_off);    // [tile] packed entries
+    float *rowbuf = reinterpret_cast<float *>(lds + a.rowbuf_off);           // [R][o_chunk] gradient rows
+    float *part = reinterpret_cast<float *>(lds + a.part_off);               // [groups][2][o_chunk] split segments
+    float *tp = reinterpret_cast<float *>(lds + a.thr_off);                  // [waves][MAX_COMPARISONS]
+    int *wtot = reinterpret_cast<int *>(lds + a.wtot_off);                   // [waves] scan carries
+    uint32_t *sink = reinterpret_cast<uint32_t *>(wtot + kWaves);            // [64] prefetch sink
 
     const int t = blockIdx.x, chunk = blockIdx.y;
-    const int oc = a.o_chunk, pitch = a.pitch;
-    const int o0 = chunk * oc;
-    const int width = min(oc, a.out_f - o0);
-    const int tid = threadIdx.x, nthr = blockDim.x;
-    const int lane = tid & (kWave - 1), wave = tid / kWave, nwaves = nthr / kWave;
-    const int S = 1 << a.slices_log2;  // lanes per gradient row (one V-wide slice each)
-    const int R = a.rows;
+    const int oc = a.o_chunk, o0 = chunk * oc;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int R = a.rows, C = a.comps;
+    const bool thr = a.grad_thr != nullptr && chunk == 0;
     const uint64_t *rec_t = a.rec + static_cast<size_t>(t) * a.items;
-    float *dp_t = a.dpart ? a.dpart + (static_cast<size_t>(chunk) * a.tables + t) * a.items : nullptr;
+    const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.grad_out, a.g_bytes);
 
-    // stage the LUT slab [R x width] as f32
+    // first tile's record (the sort waits for it), then a slice of
+    // grad_output: the workgroups that share an XCD (the dispatcher deals
+    // workgroups to the 8 XCDs in turn) each touch one slice, one dword per
+    // 128-byte line, so the grad rows the walk gathers are L2 hits by then
+    uint64_t r_next = tid < a.items ? rec_t[tid] : 0ull;
+    const float *gu_t = a.gu + static_cast<size_t>(t) * a.items;
+    float gu_next = thr && tid < a.items ? gu_t[tid] : 0.f;
+    uint32_t pf = 0u;
     {
-        const T *src = static_cast<const T *>(a.lut) + static_cast<size_t>(t) * R * a.out_f + o0;
-        const int vpr = width / V;  // width is a multiple of V
-        for (int k = tid; k < R * vpr; k += nthr) {
-            const int r = k / vpr, j = k - r * vpr;
-            float v[V];
-            load_row<T, V>(src + static_cast<size_t>(r) * a.out_f + j * V, v);
-            store_f32<V>(slab + r * pitch + j * V, v);
-        }
+        const int nwg = gridDim.x * gridDim.y;
+        const int lin = blockIdx.y * gridDim.x + blockIdx.x;
+        const int share = (nwg - (lin & 7) + 7) >> 3;
+        const uint32_t slice = ((a.g_bytes + share - 1) / share + 127u) & ~127u;
+        const uint32_t off = tid * 128u;
+        if (off < slice) pf = __builtin_amdgcn_raw_buffer_load_b32(g_rsrc, (lin >> 3) * slice + off, 0, 0);
     }
-
-    // this thread's (row, slice) units: unit = row * S + slice
-    const int nunits = R * S;
-    float acc[kUnits][V];
-#pragma unroll
-    for (int p = 0; p < kUnits; ++p)
-#pragma unroll
-        for (int e = 0; e < V; ++e) acc[p][e] = 0.f;
+    for (int k = tid * 4; k < R * oc; k += nthr * 4) *reinterpret_cast<vec_t<float, 4> *>(rowbuf + k) = 0.f;
+    if (tid < kWaves * TROPNN_MAX_COMPARISONS) tp[tid] = 0.f;
 
     for (int tile0 = 0; tile0 < a.items; tile0 += nthr) {
-        // 1. this thread's item of the tile
-        const int b = tile0 + tid;
+        const int n_tile = min(nthr, a.items - tile0);
+        // per-lane values are recomputed per tile from an opaque copy of the
+        // thread id: hoisted out of the loop they would stay live across it
+        int tidl = tid;
+        __asm__ volatile("" : "+v"(tidl));
+        const int g = tidl / S, j = tidl % S;  // walker row group and its lane
+        const int col = j * V;
+        const bool col_ok = o0 + col < a.out_f;
+        const uint32_t gcol = static_cast<uint32_t>(o0 + col) * 4u;
+
+        // 1. this thread's item and code
+        const int b = tile0 + tidl;
         const bool valid = b < a.items;
-        const uint64_t r0 = valid ? rec_t[b] : 0ull;
+        const uint64_t r0 = r_next;
+        const float gu0 = gu_next;
         const int code = rec_code(r0) & (R - 1);  // masks keep a corrupt record in range
-        const int nb = (code ^ (1 << (rec_r(r0) & 15))) & (R - 1);
-        for (int k = tid; k < nwaves * R; k += nthr) hist[k] = 0;
-        // 2. rank among equal codes of the wave: intersect per-bit ballots
-        uint64_t same = __ballot(valid);
-        for (int c = 0; c < a.comps; ++c) {
-            const uint64_t bits = __ballot(valid && ((code >> c) & 1));
-            same &= ((code >> c) & 1) ? bits : ~bits;
+
+        // 2. one ballot per code bit: each item's rank among equal codes of
+        //    its wave, and lane l's count of codes l, l + 64, ... in the wave
+        const uint64_t vmask = __ballot(valid);
+        constexpr int kCodesPerLane = (1 << TROPNN_MAX_COMPARISONS) / kWave;
+        uint64_t same = vmask;
+        uint64_t cnt[kCodesPerLane];
+#pragma unroll
+        for (int i = 0; i < kCodesPerLane; ++i) cnt[i] = vmask;
+        for (int c = 0; c < C; ++c) {
+            const uint64_t bc = __ballot(valid && ((code >> c) & 1));
+            same &= ((code >> c) & 1) ? bc : ~bc;
+#pragma unroll
+            for (int i = 0; i < kCodesPerLane; ++i) cnt[i] &= (((lane + i * kWave) >> c) & 1) ? bc : ~bc;
         }
         const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
         const int rank = __popcll(same & below);
+#pragma unroll
+        for (int i = 0; i < kCodesPerLane; ++i)
+            if (lane + i * kWave < R) hist[(lane + i * kWave) * kWaves + wave] = __popcll(cnt[i]);
         __syncthreads();
-        if (valid && rank == 0) hist[wave * R + code] = __popcll(same);
-        __syncthreads();
-        // 3. bucket starts, then per-wave bases inside each bucket
-        for (int r = tid; r < R; r += nthr) {
-            int run = 0;
-            for (int w = 0; w < nwaves; ++w) {
-                const int h = hist[w * R + r];
-                hist[w * R + r] = run;
-                run += h;
+
+        // 3. bucket offsets: code k's count per wave -> per-wave offsets
+        //    inside the bucket, bucket totals -> exclusive scan over codes
+        int hw[kWaves];
+        int total = 0;
+        const bool scanner = tidl < ((R + kWave - 1) / kWave) * kWave;  // whole waves
+        if (scanner) {
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) hw[w] = tidl < R ? hist[tidl * kWaves + w] : 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const int h = hw[w];
+                hw[w] = total;
+                total += h;
             }
-            start[r] = run;  // bucket size for now
+        }
+        int incl = scanner ? wave_inclusive_scan(total) : 0;
+        if (R > kWave) {  // carry across the scanning waves
+            if (scanner && lane == kWave - 1) wtot[wave] = incl;
+            __syncthreads();
+            if (scanner)
+                for (int w = 0; w < wave; ++w) incl += wtot[w];
+        }
+        if (tidl < R) {
+            const int excl = incl - total;
+            start[tidl] = excl;
+            if (tidl == R - 1) start[R] = incl;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) hist[tidl * kWaves + w] = excl + hw[w];
         }
         __syncthreads();
-        if (wave == 0) wave_exclusive_scan(start, R, lane);
+
+        // 4. stable placement. Row group g walks sorted positions
+        //    [g Lr, g Lr + Lr); a bucket's segment in a range is either the
+        //    whole bucket (summed into its row) or a piece of a bucket split
+        //    across ranges (written to the range's slot 0 if the segment holds
+        //    the range's first position, else slot 1)
+        const int Lr = kK * ((n_tile + NG * kK - 1) / (NG * kK));
+        if (valid) {
+            const int pos = hist[code * kWaves + wave] + rank;
+            const int q0 = (pos / Lr) * Lr, q1 = min(q0 + Lr, n_tile);
+            const int kb = start[code], ke = start[code + 1];
+            sorted[pos] = pack_entry(tidl, code, kb >= q0 && ke <= q1, kb <= q0 ? 0 : 1);
+        }
         __syncthreads();
-        // 4. stable placement
-        if (valid) sorted[start[code] + hist[wave * R + code] + rank] = static_cast<uint32_t>(tid) | (nb << 16);
-        __syncthreads();
-        // 5. owned units walk their buckets
+        if (tile0 == 0) sink[lane] = pf;  // the prefetch's only use
+
+        // 5. walk: row group g takes sorted positions [p0, p1), kK per step.
+        //    Within a step the grad rows are summed along runs of equal codes
+        //    in registers; a run is written out when the next code differs,
+        //    and the run open at the end of a step carries into the next.
+        const int p0 = g * Lr, p1 = min(p0 + Lr, n_tile);
+        float acc[V];  // open run
 #pragma unroll
-        for (int p = 0; p < kUnits; ++p) {
-            const int unit = tid + p * nthr;
-            if (p * nthr >= nunits) break;  // block-uniform
-            const bool own = unit < nunits;
-            const int row = own ? unit >> a.slices_log2 : 0;
-            const int slice = unit & (S - 1);
-            const int col = slice * V;
-            const bool live = own && col < width;
-            const int kb = own ? start[row] : 0, ke = own ? start[row + 1] : 0;
-            float lrow[V];
-            load_f32<V>(slab + row * pitch + (live ? col : 0), lrow);
-            const float *gcol = a.grad_out + o0 + (live ? col : 0);
-            for (int k0 = kb; __ballot(k0 < ke) != 0; k0 += kBatch) {  // wave-uniform trip count
-                uint32_t ent[kBatch];
-                float g[kBatch][V];
+        for (int e = 0; e < V; ++e) acc[e] = 0.f;
+        uint32_t cur = 0;   // entry of the open run's last item
+        bool open = false;  // uniform in the row group
+        auto dest = [&](uint32_t e) -> float * {
+            return entry_inside(e) ? rowbuf + entry_code(e) * oc + col : part + (g * 2 + entry_slot(e)) * oc + col;
+        };
+        for (int k0 = p0; __ballot(k0 < p1) != 0; k0 += kK) {  // wave-uniform trip count
+            uint32_t ent[kK];
+            float gv[kK][V];
 #pragma unroll
-                for (int u = 0; u < kBatch; ++u) {
-                    const int k = k0 + u;
-                    ent[u] = (k < ke) ? sorted[k] : 0u;
-                    const int item = tile0 + static_cast<int>(ent[u] & 0xffffu);
-                    load_f32<V>(gcol + static_cast<size_t>(item < a.items ? item : 0) * a.out_f, g[u]);
-                }
+            for (int u = 0; u < kK; ++u) {
+                const bool live = k0 + u < p1;
+                ent[u] = live ? sorted[k0 + u] : 0u;
+                const uint32_t item = tile0 + entry_item(ent[u]);
+                buffer_row<float, V>(g_rsrc, live && col_ok ? item * static_cast<uint32_t>(a.out_f) * 4u + gcol
+                                                            : kOutOfRange, 0, gv[u]);
+            }
+            // run sums in place: gv[u] += (previous item continues the run) ? gv[u-1] : 0
 #pragma unroll
-                for (int u = 0; u < kBatch; ++u) {
-                    const bool ok = (k0 + u < ke) && live;
-                    const int nbr = static_cast<int>(ent[u] >> 16);
-                    float d = 0.f;
-                    if (ok) {
-                        float ln[V];
-                        load_f32<V>(slab + nbr * pitch + col, ln);
+            for (int u = 0; u < kK; ++u) {
+                const bool live = k0 + u < p1;
+                const bool cont = live && (u == 0 ? open && entry_code(cur) == entry_code(ent[u])
+                                                  : entry_code(ent[u - 1]) == entry_code(ent[u]));
 #pragma unroll
-                        for (int e = 0; e < V; ++e) {
-                            const float ge = g[u][e] * a.scale;
-                            acc[p][e] += ge;
-                            d += ge * (ln[e] - lrow[e]);
-                        }
-                    }
-                    d = group_sum(d, S);
-                    if (dp_t != nullptr && (k0 + u < ke) && own && slice == 0)
-                        dp_t[tile0 + static_cast<int>(ent[u] & 0xffffu)] = d;
+                for (int e = 0; e < V; ++e) gv[u][e] = cont ? (u == 0 ? acc[e] : gv[u - 1][e]) + gv[u][e] : gv[u][e];
+            }
+            // the open run ends before item 0 if item 0 starts a new run
+            if (open && k0 < p1 && entry_code(cur) != entry_code(ent[0])) {
+                float *dst = dest(cur);
+#pragma unroll
+                for (int e = 0; e < V; ++e) dst[e] = entry_inside(cur) ? dst[e] + acc[e] : acc[e];
+            }
+            // runs that end inside the step
+#pragma unroll
+            for (int u = 0; u + 1 < kK; ++u) {
+                if (k0 + u + 1 < p1 && entry_code(ent[u]) != entry_code(ent[u + 1])) {
+                    float *dst = dest(ent[u]);
+#pragma unroll
+                    for (int e = 0; e < V; ++e) dst[e] = entry_inside(ent[u]) ? dst[e] + gv[u][e] : gv[u][e];
                 }
             }
+            // the last live item's run stays open
+#pragma unroll
+            for (int u = 0; u < kK; ++u) {
+                if (k0 + u < p1 && (u + 1 == kK || k0 + u + 1 >= p1)) {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) acc[e] = gv[u][e];
+                    cur = ent[u];
+                    open = true;
+                }
+            }
+        }
+        if (open) {
+            float *dst = dest(cur);
+#pragma unroll
+            for (int e = 0; e < V; ++e) dst[e] = entry_inside(cur) ? dst[e] + acc[e] : acc[e];
+        }
+        // threshold gradient: -gu at the item's min-margin comparison, summed
+        // per wave (fixed tree) into the wave's slots; lane 8c ends with the
+        // wave's sum for comparison c
+        if (thr) {
+            const float gu = valid ? gu0 : 0.f;
+            const int rr = rec_r(r0) & 7;
+            float tv[TROPNN_MAX_COMPARISONS];
+#pragma unroll
+            for (int c = 0; c < TROPNN_MAX_COMPARISONS; ++c) tv[c] = rr == c ? -gu : 0.f;
+            const float tot = reduce_scatter<kWave, TROPNN_MAX_COMPARISONS>(tv, lane);
+            const int c = lane >> 3;
+            if ((lane & 7) == 0 && c < C) tp[wave * TROPNN_MAX_COMPARISONS + c] += tot;
+        }
+        __syncthreads();
+
+        // 6. buckets split across ranges: their segments, in range order
+        for (int unit = tidl; unit < R * S; unit += nthr) {
+            const int k = unit / S, c0 = (unit % S) * V;
+            const int kb = start[k], ke = start[k + 1];
+            if (ke > kb && kb / Lr != (ke - 1) / Lr) {
+                const int glo = kb / Lr, ghi = (ke - 1) / Lr;
+                float sum[V];
+#pragma unroll
+                for (int e = 0; e < V; ++e) sum[e] = 0.f;
+                for (int gg = glo; gg <= ghi; ++gg) {
+                    const float *src = part + (gg * 2 + (gg == glo && kb != glo * Lr ? 1 : 0)) * oc + c0;
+#pragma unroll
+                    for (int e = 0; e < V; ++e) sum[e] += src[e];
+                }
+                float *dst = rowbuf + k * oc + c0;
+#pragma unroll
+                for (int e = 0; e < V; ++e) dst[e] += sum[e];
+            }
+        }
+        if (tile0 + nthr < a.items) {
+            const bool nv = tile0 + nthr + tidl < a.items;
+            r_next = nv ? rec_t[tile0 + nthr + tidl] : 0ull;
+            gu_next = thr && nv ? gu_t[tile0 + nthr + tidl] : 0.f;
         }
         __syncthreads();  // LDS is reused by the next tile
     }
 
-    // 6. each unit's gradient slice is written once
+    // 7. gradient rows, scaled, written once
     if (a.grad_lut != nullptr) {
         float *dst = a.grad_lut + static_cast<size_t>(t) * R * a.out_f + o0;
+        for (int unit = tid; unit < R * S; unit += nthr) {
+            const int k = unit / S, c0 = (unit % S) * V;
+            if (o0 + c0 < a.out_f) {
+                float y[V];
 #pragma unroll
-        for (int p = 0; p < kUnits; ++p) {
-            const int unit = tid + p * nthr;
-            if (unit >= nunits) break;
-            const int row = unit >> a.slices_log2, col = (unit & (S - 1)) * V;
-            if (col < width) store_f32<V>(dst + static_cast<size_t>(row) * a.out_f + col, acc[p]);
-        }
-    }
-}
-
-struct InArgs {
-    const uint64_t *rec;
-    const float *dpart;
-    const int32_t *index_offsets;  // [in_f + 1]
-    const int32_t *index_entries;  // (t << 4) | (c << 1) | side
-    float *grad_x;
-    float *grad_thr;
-    int items, in_f, tables, comps, chunks;
-    int items_per_wg, role_a_blocks;
-};
-
-// D[b,t]: the chunk partial dots summed in chunk order
-__device__ __forceinline__ float dot_of(const InArgs &a, int t, int b) {
-    const size_t stride = static_cast<size_t>(a.tables) * a.items;
-    const float *p = a.dpart + static_cast<size_t>(t) * a.items + b;
-    float dsum = p[0];
-    for (int k = 1; k < a.chunks; ++k) dsum += p[k * stride];
-    return dsum;
-}
-
-__global__ __launch_bounds__(kInThreads) void pairwise_bwd_input_kernel(InArgs a) {
-    extern __shared__ __align__(16) unsigned char lds[];
-    const int tid = threadIdx.x, nthr = blockDim.x;
-    if (static_cast<int>(blockIdx.x) < a.role_a_blocks) {
-        // role A: input gradient rows of items_per_wg items
-        const int item0 = blockIdx.x * a.items_per_wg;
-        const int n_items = min(a.items_per_wg, a.items - item0);
-        const int npairs = n_items * a.tables;
-        const int nent = 2 * a.tables * a.comps;
-        int32_t *off_s = reinterpret_cast<int32_t *>(lds);            // [in_f + 1]
-        int32_t *ent_s = off_s + (a.in_f + 1);                        // [2 T C]
-        float *gu_s = reinterpret_cast<float *>(ent_s + nent);        // [n_items][T]
-        uint8_t *r_s = reinterpret_cast<uint8_t *>(gu_s + a.items_per_wg * a.tables);  // [n_items][T]
-        for (int k = tid; k <= a.in_f; k += nthr) off_s[k] = a.index_offsets[k];
-        for (int k = tid; k < nent; k += nthr) ent_s[k] = a.index_entries[k];
-        for (int p0 = tid; p0 < npairs; p0 += kPairs * nthr) {
-            uint64_t rr[kPairs];
-            float dsum[kPairs];
-#pragma unroll
-            for (int q = 0; q < kPairs; ++q) {
-                int p = p0 + q * nthr;
-                p = p < npairs ? p : npairs - 1;
-                const int t = p / n_items, b = item0 + (p - t * n_items);
-                rr[q] = a.rec[static_cast<size_t>(t) * a.items + b];
-                dsum[q] = dot_of(a, t, b);
-            }
-#pragma unroll
-            for (int q = 0; q < kPairs; ++q) {
-                const int p = p0 + q * nthr;
-                if (p < npairs) {
-                    const int t = p / n_items, i = p - t * n_items;
-                    gu_s[i * a.tables + t] = dsum[q] * fast_sigmoid_odd(rec_u(rr[q]));
-                    r_s[i * a.tables + t] = static_cast<uint8_t>(rec_r(rr[q]));
-                }
-            }
-        }
-        __syncthreads();
-        // one thread per (item, feature): walk the feature's anchor entries in order
-        for (int k = tid; k < n_items * a.in_f; k += nthr) {
-            const int i = k / a.in_f, f = k - i * a.in_f;
-            const int e0 = off_s[f], e1 = off_s[f + 1];
-            float g = 0.f;
-            for (int e = e0; e < e1; ++e) {
-                const int ent = ent_s[e];
-                const int t = ent >> 4, c = (ent >> 1) & 7;
-                if (r_s[i * a.tables + t] == c) {
-                    const float gu = gu_s[i * a.tables + t];
-                    g = (ent & 1) ? g - gu : g + gu;
-                }
-            }
-            a.grad_x[static_cast<size_t>(item0 + i) * a.in_f + f] = g;
-        }
-        return;
-    }
-    // role B: threshold gradient of one table, fixed-order reduction
-    const int t = blockIdx.x - a.role_a_blocks;
-    float acc[TROPNN_MAX_COMPARISONS];
-#pragma unroll
-    for (int c = 0; c < TROPNN_MAX_COMPARISONS; ++c) acc[c] = 0.f;
-    const uint64_t *rec_t = a.rec + static_cast<size_t>(t) * a.items;
-    for (int b0 = tid; b0 < a.items; b0 += kPairs * nthr) {
-        uint64_t rr[kPairs];
-        float dsum[kPairs];
-#pragma unroll
-        for (int q = 0; q < kPairs; ++q) {
-            int b = b0 + q * nthr;
-            b = b < a.items ? b : a.items - 1;
-            rr[q] = rec_t[b];
-            dsum[q] = dot_of(a, t, b);
-        }
-#pragma unroll
-        for (int q = 0; q < kPairs; ++q) {
-            if (b0 + q * nthr < a.items) {
-                const float gu = dsum[q] * fast_sigmoid_odd(rec_u(rr[q]));
-                const int r = rec_r(rr[q]);
-#pragma unroll
-                for (int c = 0; c < TROPNN_MAX_COMPARISONS; ++c)
-                    if (c == r) acc[c] -= gu;
+                for (int e = 0; e < V; ++e) y[e] = rowbuf[k * oc + c0 + e] * a.scale;
+                store_f32<V>(dst + static_cast<size_t>(k) * a.out_f + c0, y);
             }
         }
     }
-    float *part = reinterpret_cast<float *>(lds);  // [waves][MAX_COMPARISONS]
-    const int lane = tid & (kWave - 1), wave = tid / kWave, nwaves = nthr / kWave;
-#pragma unroll
-    for (int c = 0; c < TROPNN_MAX_COMPARISONS; ++c) {
-        const float v = group_sum(acc[c], kWave);
-        if (lane == 0) part[wave * TROPNN_MAX_COMPARISONS + c] = v;
-    }
-    __syncthreads();
-    if (tid < a.comps) {
-        float sum = part[tid];
-        for (int w = 1; w < nwaves; ++w) sum += part[w * TROPNN_MAX_COMPARISONS + tid];
-        a.grad_thr[t * a.comps + tid] = sum;
+    // 8. threshold gradient of this table: the waves' sums in wave order
+    if (thr && tid < C) {
+        float sum = tp[tid];
+        for (int w = 1; w < kWaves; ++w) sum += tp[w * TROPNN_MAX_COMPARISONS + tid];
+        a.grad_thr[t * C + tid] = sum;
     }
 }
 
 // Inverse anchor index: for every input feature f, the entries
-// (t << 4) | (c << 1) | side of the anchors[t][c][side] equal to f, in
-// increasing (t, c, side) order. One thread per feature scans the anchors,
-// so the order is fixed.
+// ((t * C + c) << 1) | side of the anchors[t][c][side] equal to f, in
+// increasing order. One thread per feature scans the anchors, so the order is
+// fixed.
 __global__ __launch_bounds__(256) void anchor_index_kernel(const int64_t *anchors, int in_f, int tables, int comps,
                                                           int32_t *offsets, int32_t *entries) {
     extern __shared__ __align__(16) unsigned char lds[];
@@ -346,25 +574,61 @@ __global__ __launch_bounds__(256) void anchor_index_kernel(const int64_t *anchor
     for (int f = threadIdx.x; f < in_f; f += blockDim.x) {
         int pos = count[f];
         for (int k = 0; k < n; ++k)
-            if (anchors[k] == f) entries[pos++] = (k >> 1) / comps << 4 | ((k >> 1) % comps) << 1 | (k & 1);
+            if (anchors[k] == f) entries[pos++] = k;  // k = ((t * C + c) << 1) | side
     }
 }
 
-template <typename T, int V>
-hipError_t launch_table(const LutArgs &args, const BackwardPlan &p, hipStream_t stream) {
+// Kernels that may need more than the default 64 KB of dynamic LDS opt in
+// once per process.
+template <typename K>
+hipError_t allow_lds(K kernel, int bytes) {
+    static int allowed = 0;  // one flag per kernel instantiation
+    if (bytes <= 64 * 1024 || bytes <= allowed) return hipSuccess;
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess) allowed = bytes;
+    return e;
+}
+
+template <int V, int S>
+hipError_t launch_table_vs(const LutArgs &args, const BackwardPlan &p, hipStream_t stream) {
+    auto kernel = pairwise_bwd_table_kernel<V, S>;
+    if (hipError_t e = allow_lds(kernel, p.lut_lds_bytes); e != hipSuccess) return e;
     const ArmedEvents ev = take_armed_events(TROPNN_KERNEL_BACKWARD_TABLE);
     record_event(ev.start, stream);
-    hipLaunchKernelGGL((pairwise_bwd_table_kernel<T, V>), dim3(args.tables, p.o_chunks), dim3(p.lut_threads),
-                       p.lut_lds_bytes, stream, args);
+    hipLaunchKernelGGL(kernel, dim3(args.tables, p.o_chunks), dim3(p.lut_threads), p.lut_lds_bytes, stream, args);
     const hipError_t e = hipGetLastError();
     record_event(ev.stop, stream);
     return e;
 }
 
-int ilog2(int v) {
-    int r = 0;
-    while ((1 << r) < v) ++r;
-    return r;
+template <int V>
+hipError_t launch_table_v(const LutArgs &args, const BackwardPlan &p, hipStream_t stream) {
+    switch (p.slices) {
+        case 32: return launch_table_vs<V, 32>(args, p, stream);
+        case 16: return launch_table_vs<V, 16>(args, p, stream);
+        case 8: return launch_table_vs<V, 8>(args, p, stream);
+        default: return launch_table_vs<V, 4>(args, p, stream);
+    }
+}
+
+hipError_t launch_table(const LutArgs &args, const BackwardPlan &p, hipStream_t stream) {
+    switch (p.vec) {
+        case 4: return launch_table_v<4>(args, p, stream);
+        case 2: return launch_table_v<2>(args, p, stream);
+        default: return launch_table_v<1>(args, p, stream);
+    }
+}
+
+template <typename T, int N>
+hipError_t launch_item_typed(const ItemArgs &args, const BackwardPlan &p, hipStream_t stream) {
+    const ArmedEvents ev = take_armed_events(TROPNN_KERNEL_BACKWARD_ITEM);
+    record_event(ev.start, stream);
+    hipLaunchKernelGGL((pairwise_bwd_item_kernel<T, N>), dim3(args.items), dim3(p.item_threads), p.item_lds_bytes,
+                       stream, args);
+    const hipError_t e = hipGetLastError();
+    record_event(ev.stop, stream);
+    return e;
 }
 
 __global__ void fill_zero_kernel(float *p, size_t n) {
@@ -373,9 +637,37 @@ __global__ void fill_zero_kernel(float *p, size_t n) {
         p[k] = 0.f;
 }
 
-int table_lds_bytes(int rows, int pitch, int threads) {
-    const int waves = threads / kWave;
-    return rows * pitch * 4 + waves * rows * 4 + (rows + 1) * 4 + threads * 4 + 64;
+// LDS bytes of a table workgroup for a given split (see the kernel's layout)
+int table_lds(const Dims &d, int slices, int vec, BackwardPlan *p) {
+    const int waves = kLutThreads / kWave;
+    const int oc = slices * vec;
+    int off = 0;
+    const int hist_off = off;
+    off += waves * d.rows * 4;
+    const int start_off = off;
+    off += (d.rows + 1) * 4;
+    off = (off + 15) & ~15;
+    const int sorted_off = off;
+    off += kLutThreads * 4;
+    const int rowbuf_off = off;
+    off += d.rows * oc * 4;
+    const int part_off = off;
+    off += (kLutThreads / slices) * 2 * oc * 4;
+    const int thr_off = off;
+    off += waves * TROPNN_MAX_COMPARISONS * 4;
+    const int wtot_off = off;
+    off += waves * 4 + kWave * 4;  // scan carries, prefetch sink
+    if (p != nullptr) {
+        p->hist_off = hist_off;
+        p->start_off = start_off;
+        p->sorted_off = sorted_off;
+        p->rowbuf_off = rowbuf_off;
+        p->part_off = part_off;
+        p->thr_off = thr_off;
+        p->wtot_off = wtot_off;
+        p->lut_lds_bytes = off;
+    }
+    return off;
 }
 
 }  // namespace
@@ -398,32 +690,43 @@ hipError_t launch_anchor_index(const int64_t *anchors, int in_f, int tables, int
 BackwardPlan plan_backward(const Dims &d) {
     BackwardPlan p{};
     const int esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
-    // one vector width for both the f32 grad rows and the LUT rows
+    // table kernel: V columns per lane (a divisor of the row, at most 4), S
+    // lanes per row group: the smallest of 4, 8, 16, 32 whose S * V columns
+    // span the row, else 32; narrower while the LDS exceeds 160 KB
     p.vec = 4;
-    while (p.vec > 1 && (d.out_f % p.vec != 0 || (p.vec * esize) > 16)) p.vec >>= 1;
+    while (p.vec > 1 && d.out_f % p.vec != 0) p.vec >>= 1;
+    p.slices = 4;
+    while (p.slices < 32 && p.slices * p.vec < d.out_f) p.slices <<= 1;
+    while (table_lds(d, p.slices, p.vec, nullptr) > 160 * 1024 && (p.slices > 4 || p.vec > 1)) {
+        if (p.slices > 4)
+            p.slices >>= 1;
+        else
+            p.vec >>= 1;
+    }
+    table_lds(d, p.slices, p.vec, &p);
+    p.o_chunk = p.slices * p.vec;
+    p.o_chunks = (d.out_f + p.o_chunk - 1) / p.o_chunk;
     p.lut_threads = kLutThreads;
-    // widest chunk (<= 64 lanes x vec columns) whose slab + sort buffers fit
-    // 64 KB of LDS and whose (row, slice) units fit kUnits per thread
-    int oc = p.vec;
-    while (oc * 2 <= kWave * p.vec && oc * 2 <= ((d.out_f + p.vec - 1) / p.vec) * p.vec * 2 &&
-           table_lds_bytes(d.rows, oc * 2 + 4, p.lut_threads) <= 64 * 1024 &&
-           d.rows * ((oc * 2) / p.vec) <= kUnits * p.lut_threads)
-        oc *= 2;
-    if (oc > d.out_f) oc = ((d.out_f + p.vec - 1) / p.vec) * p.vec;
-    p.o_chunk = oc;
-    p.o_chunks = (d.out_f + oc - 1) / oc;
-    p.pitch = ((oc + 3) & ~3) + 4;  // +4 floats: rows start in different LDS banks
-    p.slices_log2 = ilog2((oc + p.vec - 1) / p.vec);
-    p.lut_lds_bytes = table_lds_bytes(d.rows, p.pitch, p.lut_threads);
-    const int index_lds = (d.in_f + 1) * 4 + 2 * d.tables * d.comps * 4;
-    int ipw = 4;
-    while (ipw > 1 && index_lds + static_cast<long long>(ipw) * d.tables * 5 > 64 * 1024) ipw >>= 1;
-    p.in_items_per_wg = ipw;
-    p.in_threads = kInThreads;
-    const int role_a_lds = index_lds + ipw * d.tables * 5 + 16;
-    const int role_b_lds = (kInThreads / kWave) * TROPNN_MAX_COMPARISONS * 4;
-    p.in_lds_bytes = role_a_lds > role_b_lds ? role_a_lds : role_b_lds;
-    p.workspace_bytes = static_cast<size_t>(p.o_chunks) * d.tables * d.items * sizeof(float);
+    p.workspace_bytes = static_cast<size_t>(d.tables) * d.items * sizeof(float);
+
+    // item kernel: N elements per lane as in the forward (the smallest power
+    // of two whose 64-lane tile spans the row, 16 bytes at most, dividing the
+    // row), waves of at most 16 tables, ~4096 waves in flight, at most 16
+    // waves (so at most 256 tables)
+    p.item_vec = 1;
+    while (p.item_vec * esize < 16 && p.item_vec * kWave < d.out_f) p.item_vec <<= 1;
+    while (p.item_vec > 1 && d.out_f % p.item_vec != 0) p.item_vec >>= 1;
+    p.item_o_tiles = (d.out_f + kWave * p.item_vec - 1) / (kWave * p.item_vec);
+    const int loaded = item_wave_tables(esize, p.item_vec);
+    int w = (d.tables + loaded - 1) / loaded;
+    const long long want = d.items > 0 ? (4096 + d.items - 1) / d.items : 16;
+    if (want > w) w = static_cast<int>(want < 16 ? want : 16);
+    if (w > 16) w = 16;  // more tables: each wave loops over blocks
+    if (w > d.tables) w = d.tables;
+    p.item_per_wave = (d.tables + w - 1) / w;
+    p.item_waves = (d.tables + p.item_per_wave - 1) / p.item_per_wave;
+    p.item_threads = p.item_waves * kWave;
+    p.item_lds_bytes = (d.tables * d.comps + d.in_f + 1 + 2 * d.tables * d.comps) * 4;
     return p;
 }
 
@@ -431,66 +734,71 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
                            const tropnn_route_record *rec, const int32_t *index_offsets,
                            const int32_t *index_entries, float scale, float *grad_x, float *grad_thr,
                            float *grad_lut, float *workspace, hipStream_t stream) {
-    const bool need_dots = grad_x != nullptr || grad_thr != nullptr;
     const uint64_t *rec64 = reinterpret_cast<const uint64_t *>(rec);
-    if (grad_lut != nullptr || need_dots) {
-        LutArgs a{};
+    const int esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
+    const uint32_t g_bytes = static_cast<uint32_t>(static_cast<size_t>(d.items) * d.out_f * 4);
+    if (grad_x != nullptr || grad_thr != nullptr) {
+        ItemArgs a{};
         a.grad_out = grad_out;
         a.lut = lut;
         a.rec = rec64;
+        a.index_offsets = index_offsets;
+        a.index_entries = index_entries;
         a.scale = scale;
-        a.grad_lut = grad_lut;
-        a.dpart = need_dots ? workspace : nullptr;
+        a.grad_x = grad_x;
+        a.gu = grad_thr != nullptr ? workspace : nullptr;
+        a.lut_bytes = static_cast<uint32_t>(static_cast<size_t>(d.tables) * d.rows * d.out_f * esize);
+        a.g_bytes = g_bytes;
         a.items = d.items;
+        a.in_f = d.in_f;
         a.out_f = d.out_f;
         a.tables = d.tables;
         a.comps = d.comps;
         a.rows = d.rows;
-        a.o_chunk = p.o_chunk;
-        a.pitch = p.pitch;
-        a.slices_log2 = p.slices_log2;
-        const int waves = p.lut_threads / kWave;
-        a.hist_off = d.rows * p.pitch * 4;
-        a.start_off = a.hist_off + waves * d.rows * 4;
-        a.sorted_off = (a.start_off + (d.rows + 1) * 4 + 15) & ~15;
+        a.row_bytes = d.out_f * esize;
+        a.table_bytes = d.rows * d.out_f * esize;
+        a.per_wave = p.item_per_wave;
+        a.o_tiles = p.item_o_tiles;
         hipError_t e;
         if (d.lut_dtype == TROPNN_LUT_F16) {
-            switch (p.vec) {
-                case 4: e = launch_table<_Float16, 4>(a, p, stream); break;
-                case 2: e = launch_table<_Float16, 2>(a, p, stream); break;
-                default: e = launch_table<_Float16, 1>(a, p, stream); break;
+            switch (p.item_vec) {
+                case 8: e = launch_item_typed<_Float16, 8>(a, p, stream); break;
+                case 4: e = launch_item_typed<_Float16, 4>(a, p, stream); break;
+                case 2: e = launch_item_typed<_Float16, 2>(a, p, stream); break;
+                default: e = launch_item_typed<_Float16, 1>(a, p, stream); break;
             }
         } else {
-            switch (p.vec) {
-                case 4: e = launch_table<float, 4>(a, p, stream); break;
-                case 2: e = launch_table<float, 2>(a, p, stream); break;
-                default: e = launch_table<float, 1>(a, p, stream); break;
+            switch (p.item_vec) {
+                case 4: e = launch_item_typed<float, 4>(a, p, stream); break;
+                case 2: e = launch_item_typed<float, 2>(a, p, stream); break;
+                default: e = launch_item_typed<float, 1>(a, p, stream); break;
             }
         }
         if (e != hipSuccess) return e;
     }
-    if (!need_dots) return hipSuccess;
-    InArgs b{};
+    if (grad_lut == nullptr && grad_thr == nullptr) return hipSuccess;
+    LutArgs b{};
+    b.grad_out = grad_out;
     b.rec = rec64;
-    b.dpart = workspace;
-    b.index_offsets = index_offsets;
-    b.index_entries = index_entries;
-    b.grad_x = grad_x;
+    b.gu = workspace;
+    b.scale = scale;
+    b.grad_lut = grad_lut;
     b.grad_thr = grad_thr;
+    b.g_bytes = g_bytes;
     b.items = d.items;
-    b.in_f = d.in_f;
+    b.out_f = d.out_f;
     b.tables = d.tables;
     b.comps = d.comps;
-    b.chunks = p.o_chunks;
-    b.items_per_wg = p.in_items_per_wg;
-    b.role_a_blocks = grad_x != nullptr ? (d.items + p.in_items_per_wg - 1) / p.in_items_per_wg : 0;
-    const int blocks = b.role_a_blocks + (grad_thr != nullptr ? d.tables : 0);
-    const ArmedEvents ev = take_armed_events(TROPNN_KERNEL_BACKWARD_INPUT);
-    record_event(ev.start, stream);
-    hipLaunchKernelGGL(pairwise_bwd_input_kernel, dim3(blocks), dim3(p.in_threads), p.in_lds_bytes, stream, b);
-    const hipError_t e = hipGetLastError();
-    record_event(ev.stop, stream);
-    return e;
+    b.rows = d.rows;
+    b.o_chunk = p.o_chunk;
+    b.hist_off = p.hist_off;
+    b.start_off = p.start_off;
+    b.sorted_off = p.sorted_off;
+    b.rowbuf_off = p.rowbuf_off;
+    b.part_off = p.part_off;
+    b.thr_off = p.thr_off;
+    b.wtot_off = p.wtot_off;
+    return launch_table(b, p, stream);
 }
 
 }  // namespace tropnn

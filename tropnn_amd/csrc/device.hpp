@@ -96,6 +96,62 @@ __device__ __forceinline__ float fast_sigmoid_odd(float u) {
     return num / den;
 }
 
+// Buffer-resource access (raw buffers, 32-bit offsets). An offset at or past
+// the resource's byte range reads as zero, so masked lanes just pass
+// kOutOfRange instead of branching.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+// N elements of T (f32 or f16) per lane at byte offset voff + soff (soff
+// wave-uniform), widened to f32. The loaded words are reinterpreted as whole
+// vectors, never element by element.
+template <typename T, int N>
+__device__ __forceinline__ void buffer_row(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, int soff, float (&v)[N]) {
+    constexpr int kBytes = N * static_cast<int>(sizeof(T));
+    if constexpr (kBytes == 2) {
+        const uint16_t w = __builtin_amdgcn_raw_buffer_load_b16(rsrc, voff, soff, 0);
+        v[0] = static_cast<float>(__builtin_bit_cast(_Float16, w));
+    } else if constexpr (kBytes == 4) {
+        const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff, soff, 0);
+        if constexpr (N == 1) {
+            v[0] = __builtin_bit_cast(float, w);
+        } else {
+            const vec_t<_Float16, 2> h = __builtin_bit_cast(vec_t<_Float16, 2>, w);
+            v[0] = static_cast<float>(h[0]);
+            v[1] = static_cast<float>(h[1]);
+        }
+    } else if constexpr (kBytes == 8) {
+        const auto w = __builtin_amdgcn_raw_buffer_load_b64(rsrc, voff, soff, 0);
+        if constexpr (N == 2) {
+            const vec_t<float, 2> f = __builtin_bit_cast(vec_t<float, 2>, w);
+            v[0] = f[0];
+            v[1] = f[1];
+        } else {
+            const vec_t<_Float16, 4> h = __builtin_bit_cast(vec_t<_Float16, 4>, w);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = static_cast<float>(h[e]);
+        }
+    } else {
+        static_assert(kBytes % 16 == 0, "row loads are 2, 4, 8 or a multiple of 16 bytes per lane");
+#pragma unroll
+        for (int q = 0; q < kBytes / 16; ++q) {
+            const auto w = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff + 16u * q, soff, 0);
+            if constexpr (sizeof(T) == 4) {
+                const vec_t<float, 4> f = __builtin_bit_cast(vec_t<float, 4>, w);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[4 * q + e] = f[e];
+            } else {
+                const vec_t<_Float16, 8> h = __builtin_bit_cast(vec_t<_Float16, 8>, w);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[8 * q + e] = static_cast<float>(h[e]);
+            }
+        }
+    }
+}
+
 // Clamp an anchor into [0, n) so a corrupt anchor can never address memory
 // outside the staged input row; the host validates anchors before launch.
 __device__ __forceinline__ int clamp_index(int64_t a, int n) {

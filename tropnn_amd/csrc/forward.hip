@@ -7,22 +7,28 @@
 //   scale   layers/base.py:76-77
 //   min-margin selection saved for the backward: layers/pairwise.py:138-140
 //
-// Workgroup = items_per_wg items x one output tile. The kernel is latency
-// bound at small batch, so every phase issues all of its independent global
-// loads before it waits:
-//   1. each wave loads the anchors and thresholds of its first route ballots
-//      while the workgroup stages the items' input rows in LDS (one round trip);
-//   2. route: one wave ballot evaluates 64 / P tables (P lanes per table, one
-//      comparison per lane, P = next power of two >= C); P-bit fields of the
-//      ballot mask are the LUT row codes, written to LDS. Training also
-//      reduces argmin |margin| inside each P-lane group and writes the route
-//      record; the debug path writes int64 codes and f32 margins;
-//   3. gather: lanes cover the output tile with 16-byte row loads (float4 or
-//      8 x f16); the 64 / lanes_per_row sub-groups of a wave and the
-//      waves_per_item waves of an item take disjoint strided sets of tables,
-//      issuing up to 16 row loads per lane before the first add; partial sums
-//      are combined by a lane butterfly and, across waves, through LDS in a
-//      fixed order, then scaled and stored.
+// Workgroup = one item x one output tile of 64 * N columns; its W waves take
+// disjoint contiguous blocks of tables. The kernel is latency bound at the
+// batch sizes of interest, so each wave keeps its instruction count small and
+// issues every independent load before it waits:
+//   1. each wave loads the comparators of its first ballots while the
+//      workgroup stages the item's input row in LDS (one round trip);
+//   2. route: one wave ballot evaluates 64 / P of the wave's tables (P lanes
+//      per table, one comparison per lane, P = next power of two >= C); the
+//      P-bit fields of the ballot mask are the LUT row codes, which the table's
+//      first lane writes to the wave's own LDS code list. Training also picks
+//      argmin |margin| inside each P-lane group with DPP moves on a 64-bit key
+//      and the winning lane writes the route record; the debug path writes
+//      int64 codes and f32 margins;
+//   3. gather: the wave reads its codes back 16 at a time (one broadcast LDS
+//      read), moves them to scalar registers, and loads each table's row with
+//      one buffer load whose row offset is a scalar: lane l reads columns
+//      [l N, l N + N) of the tile. Lanes past the last column get an offset
+//      beyond the buffer range, which the buffer unit answers with zeros, so
+//      the loop carries no masks. All of a chunk's row loads are in flight
+//      before the first add;
+//   4. the waves' partial rows are summed through LDS in wave order, scaled
+//      and stored by wave 0.
 #include "device.hpp"
 #include "launch.hpp"
 
@@ -36,210 +42,217 @@ struct FwdArgs {
     const void *lut;
     float scale;
     float *out;
-    tropnn_route_record *rec;
+    uint64_t *rec;
     int64_t *indices;
     float *margins;
-    int items, in_f, out_f, tables, comps, rows;
-    int lpt_log2, lpr_log2, o_tile, items_per_wg, waves_per_item;
+    uint32_t lut_bytes;  // buffer range of the LUT (<= 2^31)
+    int items, in_f, out_f, tables, comps;
+    int row_bytes, table_bytes;
+    int lpt_log2, per_wave, codes_pitch;
     int codes_off, red_off;
 };
 
-constexpr int kGather = 16;   // row loads in flight per lane
-constexpr int kBallots = 4;   // ballots whose parameters a wave prefetches
+constexpr int kBallots = 4;             // ballots whose comparators a wave prefetches
 
 // One lane's comparator: anchors (clamped) and threshold of (table, comparison).
+// Padding lanes load table 0 / comparison 0 so that the loads are issued
+// unconditionally; `valid` masks them out.
 struct Comparator {
     int a, b;
     float thr;
     bool valid;
 };
 
-__device__ __forceinline__ Comparator load_comparator(const FwdArgs &p, int t, int c) {
-    Comparator q{0, 0, 0.f, false};
-    if (t < p.tables && c < p.comps) {
-        const int64_t *ap = p.anchors + (static_cast<size_t>(t) * p.comps + c) * 2;
-        q.a = clamp_index(ap[0], p.in_f);
-        q.b = clamp_index(ap[1], p.in_f);
-        q.thr = p.thr[t * p.comps + c];
-        q.valid = true;
-    }
+__device__ __forceinline__ Comparator load_comparator(const FwdArgs &p, int t, int t_end, int c) {
+    Comparator q;
+    q.valid = t < t_end && c < p.comps;
+    const size_t k = q.valid ? static_cast<size_t>(t) * p.comps + c : 0;
+    q.a = clamp_index(p.anchors[2 * k], p.in_f);
+    q.b = clamp_index(p.anchors[2 * k + 1], p.in_f);
+    q.thr = p.thr[k];
     return q;
 }
 
-template <bool TRAIN, bool DEBUG>
-__device__ __forceinline__ void route_ballot(const FwdArgs &p, const float *xs, uint16_t *codes, const Comparator &q,
-                                             int t, int c, int slot, int lpt, int n_items, int item0) {
-    const uint64_t field = (1ull << lpt) - 1ull;
-    for (int i = 0; i < n_items; ++i) {  // wave-uniform
-        float m = 0.f;
-        if (q.valid) m = (xs[i * p.in_f + q.a] - xs[i * p.in_f + q.b]) - q.thr;
-        const uint64_t mask = __ballot(q.valid && m > 0.f);
-        const int code = static_cast<int>((mask >> (slot * lpt)) & field);
-        const bool head = (c == 0) && (t < p.tables);
-        const size_t b = static_cast<size_t>(item0 + i);
-        if (head) codes[i * p.tables + t] = static_cast<uint16_t>(code);
-        if constexpr (DEBUG) {
-            if (p.margins != nullptr && q.valid) p.margins[(b * p.tables + t) * p.comps + c] = m;
-            if (p.indices != nullptr && head) p.indices[b * p.tables + t] = code;
-        }
-        if constexpr (TRAIN) {
-            // argmin |m| over the P lanes of this table; padding lanes
-            // (c >= C) carry +inf and index 64 so they never win.
-            float mag = q.valid ? fabsf(m) : __builtin_inff();
-            int idx = q.valid ? c : kWave;
-            float val = m;
-            for (int s = 1; s < lpt; s <<= 1) {
-                const float omag = __shfl_xor(mag, s, kWave);
-                const int oidx = __shfl_xor(idx, s, kWave);
-                const float oval = __shfl_xor(val, s, kWave);
-                if (min_margin_before(omag, oidx, mag, idx)) {
-                    mag = omag;
-                    idx = oidx;
-                    val = oval;
-                }
-            }
-            if (head) {
-                tropnn_route_record r;
-                r.u = val;
-                r.code = static_cast<uint16_t>(code);
-                r.r = static_cast<uint8_t>(idx);
-                r.reserved = 0;
-                p.rec[static_cast<size_t>(t) * p.items + b] = r;
-            }
-        }
-    }
+// One DPP step of the min-margin argmin: keep the smaller 64-bit key of this
+// lane and its CTRL partner.
+template <int CTRL>
+__device__ __forceinline__ void key_min_step(uint32_t &hi, uint32_t &lo) {
+    const uint32_t ohi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(hi), CTRL, 0xF, 0xF, false));
+    const uint32_t olo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(lo), CTRL, 0xF, 0xF, false));
+    const bool take = ohi < hi || (ohi == hi && olo < lo);
+    hi = take ? ohi : hi;
+    lo = take ? olo : lo;
 }
 
-template <typename T, int V, bool TRAIN, bool DEBUG>
-__global__ __launch_bounds__(512) void pairwise_forward_kernel(FwdArgs a) {
+// Route record of a table, held by the lane that wins its min-margin pick.
+struct RouteOut {
+    uint64_t rec;
+    bool win;
+};
+
+template <bool TRAIN, bool DEBUG>
+__device__ __forceinline__ RouteOut route_ballot(const FwdArgs &p, const float *xs, uint8_t *my_codes,
+                                                 const Comparator &q, int t, int j, int c, int slot, int item) {
+    const float m = (xs[q.a] - xs[q.b]) - q.thr;
+    const uint64_t mask = __ballot(q.valid && m > 0.f);
+    const int code = static_cast<int>((mask >> (slot << p.lpt_log2)) & ((1ull << p.comps) - 1ull));
+    const bool head = q.valid && c == 0;
+    if (head) my_codes[j] = static_cast<uint8_t>(code);
+    if constexpr (DEBUG) {
+        const size_t bt = static_cast<size_t>(item) * p.tables + t;
+        if (p.margins != nullptr && q.valid) p.margins[bt * p.comps + c] = m;
+        if (p.indices != nullptr && head) p.indices[bt] = code;
+    }
+    RouteOut r{0ull, false};
+    if constexpr (TRAIN) {
+        // torch.argmin over |m|: NaN first, then the smaller magnitude, then
+        // the lower comparison index. Key (hi, lo) = (0 for NaN else
+        // bits(|m|) + 1, c); padding lanes carry the largest key.
+        const float mag = fabsf(m);
+        uint32_t hi = q.valid ? (mag != mag ? 0u : __builtin_bit_cast(uint32_t, mag) + 1u) : 0xFFFFFFFFu;
+        uint32_t lo = static_cast<uint32_t>(c);
+        const int lpt = 1 << p.lpt_log2;   // wave-uniform
+        if (lpt >= 2) key_min_step<0xB1>(hi, lo);   // quad_perm [1,0,3,2]
+        if (lpt >= 4) key_min_step<0x4E>(hi, lo);   // quad_perm [2,3,0,1]
+        if (lpt >= 8) key_min_step<0x141>(hi, lo);  // row_half_mirror
+        r.win = q.valid && lo == static_cast<uint32_t>(c);
+        r.rec = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, m)) | (static_cast<uint64_t>(code) << 32) |
+                (static_cast<uint64_t>(c) << 48);
+    }
+    return r;
+}
+
+template <typename T, int N, bool TRAIN, bool DEBUG>
+__global__ __launch_bounds__(1024) void pairwise_forward_kernel(FwdArgs a) {
+    constexpr int kG = gather_chunk(static_cast<int>(sizeof(T)), N);
     extern __shared__ __align__(16) unsigned char lds[];
     float *xs = reinterpret_cast<float *>(lds);
-    uint16_t *codes = reinterpret_cast<uint16_t *>(lds + a.codes_off);
     float *red = reinterpret_cast<float *>(lds + a.red_off);
 
-    const int tid = threadIdx.x, nthr = blockDim.x;
-    const int lane = tid & (kWave - 1), wave = tid / kWave, nwaves = nthr / kWave;
-    const int item0 = blockIdx.x * a.items_per_wg;
-    const int n_items = min(a.items_per_wg, a.items - item0);
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nwaves = blockDim.x >> 6;
+    const int item = blockIdx.x;
+    uint8_t *my_codes = lds + a.codes_off + wave * a.codes_pitch;
 
-    const int lpt = 1 << a.lpt_log2;
     const int tpb = kWave >> a.lpt_log2;
-    const int nballot = (a.tables + tpb - 1) / tpb;
     const int slot = lane >> a.lpt_log2;
-    const int c = lane & (lpt - 1);
+    const int c = lane & ((1 << a.lpt_log2) - 1);
+    const int t_begin = wave * a.per_wave;
+    const int t_end = min(a.tables, t_begin + a.per_wave);
+    const int n_t = max(0, t_end - t_begin);
+    const int nballot = (n_t + tpb - 1) / tpb;
 
-    // 1. prefetch this wave's first ballots, stage the input rows
+    // 1. prefetch this wave's first ballots, stage the input row
     Comparator pre[kBallots];
 #pragma unroll
-    for (int j = 0; j < kBallots; ++j) pre[j] = load_comparator(a, (wave + j * nwaves) * tpb + slot, c);
+    for (int j = 0; j < kBallots; ++j) pre[j] = load_comparator(a, t_begin + j * tpb + slot, t_end, c);
     {
-        const float *src = a.x + static_cast<size_t>(item0) * a.in_f;
-        const int n = n_items * a.in_f;
+        const float *src = a.x + static_cast<size_t>(item) * a.in_f;
         if ((a.in_f & 3) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
-            const int n4 = n >> 2;
-            for (int k = tid; k < n4; k += nthr)
+            for (int k = tid; k < (a.in_f >> 2); k += blockDim.x)
                 reinterpret_cast<vec_t<float, 4> *>(xs)[k] = reinterpret_cast<const vec_t<float, 4> *>(src)[k];
         } else {
-            for (int k = tid; k < n; k += nthr) xs[k] = src[k];
+            for (int k = tid; k < a.in_f; k += blockDim.x) xs[k] = src[k];
         }
     }
     __syncthreads();
 
-    // 2. route
+    // 2. route this wave's tables; codes go to the wave's LDS list, route
+    //    records are stored after the last ballot (off the ballots' path)
+    RouteOut ro[kBallots];
 #pragma unroll
     for (int j = 0; j < kBallots; ++j) {
-        const int kb = wave + j * nwaves;
-        if (kb < nballot) route_ballot<TRAIN, DEBUG>(a, xs, codes, pre[j], kb * tpb + slot, c, slot, lpt, n_items, item0);
+        ro[j] = RouteOut{0ull, false};
+        if (j < nballot)
+            ro[j] = route_ballot<TRAIN, DEBUG>(a, xs, my_codes, pre[j], t_begin + j * tpb + slot, j * tpb + slot, c,
+                                               slot, item);
     }
-    for (int kb = wave + kBallots * nwaves; kb < nballot; kb += nwaves) {  // many tables: rest of the ballots
-        const Comparator q = load_comparator(a, kb * tpb + slot, c);
-        route_ballot<TRAIN, DEBUG>(a, xs, codes, q, kb * tpb + slot, c, slot, lpt, n_items, item0);
+    for (int k = kBallots; k < nballot; ++k) {
+        const Comparator q = load_comparator(a, t_begin + k * tpb + slot, t_end, c);
+        const RouteOut r =
+            route_ballot<TRAIN, DEBUG>(a, xs, my_codes, q, t_begin + k * tpb + slot, k * tpb + slot, c, slot, item);
+        if (TRAIN && r.win) a.rec[static_cast<size_t>(t_begin + k * tpb + slot) * a.items + item] = r.rec;
     }
-    __syncthreads();
+    if constexpr (TRAIN) {
+#pragma unroll
+        for (int j = 0; j < kBallots; ++j)
+            if (ro[j].win) a.rec[static_cast<size_t>(t_begin + j * tpb + slot) * a.items + item] = ro[j].rec;
+    }
+    // LDS operations of one wave complete in order: the code list is ready
 
-    // 3. gather + sum over tables
-    const int lpr = 1 << a.lpr_log2;
-    const int sub = kWave >> a.lpr_log2;
-    const int i = wave / a.waves_per_item;
-    const int wi = wave - i * a.waves_per_item;
-    const int sg = lane >> a.lpr_log2;
-    const int l = lane & (lpr - 1);
-    const int gid = wi * sub + sg;
-    const int gpi = a.waves_per_item * sub;
-    const int col = blockIdx.y * a.o_tile + l * V;
-    const bool in_tile = (l * V < a.o_tile) && (col < a.out_f);
-    const bool active = (i < n_items) && in_tile;
-
-    float acc[V];
+    // 3. gather + sum over the wave's tables
+    const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(a.lut, a.lut_bytes);
+    const int col = blockIdx.y * (kWave * N) + lane * N;
+    const uint32_t voff = col < a.out_f ? static_cast<uint32_t>(col) * static_cast<uint32_t>(sizeof(T)) : kOutOfRange;
+    float acc[N];
 #pragma unroll
-    for (int e = 0; e < V; ++e) acc[e] = 0.f;
-
-    if (active) {
-        const T *lut = static_cast<const T *>(a.lut) + col;
-        const uint16_t *my = codes + i * a.tables;
-        const size_t row_stride = static_cast<size_t>(a.out_f);
-        const size_t table_stride = static_cast<size_t>(a.rows) * a.out_f;
-        for (int t0 = gid; t0 < a.tables; t0 += kGather * gpi) {
-            float v[kGather][V];
+    for (int e = 0; e < N; ++e) acc[e] = 0.f;
+    for (int t0 = 0; t0 < n_t; t0 += kG) {
+        const int cnt = min(kG, n_t - t0);
+        static_assert(kG % 8 == 0, "codes are read 8 or 16 at a time");
+        constexpr int kRead = kG >= 16 ? 16 : 8;  // bytes per broadcast LDS read
+        uint32_t words[kG / 4];
 #pragma unroll
-            for (int u = 0; u < kGather; ++u) {
-                const int tt = t0 + u * gpi;
-                const bool ok = tt < a.tables;
-                const int ts = ok ? tt : 0;  // masked lanes read row 0 of table 0
-                load_row<T, V>(lut + ts * table_stride + (ok ? my[ts] : 0) * row_stride, v[u]);
-                if (!ok) {
+        for (int q = 0; q < kG / kRead; ++q) {
+            const vec_t<uint32_t, kRead / 4> w =
+                *reinterpret_cast<const vec_t<uint32_t, kRead / 4> *>(my_codes + t0 + kRead * q);
 #pragma unroll
-                    for (int e = 0; e < V; ++e) v[u][e] = 0.f;
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < kGather; ++u)
-#pragma unroll
-                for (int e = 0; e < V; ++e) acc[e] += v[u][e];
+            for (int e = 0; e < kRead / 4; ++e) words[(kRead / 4) * q + e] = __builtin_amdgcn_readfirstlane(w[e]);
         }
+        const int tbase = (t_begin + t0) * a.table_bytes;
+        // every slot issues its load; slots past the wave's last table read
+        // out of range (zeros), so the loads need no branches
+        float v[kG][N];
+#pragma unroll
+        for (int u = 0; u < kG; ++u) {
+            const bool live = u < cnt;
+            const int code = static_cast<int>((words[u >> 2] >> (8 * (u & 3))) & 0xffu);
+            const int soff = live ? tbase + u * a.table_bytes + code * a.row_bytes : 0;
+            buffer_row<T, N>(rsrc, live ? voff : kOutOfRange, soff, v[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kG; ++u)
+#pragma unroll
+            for (int e = 0; e < N; ++e) acc[e] += v[u][e];
     }
 
-    // combine the sub-groups of the wave (lanes that differ in bits >= lpr)
+    // 4. sum the waves' partial rows in wave order, scale, store
+    if (nwaves > 1) {
+        if (wave > 0) {
 #pragma unroll
-    for (int e = 0; e < V; ++e) acc[e] = xor_sum(acc[e], lpr, kWave);
-
-    if (a.waves_per_item > 1) {
-        if (sg == 0 && in_tile && wi > 0) {
-            float *dst = red + ((i * a.waves_per_item + wi) * a.o_tile) + l * V;
-#pragma unroll
-            for (int e = 0; e < V; ++e) dst[e] = acc[e];
+            for (int e = 0; e < N; ++e) red[((wave - 1) * kWave + lane) * N + e] = acc[e];
         }
         __syncthreads();
-        if (wi == 0 && sg == 0 && active) {
-            for (int w = 1; w < a.waves_per_item; ++w) {
-                const float *src = red + ((i * a.waves_per_item + w) * a.o_tile) + l * V;
+        if (wave == 0) {
+            for (int w = 1; w < nwaves; ++w) {
 #pragma unroll
-                for (int e = 0; e < V; ++e) acc[e] += src[e];
+                for (int e = 0; e < N; ++e) acc[e] += red[((w - 1) * kWave + lane) * N + e];
             }
         }
     }
-
-    if (wi == 0 && sg == 0 && active) {
-        float y[V];
+    if (wave == 0 && col < a.out_f) {
+        float y[N];
 #pragma unroll
-        for (int e = 0; e < V; ++e) y[e] = acc[e] * a.scale;
-        store_f32<V>(a.out + static_cast<size_t>(item0 + i) * a.out_f + col, y);
+        for (int e = 0; e < N; ++e) y[e] = acc[e] * a.scale;
+        store_f32<N>(a.out + static_cast<size_t>(item) * a.out_f + col, y);
     }
 }
 
-template <typename T, int V>
+template <typename T, int N>
 hipError_t launch_typed(const FwdArgs &args, const ForwardPlan &p, bool train, bool debug, hipStream_t stream) {
     const dim3 grid(p.blocks, p.o_tiles), block(p.threads);
     const ArmedEvents ev = take_armed_events(TROPNN_KERNEL_FORWARD);
     record_event(ev.start, stream);
     if (train && debug)
-        hipLaunchKernelGGL((pairwise_forward_kernel<T, V, true, true>), grid, block, p.lds_bytes, stream, args);
+        hipLaunchKernelGGL((pairwise_forward_kernel<T, N, true, true>), grid, block, p.lds_bytes, stream, args);
     else if (train)
-        hipLaunchKernelGGL((pairwise_forward_kernel<T, V, true, false>), grid, block, p.lds_bytes, stream, args);
+        hipLaunchKernelGGL((pairwise_forward_kernel<T, N, true, false>), grid, block, p.lds_bytes, stream, args);
     else if (debug)
-        hipLaunchKernelGGL((pairwise_forward_kernel<T, V, false, true>), grid, block, p.lds_bytes, stream, args);
+        hipLaunchKernelGGL((pairwise_forward_kernel<T, N, false, true>), grid, block, p.lds_bytes, stream, args);
     else
-        hipLaunchKernelGGL((pairwise_forward_kernel<T, V, false, false>), grid, block, p.lds_bytes, stream, args);
+        hipLaunchKernelGGL((pairwise_forward_kernel<T, N, false, false>), grid, block, p.lds_bytes, stream, args);
     const hipError_t e = hipGetLastError();
     record_event(ev.stop, stream);
     return e;
@@ -256,40 +269,37 @@ int ilog2(int v) {
 ForwardPlan plan_forward(const Dims &d) {
     ForwardPlan p{};
     const int esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
-    // widest load (<= 16 bytes) that divides a row, so every row start and
-    // every lane offset stays aligned
-    p.vec = 16 / esize;
+    // N elements per lane: the smallest power of two whose 64-lane tile spans
+    // the row (16 bytes at most), reduced until it divides the row so that
+    // every lane's slice is aligned and either wholly inside or outside it
+    p.vec = 1;
+    while (p.vec * esize < 16 && p.vec * kWave < d.out_f) p.vec <<= 1;
     while (p.vec > 1 && d.out_f % p.vec != 0) p.vec >>= 1;
-    p.lpt_log2 = ilog2(d.comps);
-    const int lanes_needed = (d.out_f + p.vec - 1) / p.vec;
-    const int lanes = lanes_needed < kWave ? lanes_needed : kWave;
-    p.lpr_log2 = ilog2(lanes);
-    p.o_tile = (1 << p.lpr_log2) * p.vec;
-    if (p.o_tile > d.out_f) p.o_tile = d.out_f;
+    p.o_tile = kWave * p.vec;
     p.o_tiles = (d.out_f + p.o_tile - 1) / p.o_tile;
-    const int sub = kWave >> p.lpr_log2;
+    p.lpt_log2 = ilog2(d.comps);
+    const int chunk = gather_chunk(esize, p.vec);
 
-    // Aim for ~4096 waves (256 CUs x 16): split an item's tables over several
-    // waves only when items x tiles alone cannot fill the chip.
+    // waves per item: enough that one gather chunk covers a wave's tables,
+    // more while items x tiles alone cannot give ~4096 waves, at most 16
     const long long units = static_cast<long long>(d.items) * p.o_tiles;
-    int wpi = 1;
-    while (wpi < 8 && units * wpi < 4096 && static_cast<long long>(wpi) * 2 * sub <= d.tables) wpi <<= 1;
-    int ipw = 8 / wpi;
-    // keep the staged input rows within 32 KB of LDS
-    while (ipw > 1 && static_cast<long long>(ipw) * d.in_f * 4 > 32 * 1024) ipw >>= 1;
-    if (ipw > d.items) ipw = d.items < 1 ? 1 : d.items;
-    p.waves_per_item = wpi;
-    p.items_per_wg = ipw;
-    p.threads = ipw * wpi * kWave;
-    p.blocks = (d.items + ipw - 1) / ipw;
+    int w = (d.tables + chunk - 1) / chunk;
+    const long long want = units > 0 ? (4096 + units - 1) / units : 16;
+    if (want > w) w = static_cast<int>(want < 16 ? want : 16);
+    if (w > 16) w = 16;
+    if (w > d.tables) w = d.tables;
+    p.per_wave = (d.tables + w - 1) / w;
+    p.waves_per_item = (d.tables + p.per_wave - 1) / p.per_wave;
+    p.threads = p.waves_per_item * kWave;
+    p.blocks = d.items;
+    p.codes_pitch = ((p.per_wave + chunk - 1) / chunk) * chunk;
 
-    int off = ipw * d.in_f * 4;
-    off = (off + 15) & ~15;
+    int off = ((d.in_f * 4) + 15) & ~15;
     p.codes_off = off;
-    off += ipw * d.tables * 2;
+    off += p.waves_per_item * p.codes_pitch;
     off = (off + 15) & ~15;
     p.red_off = off;
-    if (wpi > 1) off += ipw * wpi * p.o_tile * 4;
+    off += (p.waves_per_item - 1) * kWave * p.vec * 4;
     p.lds_bytes = off;
     return p;
 }
@@ -297,6 +307,7 @@ ForwardPlan plan_forward(const Dims &d) {
 hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, const int64_t *anchors,
                           const float *thr, const void *lut, float scale, float *out, tropnn_route_record *rec,
                           int64_t *indices, float *margins, hipStream_t stream) {
+    const int esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
     FwdArgs a{};
     a.x = x;
     a.anchors = anchors;
@@ -304,20 +315,20 @@ hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, c
     a.lut = lut;
     a.scale = scale;
     a.out = out;
-    a.rec = rec;
+    a.rec = reinterpret_cast<uint64_t *>(rec);
     a.indices = indices;
     a.margins = margins;
+    a.lut_bytes = static_cast<uint32_t>(static_cast<size_t>(d.tables) * d.rows * d.out_f * esize);
     a.items = d.items;
     a.in_f = d.in_f;
     a.out_f = d.out_f;
     a.tables = d.tables;
     a.comps = d.comps;
-    a.rows = d.rows;
+    a.row_bytes = d.out_f * esize;
+    a.table_bytes = d.rows * d.out_f * esize;
     a.lpt_log2 = p.lpt_log2;
-    a.lpr_log2 = p.lpr_log2;
-    a.o_tile = p.o_tile;
-    a.items_per_wg = p.items_per_wg;
-    a.waves_per_item = p.waves_per_item;
+    a.per_wave = p.per_wave;
+    a.codes_pitch = p.codes_pitch;
     a.codes_off = p.codes_off;
     a.red_off = p.red_off;
     const bool train = rec != nullptr;

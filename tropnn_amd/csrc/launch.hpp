@@ -23,37 +23,53 @@ struct Dims {
 
 // Launch shape of the fused route + gather + scale forward.
 struct ForwardPlan {
-    int vec;             // LUT elements per lane load (16 bytes at most)
+    int vec;             // N: LUT elements per lane load (16 bytes at most)
     int lpt_log2;        // lanes per table in a route ballot (>= C)
-    int lpr_log2;        // lanes per LUT row in the gather
-    int o_tile;          // output columns per workgroup
+    int o_tile;          // output columns per workgroup (64 * N)
     int o_tiles;         // grid.y
-    int items_per_wg;    // items per workgroup
-    int waves_per_item;  // waves sharing one item's tables
-    int threads;         // items_per_wg * waves_per_item * 64
-    int blocks;          // grid.x
+    int per_wave;        // tables per wave (contiguous block)
+    int waves_per_item;  // waves of a workgroup (one item per workgroup)
+    int threads;         // waves_per_item * 64
+    int blocks;          // grid.x = items
+    int codes_pitch;     // LDS bytes of a wave's code list
     int codes_off;       // LDS byte offsets
     int red_off;
     int lds_bytes;
 };
 
-// Launch shape of the table-major backward (LUT gradient + STE dot) and of
-// the input-side backward (input / threshold gradients).
+// Launch shape of the backward: the item kernel (STE dots, gu, input
+// gradient) and the table kernel (LUT gradient, threshold gradient).
 struct BackwardPlan {
-    int vec;            // elements per lane load of grad_output / LUT rows
-    int o_chunk;        // output columns per table workgroup
+    // table kernel
+    int vec;            // V: columns per lane (divides the row, at most 4)
+    int slices;         // S: lanes per row group (4 to 32)
+    int o_chunk;        // S * V output columns per table workgroup
     int o_chunks;       // grid.y of the table kernel
-    int pitch;          // LDS row pitch (floats) of the LUT slab
-    int slices_log2;    // lanes (vec-wide column slices) per gradient row
     int lut_threads;    // threads of a table workgroup = items per sort tile
-    int lut_lds_bytes;  // slab + histograms + bucket starts + sorted tile
-    int in_items_per_wg;
-    int in_threads;
-    int in_lds_bytes;
-    size_t workspace_bytes;  // partial STE dots [o_chunks][T][B] f32
+    int hist_off, start_off, sorted_off, rowbuf_off, part_off, thr_off, wtot_off;  // LDS byte offsets
+    int lut_lds_bytes;
+    // item kernel
+    int item_vec;       // N: LUT / grad elements per lane load (16 bytes at most)
+    int item_o_tiles;   // 64 * N column tiles per row
+    int item_per_wave;  // tables per wave
+    int item_waves;     // waves per workgroup (one item per workgroup)
+    int item_threads;
+    int item_lds_bytes; // the item's gu slots [T * C] f32 + the inverse anchor index
+    size_t workspace_bytes;  // gu [T][B] f32
 };
 
+// Row loads a forward wave keeps in flight (its gather chunk), by LUT element
+// size and elements per lane; sized to stay within 128 VGPRs.
+constexpr int gather_chunk(int esize, int vec) { return esize == 2 && vec == 8 ? 8 : 16; }
+
 ForwardPlan plan_forward(const Dims &d);
+// Tables whose two LUT rows an item-kernel wave keeps in flight, by LUT
+// element size and elements per lane: about 48 VGPRs of rows, so the kernel
+// stays within 80 VGPRs and two workgroups share a CU.
+constexpr int item_wave_tables(int esize, int vec) {
+    return esize * vec <= 4 ? 16 : (esize * vec == 8 ? 12 : (esize == 4 ? 6 : 3));
+}
+
 BackwardPlan plan_backward(const Dims &d);
 
 hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, const int64_t *anchors,
