@@ -9,11 +9,14 @@ the module's seeded init (seed 0); inputs are synthetic and already in HBM.
 Timed regions (both full fwd+bwd of the module API, no work skipped):
   graph  -- the step captured once per input batch in a HIP graph
             (torch.cuda.CUDAGraph); K replays round-robin over 4 distinct
-            resident (x, G) batches. This is `value`.
-  eager  -- K plain autograd steps; the three kernels of each step are
-            bracketed with HIP events recorded on their own launch stream
-            (library hook tropnn_hip_arm_kernel_events), giving the per-kernel
-            average durations used for `roofline`.
+            resident (x, G) batches, after >= 0.3 s of replays (the GPU clocks
+            ramp up under sustained load). This is `value`. The same with four
+            steps (four batches) per graph is reported beside it.
+  eager  -- up to 200 plain autograd steps right after the graph phase; the
+            three kernels of each step carry HIP events that their own
+            dispatch stamps (library hook tropnn_hip_arm_kernel_events, via
+            hipExtLaunchKernel), giving the per-kernel average durations used
+            for `roofline`.
 cpu_baseline: the oracle's torch restatement of the reference torch path, same
 step on the host CPU for a bounded number of steps (rank 0, N=1 only).
 
@@ -172,29 +175,12 @@ def main() -> int:
         xs[k].grad = None
         layer(xs[k]).backward(gs[k])
 
-    # ---- eager warmup + per-kernel event timing
-    for w in range(args.warmup):
+    stream = torch.cuda.current_stream(dev)
+    for w in range(args.warmup):  # eager warmup (allocator, library, anchor index)
         step(w % nb)
     torch.cuda.synchronize()
-    names = ("forward", "backward_item", "backward_table")
-    evs = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)] for n in names}
-    stream = torch.cuda.current_stream(dev)
-    for n in names:  # create the event handles
-        for e0, e1 in evs[n]:
-            e0.record(stream)
-            e1.record(stream)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(args.steps):
-        for n in names:
-            arm_kernel_events(n, *evs[n][k])
-        step(k % nb)
-    torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    kern_us = {n: 1e3 * sum(e0.elapsed_time(e1) for e0, e1 in evs[n]) / args.steps for n in names}
-    log(f"eager {eager_ms * 1e3:.1f} us/step; kernels (us): " + ", ".join(f"{n}={v:.2f}" for n, v in kern_us.items()))
 
-    # ---- graph capture: one graph per resident batch
+    # ---- graph capture: one graph per resident batch, one step per graph
     side = torch.cuda.Stream(dev)
     side.wait_stream(stream)
     with torch.cuda.stream(side):
@@ -202,24 +188,63 @@ def main() -> int:
             step(w % nb)
     stream.wait_stream(side)
     torch.cuda.synchronize()
-    graphs = []
-    for k in range(nb):
+
+    def capture(ks: list[int]) -> torch.cuda.CUDAGraph:
         layer.zero_grad(set_to_none=True)
-        xs[k].grad = None
+        for k in ks:
+            xs[k].grad = None
         gph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gph):
-            layer(xs[k]).backward(gs[k])
-        graphs.append(gph)
-    torch.cuda.synchronize()
-    for w in range(args.warmup):
-        graphs[w % nb].replay()
+            for k in ks:
+                layer.zero_grad(set_to_none=True)
+                layer(xs[k]).backward(gs[k])
+        return gph
+
+    def replay_rate(graphs: list, steps_per_graph: int, steps: int) -> float:
+        """us per step over `steps` steps, after >= 0.3 s (and >= --warmup
+        replays) of warmup: the GPU clocks ramp up under sustained load."""
+        torch.cuda.synchronize()
+        t0, w = time.perf_counter(), 0
+        while w < args.warmup or time.perf_counter() - t0 < 0.3:
+            graphs[w % len(graphs)].replay()
+            w += 1
+        torch.cuda.synchronize()
+        n = max(1, steps // steps_per_graph)
+        t0 = time.perf_counter()
+        for k in range(n):
+            graphs[k % len(graphs)].replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e6 / (n * steps_per_graph)
+
+    graphs = [capture([k]) for k in range(nb)]
+    graph_us = replay_rate(graphs, 1, args.steps)
+    graph_ms = graph_us * 1e-3
+    log(f"graph {graph_us:.1f} us/step (one step per graph)")
+    graphs4 = [capture([(j + i) % nb for i in range(4)]) for j in range(nb)]
+    graph4_us = replay_rate(graphs4, 4, args.steps)
+    log(f"graph {graph4_us:.1f} us/step (four steps per graph)")
+
+    # ---- per-kernel durations: eager steps right after the graph phase (GPU
+    # clocks still up); each kernel's own dispatch stamps the armed events
+    names = ("forward", "backward_item", "backward_table")
+    ksteps = min(args.steps, 200)
+    evs = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(ksteps)] for n in names}
+    for n in names:  # create the event handles
+        for e0, e1 in evs[n]:
+            e0.record(stream)
+            e1.record(stream)
+    for w in range(nb):
+        step(w)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for k in range(args.steps):
-        graphs[k % nb].replay()
+    for k in range(ksteps):
+        for n in names:
+            arm_kernel_events(n, *evs[n][k])
+        step(k % nb)
     torch.cuda.synchronize()
-    graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    log(f"graph {graph_ms * 1e3:.1f} us/step")
+    eager_ms = (time.perf_counter() - t0) * 1e3 / ksteps
+    kern_us = {n: 1e3 * sum(e0.elapsed_time(e1) for e0, e1 in evs[n]) / ksteps for n in names}
+    log(f"eager {eager_ms * 1e3:.1f} us/step; kernels (us): " + ", ".join(f"{n}={v:.2f}" for n, v in kern_us.items()))
 
     # ---- roofline of the dominant kernel
     algo = algorithmic_bytes()
@@ -283,6 +308,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "step_algorithmic_GBs": round(total_algo / (graph_ms * 1e-3) / 1e9, 1),
+        "us_per_step_four_steps_per_graph": round(graph4_us, 3),
         "eager_ms_per_step": round(eager_ms, 6),
         "kernels": kernels,
     }

@@ -594,12 +594,8 @@ template <int V, int S>
 hipError_t launch_table_vs(const LutArgs &args, const BackwardPlan &p, hipStream_t stream) {
     auto kernel = pairwise_bwd_table_kernel<V, S>;
     if (hipError_t e = allow_lds(kernel, p.lut_lds_bytes); e != hipSuccess) return e;
-    const ArmedEvents ev = take_armed_events(TROPNN_KERNEL_BACKWARD_TABLE);
-    record_event(ev.start, stream);
-    hipLaunchKernelGGL(kernel, dim3(args.tables, p.o_chunks), dim3(p.lut_threads), p.lut_lds_bytes, stream, args);
-    const hipError_t e = hipGetLastError();
-    record_event(ev.stop, stream);
-    return e;
+    return launch_kernel(TROPNN_KERNEL_BACKWARD_TABLE, kernel, dim3(args.tables, p.o_chunks), dim3(p.lut_threads),
+                         p.lut_lds_bytes, stream, args);
 }
 
 template <int V>
@@ -622,13 +618,8 @@ hipError_t launch_table(const LutArgs &args, const BackwardPlan &p, hipStream_t 
 
 template <typename T, int N>
 hipError_t launch_item_typed(const ItemArgs &args, const BackwardPlan &p, hipStream_t stream) {
-    const ArmedEvents ev = take_armed_events(TROPNN_KERNEL_BACKWARD_ITEM);
-    record_event(ev.start, stream);
-    hipLaunchKernelGGL((pairwise_bwd_item_kernel<T, N>), dim3(args.items), dim3(p.item_threads), p.item_lds_bytes,
-                       stream, args);
-    const hipError_t e = hipGetLastError();
-    record_event(ev.stop, stream);
-    return e;
+    return launch_kernel(TROPNN_KERNEL_BACKWARD_ITEM, pairwise_bwd_item_kernel<T, N>, dim3(args.items),
+                         dim3(p.item_threads), p.item_lds_bytes, stream, args);
 }
 
 __global__ void fill_zero_kernel(float *p, size_t n) {

@@ -243,19 +243,9 @@ __global__ __launch_bounds__(1024) void pairwise_forward_kernel(FwdArgs a) {
 template <typename T, int N>
 hipError_t launch_typed(const FwdArgs &args, const ForwardPlan &p, bool train, bool debug, hipStream_t stream) {
     const dim3 grid(p.blocks, p.o_tiles), block(p.threads);
-    const ArmedEvents ev = take_armed_events(TROPNN_KERNEL_FORWARD);
-    record_event(ev.start, stream);
-    if (train && debug)
-        hipLaunchKernelGGL((pairwise_forward_kernel<T, N, true, true>), grid, block, p.lds_bytes, stream, args);
-    else if (train)
-        hipLaunchKernelGGL((pairwise_forward_kernel<T, N, true, false>), grid, block, p.lds_bytes, stream, args);
-    else if (debug)
-        hipLaunchKernelGGL((pairwise_forward_kernel<T, N, false, true>), grid, block, p.lds_bytes, stream, args);
-    else
-        hipLaunchKernelGGL((pairwise_forward_kernel<T, N, false, false>), grid, block, p.lds_bytes, stream, args);
-    const hipError_t e = hipGetLastError();
-    record_event(ev.stop, stream);
-    return e;
+    auto kernel = train ? (debug ? pairwise_forward_kernel<T, N, true, true> : pairwise_forward_kernel<T, N, true, false>)
+                        : (debug ? pairwise_forward_kernel<T, N, false, true> : pairwise_forward_kernel<T, N, false, false>);
+    return launch_kernel(TROPNN_KERNEL_FORWARD, kernel, grid, block, p.lds_bytes, stream, args);
 }
 
 int ilog2(int v) {

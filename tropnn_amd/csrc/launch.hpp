@@ -2,6 +2,7 @@
 // (forward.hip, backward.hip). Not exported.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -86,15 +87,26 @@ hipError_t launch_anchor_index(const int64_t *anchors, int in_f, int tables, int
                                int32_t *entries, hipStream_t stream);
 
 // Events armed by tropnn_hip_arm_kernel_events for the next launch of a
-// kernel; take_armed_events clears them. record_event tolerates NULL.
+// kernel; take_armed_events clears them.
 struct ArmedEvents {
     hipEvent_t start = nullptr;
     hipEvent_t stop = nullptr;
 };
 ArmedEvents take_armed_events(int kernel);
 void arm_events(int kernel, hipEvent_t start, hipEvent_t stop);
-inline void record_event(hipEvent_t e, hipStream_t s) {
-    if (e != nullptr) (void)hipEventRecord(e, s);
+
+// Launches `kernel`; when events are armed for `kernel_id`, the dispatch
+// itself stamps them with the kernel's start and end (hipExtLaunchKernel), so
+// they time the kernel alone, without marker packets around it.
+template <typename F, typename... Args>
+hipError_t launch_kernel(int kernel_id, F kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t stream,
+                         Args... args) {
+    const ArmedEvents ev = take_armed_events(kernel_id);
+    if (ev.start != nullptr)
+        hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, ev.start, ev.stop, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+    return hipGetLastError();
 }
 
 // Writes n zeros with a kernel (no hipMemsetAsync node in captured graphs).
