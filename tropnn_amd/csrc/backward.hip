@@ -49,7 +49,7 @@ namespace {
 constexpr int kLutThreads = 1024;  // items per sort tile
 constexpr int kItemTables = 16;    // tables per item-kernel wave (one reduce-scatter)
 constexpr int kEntries = 16;       // index entries a walker reads per batch
-constexpr int kIndexRegs = 2;      // index words per thread loaded ahead of the dots
+constexpr int kIndexRegs = 4;      // index words per thread loaded with the first record
 
 struct ItemArgs {
     const float *grad_out;
@@ -163,22 +163,31 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void 
     //    for the feature walk; its first loads go out with the first block's
     const int nidx = a.grad_x != nullptr ? a.in_f + 1 + 2 * a.tables * C : 0;
     int *idx_s = reinterpret_cast<int *>(gud + a.tables * C);  // [in_f + 1 + 2 T C]
-    int iv[kIndexRegs];
+    constexpr int kLoaded = item_wave_tables(static_cast<int>(sizeof(T)), N);  // tables with rows in flight
+    const int ti = lane >> 2;  // lane l serves table l / 4 of a block
+    // the first block's record of this lane, then this thread's index words,
+    // which go to LDS as soon as they arrive (the dots need the record first
+    // anyway)
+    uint64_t rr_next = ti < min(kLoaded, nt) ? a.rec[static_cast<size_t>(t0 + ti) * a.items + b] : 0ull;
+    {
+        int iv[kIndexRegs];
 #pragma unroll
-    for (int q = 0; q < kIndexRegs; ++q) {
-        const int k = tid + q * nthr;
-        iv[q] = k < nidx ? (k <= a.in_f ? a.index_offsets[k] : a.index_entries[k - a.in_f - 1]) : 0;
+        for (int q = 0; q < kIndexRegs; ++q) {
+            const int k = tid + q * nthr;
+            iv[q] = k < nidx ? (k <= a.in_f ? a.index_offsets[k] : a.index_entries[k - a.in_f - 1]) : 0;
+        }
+#pragma unroll
+        for (int q = 0; q < kIndexRegs; ++q)
+            if (tid + q * nthr < nidx) idx_s[tid + q * nthr] = iv[q];
     }
 
     const __amdgpu_buffer_rsrc_t lut_rsrc = buffer_rsrc(a.lut, a.lut_bytes);
     const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.grad_out, a.g_bytes);
-    constexpr int kLoaded = item_wave_tables(static_cast<int>(sizeof(T)), N);  // tables with rows in flight
-    const int ti = lane >> 2;  // lane l serves table l / 4 of a block
     for (int tb = t0; tb < t0 + nt; tb += kLoaded) {  // blocks of kLoaded tables
         const int ntb = min(kLoaded, t0 + nt - tb);
         // 1. this lane's table record
         const bool has = ti < ntb;
-        const uint64_t rr = has ? a.rec[static_cast<size_t>(tb + ti) * a.items + b] : 0ull;
+        const uint64_t rr = rr_next;
         const int code_v = rec_code(rr) & (R - 1);
         const int r_v = rec_r(rr) & 7;
 
@@ -222,11 +231,10 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void 
             float *slot = gud + (tb + ti) * C;
             for (int c = 0; c < C; ++c) slot[c] = c == r_v ? gu : 0.f;
         }
+        const int tn = tb + kLoaded;  // next block's record
+        if (tn < t0 + nt) rr_next = ti < min(kLoaded, t0 + nt - tn) ? a.rec[static_cast<size_t>(tn + ti) * a.items + b] : 0ull;
     }
     if (a.grad_x == nullptr) return;
-#pragma unroll
-    for (int q = 0; q < kIndexRegs; ++q)
-        if (tid + q * nthr < nidx) idx_s[tid + q * nthr] = iv[q];
     for (int k = tid + kIndexRegs * nthr; k < nidx; k += nthr)
         idx_s[k] = k <= a.in_f ? a.index_offsets[k] : a.index_entries[k - a.in_f - 1];
     __syncthreads();
