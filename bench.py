@@ -16,7 +16,8 @@ Timed regions (both full fwd+bwd of the module API, no work skipped):
             three kernels of each step carry HIP events that their own
             dispatch stamps (library hook tropnn_hip_arm_kernel_events, via
             hipExtLaunchKernel), giving the per-kernel average durations used
-            for `roofline`.
+            for `roofline`. c2's backward is the fused table kernel plus the
+            input-gradient scatter kernel.
 cpu_baseline: the oracle's torch restatement of the reference torch path, same
 step on the host CPU for a bounded number of steps (rank 0, N=1 only).
 
@@ -43,20 +44,43 @@ R = 1 << C
 E = 4  # f32 LUT element bytes
 
 
-def algorithmic_bytes() -> dict[str, int]:
+def algorithmic_bytes(fused: bool) -> dict[str, int]:
     """Per-launch algorithmic bytes (gather / embedding-bag convention: every
     (item, table) pair moves its LUT row(s) once, streamed tensors and params
     once), split by the kernel that moves them. Sums to the FwdBwd figure of
     the c2 plan: 148,548,672 B.
       forward: x, anchors + thresholds, one row per (item, table), y, codes;
+    fused backward (narrow rows, c2's path):
+      backward_fused: G, codes, current + neighbour rows per (item, table),
+        one f32 grad-row contribution per (item, table), grad_lut once,
+        grad_thr;
+      backward_scatter: x re-read (margins), grad_x, anchors + thresholds;
+    general backward:
       backward_item: G, x re-read, codes, current + neighbour rows per
         (item, table), grad_x, anchors + thresholds;
       backward_table: one f32 grad-row contribution per (item, table),
         grad_lut once, grad_thr."""
     fwd = 4 * B * I + 20 * T * C + E * B * T * O + 4 * B * O + B * T
-    item = 4 * B * O + 4 * B * I + B * T + 2 * E * B * T * O + 4 * B * I + 20 * T * C
-    table = 4 * B * T * O + 4 * T * R * O + 4 * T * C
-    return {"forward": fwd, "backward_item": item, "backward_table": table}
+    g_codes_rows = 4 * B * O + B * T + 2 * E * B * T * O
+    x_side = 4 * B * I + 4 * B * I + 20 * T * C
+    lut_side = 4 * B * T * O + 4 * T * R * O + 4 * T * C
+    if fused:
+        return {"forward": fwd, "backward_fused": g_codes_rows + lut_side, "backward_scatter": x_side}
+    return {"forward": fwd, "backward_item": g_codes_rows + x_side, "backward_table": lut_side}
+
+
+def fused_backward() -> bool:
+    """Whether the library runs c2's backward as the fused table kernel plus
+    the scatter kernel (its workspace then holds 8-byte {gu, r} records)."""
+    import ctypes
+
+    from tropnn_amd.backends.pairwise_hip import load_library
+
+    lib = load_library()
+    fn = lib.tropnn_hip_pairwise_backward_workspace_size
+    fn.restype = ctypes.c_size_t
+    fn.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int]
+    return fn(B, I, O, T, C, 0) == 8 * T * B
 
 
 def log(msg: str) -> None:
@@ -226,7 +250,8 @@ def main() -> int:
 
     # ---- per-kernel durations: eager steps right after the graph phase (GPU
     # clocks still up); each kernel's own dispatch stamps the armed events
-    names = ("forward", "backward_item", "backward_table")
+    algo = algorithmic_bytes(fused_backward())
+    names = tuple(algo)
     ksteps = min(args.steps, 200)
     evs = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(ksteps)] for n in names}
     for n in names:  # create the event handles
@@ -247,7 +272,6 @@ def main() -> int:
     log(f"eager {eager_ms * 1e3:.1f} us/step; kernels (us): " + ", ".join(f"{n}={v:.2f}" for n, v in kern_us.items()))
 
     # ---- roofline of the dominant kernel
-    algo = algorithmic_bytes()
     dom = max(names, key=lambda n: kern_us[n])
     achieved = algo[dom] / (kern_us[dom] * 1e-6) / 1e9
     kernels = {

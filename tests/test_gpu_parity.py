@@ -237,6 +237,10 @@ def test_c2_north_star_config():
         (40, 3, 33, 4, 70, 0.5),
         (256, 512, 16, 6, 8, 0.0),
         (100, 96, 7, 2, 300, 0.2),
+        (32, 64, 10, 5, 2500, 0.2),
+        (48, 128, 12, 6, 2100, 0.1),
+        (24, 200, 9, 6, 1500, 0.3),
+        (20, 100, 6, 4, 40, 0.2),
     ],
 )
 def test_train_parity(i, o, t, c, b, thr_std):

@@ -26,7 +26,7 @@ from typing import Any
 import torch
 from torch import Tensor
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LUT_F32, LUT_F16 = 0, 1
 SURROGATE_IDS = {"fast_sigmoid_odd": 0, "izhikevich": 1}
 STE_MIN_MARGIN, STE_FULL = 0, 1
@@ -55,7 +55,7 @@ EXPORTED_SYMBOLS = (
     "tropnn_hip_build_anchor_index",
     "tropnn_hip_arm_kernel_events",
 )
-KERNEL_IDS = {"forward": 0, "backward_table": 1, "backward_item": 2}
+KERNEL_IDS = {"forward": 0, "backward_table": 1, "backward_item": 2, "backward_fused": 3, "backward_scatter": 4}
 
 
 def library_path() -> Path:

@@ -142,6 +142,30 @@ __device__ __forceinline__ float reduce_scatter(const float (&d)[N], int j) {
     return v[0];
 }
 
+// grad_x row of one item: thread f sums the item's signed gu slots gud[(t * C
+// + c)] named by feature f's entries of the inverse anchor index (staged in
+// LDS as offsets [in_f + 1] then entries), in entry order; side 1 subtracts.
+__device__ __forceinline__ void feature_walk(const float *gud, const int *idx_s, int in_f, float *grad_x_row, int tid,
+                                             int nthr) {
+    const int *off_s = idx_s, *ent_s = idx_s + in_f + 1;
+    for (int f = tid; f < in_f; f += nthr) {
+        const int f0 = off_s[f], f1 = off_s[f + 1];
+        float gx = 0.f;
+        for (int eb = f0; eb < f1; eb += kEntries) {
+            int en[kEntries];
+#pragma unroll
+            for (int q = 0; q < kEntries; ++q) en[q] = eb + q < f1 ? ent_s[eb + q] : 0;
+            float v[kEntries];
+#pragma unroll
+            for (int q = 0; q < kEntries; ++q) v[q] = eb + q < f1 ? gud[en[q] >> 1] : 0.f;
+#pragma unroll
+            for (int q = 0; q < kEntries; ++q)
+                if (eb + q < f1) gx = (en[q] & 1) ? gx - v[q] : gx + v[q];
+        }
+        grad_x_row[f] = gx;
+    }
+}
+
 // ------------------------------------------------------------------ item kernel
 
 // At most 80 VGPRs (6 waves per SIMD): two workgroups of up to 9 waves then
@@ -240,23 +264,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void 
     __syncthreads();
 
     // 4. one thread per input feature: its signed slots in entry order
-    const int *off_s = idx_s, *ent_s = idx_s + a.in_f + 1;
-    for (int f = tid; f < a.in_f; f += nthr) {
-        const int f0 = off_s[f], f1 = off_s[f + 1];
-        float gx = 0.f;
-        for (int eb = f0; eb < f1; eb += kEntries) {
-            int en[kEntries];
-#pragma unroll
-            for (int q = 0; q < kEntries; ++q) en[q] = eb + q < f1 ? ent_s[eb + q] : 0;
-            float v[kEntries];
-#pragma unroll
-            for (int q = 0; q < kEntries; ++q) v[q] = eb + q < f1 ? gud[en[q] >> 1] : 0.f;
-#pragma unroll
-            for (int q = 0; q < kEntries; ++q)
-                if (eb + q < f1) gx = (en[q] & 1) ? gx - v[q] : gx + v[q];
-        }
-        a.grad_x[static_cast<size_t>(b) * a.in_f + f] = gx;
-    }
+    feature_walk(gud, idx_s, a.in_f, a.grad_x + static_cast<size_t>(b) * a.in_f, tid, nthr);
 }
 
 // ------------------------------------------------------------------ table kernel
@@ -561,6 +569,334 @@ __global__ __launch_bounds__(kLutThreads) void pairwise_bwd_table_kernel(LutArgs
     }
 }
 
+// ------------------------------------------------------------------ fused row kernel
+
+constexpr int kFusedThreads = 1024;  // threads of a fused workgroup = items per sort tile
+constexpr int kFusedFloats = 32;     // grad-row floats a lane has in flight: 32 / V items per batch
+
+struct FusedArgs {
+    const float *grad_out;
+    const void *lut;
+    const uint64_t *rec;
+    float scale;
+    float *grad_lut;  // or null
+    float *grad_thr;  // or null
+    uint64_t *gurec;  // [T][B] {gu bits, r} for the scatter kernel, or null
+    uint32_t lut_bytes, g_bytes;
+    int items, out_f, tables, comps, rows, pitch;
+    int lut_off, cnt_off, off_off, sorted_off, u_off, rowbuf_off, thr_off, wtot_off;  // LDS byte offsets
+};
+
+// One workgroup per table; the row group of S lanes x V columns spans the
+// whole output row (S * V >= O). The table's LUT rows sit in LDS as f32.
+// Per tile of 1024 items: counting sort by code (as in the table kernel),
+// then row group g owns rows g, g + groups, ... and walks each row's items
+// in item order, 32 / V at a time: one grad row load per item serves both the
+// LUT-gradient sum and the item's STE dot against L[nb] - L[code] (L[code]
+// in registers for the whole row, L[nb] from LDS). One reduce-scatter per
+// batch completes its dots; lanes holding a dot form gu, store {gu, r} for
+// the scatter kernel and leave gu in the sorted position's LDS slot, from
+// which a pass per tile reduces the threshold gradient.
+template <typename T, int V, int S>
+__global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(FusedArgs a) {
+    constexpr int kWaves = kFusedThreads / kWave;
+    constexpr int NG = kFusedThreads / S;  // row groups
+    constexpr int K = kFusedFloats / V;  // items per batch
+    constexpr int kCodesPerLane = (1 << TROPNN_MAX_COMPARISONS) / kWave;
+    constexpr int kStage = 4;  // LUT chunks (4 elements) a thread stages, R * O <= 16384
+    static_assert(K <= S, "a batch's dots are scattered over the row group");
+    extern __shared__ __align__(16) unsigned char lds[];
+    float *lut_s = reinterpret_cast<float *>(lds + a.lut_off);             // [R][pitch] table rows, f32
+    int *cnt = reinterpret_cast<int *>(lds + a.cnt_off);                   // [waves][R] counts -> offsets
+    int *off = reinterpret_cast<int *>(lds + a.off_off);                   // [R + 1] row starts
+    uint32_t *sorted = reinterpret_cast<uint32_t *>(lds + a.sorted_off);  // [tile] item | r << 10
+    float *us = reinterpret_cast<float *>(lds + a.u_off);                  // [tile] margin u, by position
+    float *rowbuf = reinterpret_cast<float *>(lds + a.rowbuf_off);         // [R][pitch] (several tiles)
+    float *tp = reinterpret_cast<float *>(lds + a.thr_off);                // [waves][8]
+    int *wtot = reinterpret_cast<int *>(lds + a.wtot_off);                 // [waves] scan carries, [1] sink
+
+    const int t = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int R = a.rows, C = a.comps, O = a.out_f, P = a.pitch;
+    const bool single = a.items <= kFusedThreads;
+    const bool need_gu = a.grad_thr != nullptr || a.gurec != nullptr;
+    const uint64_t *rec_t = a.rec + static_cast<size_t>(t) * a.items;
+    const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.grad_out, a.g_bytes);
+    const __amdgpu_buffer_rsrc_t lut_rsrc = buffer_rsrc(a.lut, a.lut_bytes);
+
+    // 0. first tile's record, the table's LUT rows (all loads in flight, then
+    //    LDS as f32 with zero columns past O), and a touch of one slice of G
+    //    per XCD as in the table kernel
+    uint64_t r_next = tid < a.items ? rec_t[tid] : 0ull;
+    uint32_t pf = 0u;
+    {
+        const int quads = R * O / 4;  // O % 4 == 0: no chunk crosses a row
+        const int tbase = t * R * O * static_cast<int>(sizeof(T));
+        float v[kStage][4];
+#pragma unroll
+        for (int i = 0; i < kStage; ++i) {
+            const int q = tid + i * kFusedThreads;
+            buffer_row<T, 4>(lut_rsrc, q < quads ? static_cast<uint32_t>(q) * 4u * sizeof(T) : kOutOfRange, tbase, v[i]);
+        }
+        {
+            const int nwg = gridDim.x;
+            const int lin = blockIdx.x;
+            const int share = (nwg - (lin & 7) + 7) >> 3;
+            const uint32_t slice = ((a.g_bytes + share - 1) / share + 127u) & ~127u;
+            const uint32_t o = tid * 128u;
+            if (o < slice) pf = __builtin_amdgcn_raw_buffer_load_b32(g_rsrc, (lin >> 3) * slice + o, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < kStage; ++i) {
+            const int q = tid + i * kFusedThreads;
+            if (q < quads) {
+                const int row = (q * 4) / O, col = q * 4 - row * O;
+                vec_t<float, 4> w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = v[i][e];
+                *reinterpret_cast<vec_t<float, 4> *>(lut_s + row * P + col) = w;
+            }
+        }
+        const int pad = P - O;
+        for (int k = tid; k < R * pad; k += kFusedThreads) lut_s[(k / pad) * P + O + k % pad] = 0.f;
+    }
+    if (!single)
+        for (int k = tid; k < R * P; k += kFusedThreads) rowbuf[k] = 0.f;
+
+    if (tid < kWaves * 8) tp[tid] = 0.f;
+
+    for (int tile0 = 0; tile0 < a.items; tile0 += kFusedThreads) {
+        const int n_tile = min(kFusedThreads, a.items - tile0);
+        const uint64_t r0 = r_next;
+        const bool valid = tid < n_tile;
+        const int code = rec_code(r0) & (R - 1);  // masks keep a corrupt record in range
+
+        // 1. one ballot per code bit: the item's rank among equal codes of
+        //    its wave, lane l's count of codes l, l + 64, ... in the wave
+        const uint64_t vmask = __ballot(valid);
+        uint64_t same = vmask;
+        uint64_t cm[kCodesPerLane];
+#pragma unroll
+        for (int i = 0; i < kCodesPerLane; ++i) cm[i] = vmask;
+        for (int c = 0; c < C; ++c) {
+            const uint64_t bc = __ballot(valid && ((code >> c) & 1));
+            same &= ((code >> c) & 1) ? bc : ~bc;
+#pragma unroll
+            for (int i = 0; i < kCodesPerLane; ++i)
+                if (i * kWave < R) cm[i] &= (((lane + i * kWave) >> c) & 1) ? bc : ~bc;
+        }
+        const int rank = __popcll(same & ((1ull << lane) - 1ull));
+#pragma unroll
+        for (int i = 0; i < kCodesPerLane; ++i)
+            if (lane + i * kWave < R) cnt[wave * R + lane + i * kWave] = __popcll(cm[i]);
+        __syncthreads();
+
+        // 2. thread k: row k's per-wave counts -> offsets inside the row,
+        //    row totals -> exclusive scan over rows
+        const int nscan = ((R + kWave - 1) / kWave) * kWave;  // whole waves
+        int h[kWaves];
+        int total = 0;
+        int incl = 0;
+        if (tid < nscan) {  // whole waves
+            const int kr = min(tid, R - 1);  // in-bounds reads, zeroed past R
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const int x = cnt[w * R + kr];
+                h[w] = total;
+                total += tid < R ? x : 0;
+            }
+            incl = wave_inclusive_scan(total);
+        }
+        if (R > kWave) {
+            if (tid < nscan && lane == kWave - 1) wtot[wave] = incl;
+            __syncthreads();
+            if (tid < nscan)
+                for (int w = 0; w < wave; ++w) incl += wtot[w];
+        }
+        if (tid < R) {
+            const int excl = incl - total;
+            off[tid] = excl;
+            if (tid == R - 1) off[R] = incl;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) cnt[w * R + tid] = excl + h[w];
+        }
+        __syncthreads();
+
+        // 3. stable placement: item order inside every row
+        if (valid) {
+            const int pos = cnt[wave * R + code] + rank;
+            sorted[pos] = static_cast<uint32_t>(tid) | (static_cast<uint32_t>(rec_r(r0) & 7) << 10);
+            us[pos] = rec_u(r0);
+        }
+        __syncthreads();
+        // the G touch's only use: a word of its own after the scan carries
+        if (tile0 == 0 && tid == 0) wtot[kWaves] = static_cast<int>(pf);
+
+        // 4. row walk. Per-lane values come from an opaque copy of the thread
+        //    id: hoisted out of the tile loop they would stay live across it.
+        int tidl = tid;
+        __asm__ volatile("" : "+v"(tidl));
+        const int g = tidl / S, j = tidl % S;
+        const int col = j * V;
+        const bool col_ok = col < O;
+        const uint32_t gcol = static_cast<uint32_t>(col) * 4u;
+        for (int k = g; k < R; k += NG) {
+            const int k0 = off[k], nk = off[k + 1] - k0;
+            const vec_t<float, V> lkv = *reinterpret_cast<const vec_t<float, V> *>(lut_s + k * P + col);
+            float acc[V];
+#pragma unroll
+            for (int e = 0; e < V; ++e) acc[e] = 0.f;
+            for (int p = 0; __ballot(p < nk) != 0; p += K) {  // wave-uniform trip count
+                uint32_t ent[K];
+                float gv[K][V];
+#pragma unroll
+                for (int i = 0; i < K; ++i) {
+                    const bool live = p + i < nk;
+                    ent[i] = sorted[(k0 + p + i) & (kFusedThreads - 1)];  // in bounds; dead ones masked below
+                    const uint32_t item = static_cast<uint32_t>(tile0) + (ent[i] & 1023u);
+                    buffer_row<float, V>(g_rsrc, live && col_ok ? item * static_cast<uint32_t>(O) * 4u + gcol : kOutOfRange,
+                                         0, gv[i]);
+                }
+                float d[K];
+#pragma unroll
+                for (int i = 0; i < K; ++i) {
+                    const int nb = (k ^ (1 << ((ent[i] >> 10) & 7u))) & (R - 1);
+                    const vec_t<float, V> lnv = *reinterpret_cast<const vec_t<float, V> *>(lut_s + nb * P + col);
+                    float s = 0.f;
+#pragma unroll
+                    for (int e = 0; e < V; ++e) {
+                        s += gv[i][e] * (lnv[e] - lkv[e]);
+                        acc[e] += gv[i][e];
+                    }
+                    d[i] = s;
+                }
+                if (need_gu) {
+                    const float dot = reduce_scatter<S, K>(d, j) * a.scale;
+                    const int q = (j / (S / K)) & (K - 1);  // the item whose dot this lane holds
+                    if (j % (S / K) == 0 && p + q < nk) {
+                        const uint32_t e = sorted[k0 + p + q];
+                        const int r = static_cast<int>((e >> 10) & 7u);
+                        const float gu = dot * fast_sigmoid_odd(us[k0 + p + q]);
+                        if (a.gurec != nullptr)
+                            a.gurec[static_cast<size_t>(t) * a.items + tile0 + (e & 1023u)] =
+                                static_cast<uint64_t>(__builtin_bit_cast(uint32_t, gu)) |
+                                (static_cast<uint64_t>(r) << 32);
+                        us[k0 + p + q] = gu;  // the position's margin is spent: it now holds gu
+                    }
+                }
+            }
+            // row k's sum over this tile: scaled and stored (one tile), or
+            // added to the row buffer (this group owns row k in every tile)
+            if (a.grad_lut != nullptr) {
+                if (single) {
+                    if (col_ok) {
+                        float y[V];
+#pragma unroll
+                        for (int e = 0; e < V; ++e) y[e] = acc[e] * a.scale;
+                        store_f32<V>(a.grad_lut + (static_cast<size_t>(t) * R + k) * O + col, y);
+                    }
+                } else {
+                    vec_t<float, V> *rb = reinterpret_cast<vec_t<float, V> *>(rowbuf + k * P + col);
+                    vec_t<float, V> w = *rb;
+#pragma unroll
+                    for (int e = 0; e < V; ++e) w[e] += acc[e];
+                    *rb = w;
+                }
+            }
+        }
+        if (tile0 + kFusedThreads < a.items) {
+            const bool nv = tile0 + kFusedThreads + tid < a.items;
+            r_next = nv ? rec_t[tile0 + kFusedThreads + tid] : 0ull;
+        }
+        __syncthreads();
+        // 5. threshold gradient of the tile: -gu at each sorted position's
+        //    min-margin comparison, a fixed tree per wave (lane 8c ends with
+        //    the wave's sum for comparison c) added to the wave's slots. The
+        //    next placement rewrites the sorted list only after two barriers.
+        if (a.grad_thr != nullptr) {
+            float tv[8];
+            const bool has = tid < n_tile;
+            const int r = has ? static_cast<int>((sorted[tid] >> 10) & 7u) : 0;
+            const float gu = has ? us[tid] : 0.f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) tv[c] = r == c ? -gu : 0.f;
+            const float tot = reduce_scatter<kWave, 8>(tv, lane);
+            if ((lane & 7) == 0) tp[wave * 8 + (lane >> 3)] += tot;
+        }
+    }
+
+    // 6. several tiles: the row buffer, scaled, written once
+    if (!single && a.grad_lut != nullptr) {
+        const int qp = P / 4;
+        for (int unit = tid; unit < R * qp; unit += kFusedThreads) {
+            const int k = unit / qp, c0 = (unit % qp) * 4;
+            if (c0 < O) {
+                float y[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[e] = rowbuf[k * P + c0 + e] * a.scale;
+                store_f32<4>(a.grad_lut + (static_cast<size_t>(t) * R + k) * O + c0, y);
+            }
+        }
+    }
+    // 7. threshold gradient: the waves' sums in wave order
+    if (a.grad_thr != nullptr) {
+        __syncthreads();
+        if (tid < C) {
+            float sum = tp[tid];
+            for (int w = 1; w < kWaves; ++w) sum += tp[w * 8 + tid];
+            a.grad_thr[t * C + tid] = sum;
+        }
+    }
+}
+
+// Input gradient of the fused path: one workgroup per item expands the item's
+// {gu, r} records (one per table) into signed slots and walks the inverse
+// anchor index as the item kernel does.
+struct ScatterArgs {
+    const uint64_t *gurec;  // [T][B]
+    const int32_t *index_offsets;
+    const int32_t *index_entries;
+    float *grad_x;
+    int items, in_f, tables, comps;
+};
+
+constexpr int kScatterThreads = 256;
+constexpr int kScatterIndex = 8;  // index words per thread in flight
+
+__global__ __launch_bounds__(kScatterThreads) void pairwise_bwd_scatter_kernel(ScatterArgs a) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int C = a.comps;
+    float *gud = reinterpret_cast<float *>(lds);                     // [T * C]
+    int *idx_s = reinterpret_cast<int *>(gud + a.tables * C);         // [in_f + 1 + 2 T C]
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const int nidx = a.in_f + 1 + 2 * a.tables * C;
+    for (int t0 = 0; t0 < a.tables; t0 += kScatterThreads) {
+        const int tt = t0 + tid;
+        const uint64_t rr = tt < a.tables ? a.gurec[static_cast<size_t>(tt) * a.items + b] : 0ull;
+        int iv[kScatterIndex];
+        const int kb = t0 == 0 ? 0 : nidx;  // the index goes out with the first records
+#pragma unroll
+        for (int q = 0; q < kScatterIndex; ++q) {
+            const int k = kb + tid + q * kScatterThreads;
+            iv[q] = k < nidx ? (k <= a.in_f ? a.index_offsets[k] : a.index_entries[k - a.in_f - 1]) : 0;
+        }
+#pragma unroll
+        for (int q = 0; q < kScatterIndex; ++q)
+            if (kb + tid + q * kScatterThreads < nidx) idx_s[kb + tid + q * kScatterThreads] = iv[q];
+        if (tt < a.tables) {
+            const float gu = __builtin_bit_cast(float, static_cast<uint32_t>(rr));
+            const int r = static_cast<int>(rr >> 32);
+            for (int c = 0; c < C; ++c) gud[tt * C + c] = c == r ? gu : 0.f;
+        }
+    }
+    for (int k = tid + kScatterIndex * kScatterThreads; k < nidx; k += kScatterThreads)
+        idx_s[k] = k <= a.in_f ? a.index_offsets[k] : a.index_entries[k - a.in_f - 1];
+    __syncthreads();
+    feature_walk(gud, idx_s, a.in_f, a.grad_x + static_cast<size_t>(b) * a.in_f, tid, kScatterThreads);
+}
+
 // Inverse anchor index: for every input feature f, the entries
 // ((t * C + c) << 1) | side of the anchors[t][c][side] equal to f, in
 // increasing order. One thread per feature scans the anchors, so the order is
@@ -628,6 +964,21 @@ template <typename T, int N>
 hipError_t launch_item_typed(const ItemArgs &args, const BackwardPlan &p, hipStream_t stream) {
     return launch_kernel(TROPNN_KERNEL_BACKWARD_ITEM, pairwise_bwd_item_kernel<T, N>, dim3(args.items),
                          dim3(p.item_threads), p.item_lds_bytes, stream, args);
+}
+
+template <typename T, int V, int S>
+hipError_t launch_fused_vs(const FusedArgs &args, const BackwardPlan &p, hipStream_t stream) {
+    auto kernel = pairwise_bwd_fused_kernel<T, V, S>;
+    if (hipError_t e = allow_lds(kernel, p.f_lds_bytes); e != hipSuccess) return e;
+    return launch_kernel(TROPNN_KERNEL_BACKWARD_FUSED, kernel, dim3(args.tables), dim3(kFusedThreads), p.f_lds_bytes,
+                         stream, args);
+}
+
+template <typename T>
+hipError_t launch_fused_typed(const FusedArgs &args, const BackwardPlan &p, hipStream_t stream) {
+    if (p.fvec == 4) return launch_fused_vs<T, 4, 16>(args, p, stream);
+    if (p.fslices == 16) return launch_fused_vs<T, 8, 16>(args, p, stream);
+    return launch_fused_vs<T, 8, 32>(args, p, stream);
 }
 
 __global__ void fill_zero_kernel(float *p, size_t n) {
@@ -706,7 +1057,6 @@ BackwardPlan plan_backward(const Dims &d) {
     p.o_chunk = p.slices * p.vec;
     p.o_chunks = (d.out_f + p.o_chunk - 1) / p.o_chunk;
     p.lut_threads = kLutThreads;
-    p.workspace_bytes = static_cast<size_t>(d.tables) * d.items * sizeof(float);
 
     // item kernel: N elements per lane as in the forward (the smallest power
     // of two whose 64-lane tile spans the row, 16 bytes at most, dividing the
@@ -726,6 +1076,39 @@ BackwardPlan plan_backward(const Dims &d) {
     p.item_waves = (d.tables + p.item_per_wave - 1) / p.item_per_wave;
     p.item_threads = p.item_waves * kWave;
     p.item_lds_bytes = (d.tables * d.comps + d.in_f + 1 + 2 * d.tables * d.comps) * 4;
+    p.scatter_lds_bytes = p.item_lds_bytes;
+
+    // fused path: the row group spans the row, lanes own whole V-column
+    // pieces of it (V = 4 up to 64 columns, else V = 8 and O % 8 == 0), and
+    // the table's rows fit in LDS
+    p.fused = false;
+    if (d.out_f % 4 == 0 && (d.out_f <= 64 || (d.out_f % 8 == 0 && d.out_f <= 256))) {
+        p.fvec = d.out_f <= 64 ? 4 : 8;
+        p.fslices = d.out_f <= 128 ? 16 : 32;
+        p.fpitch = p.fvec * p.fslices;
+        const bool single = d.items <= kFusedThreads;
+        const int waves = kFusedThreads / kWave;
+        int off = 0;
+        p.f_lut_off = off;
+        off += d.rows * p.fpitch * 4;
+        p.f_rowbuf_off = off;
+        off += single ? 0 : d.rows * p.fpitch * 4;
+        p.f_cnt_off = off;
+        off += waves * d.rows * 4;
+        p.f_off_off = off;
+        off += ((d.rows + 1) * 4 + 15) & ~15;
+        p.f_sorted_off = off;
+        off += kFusedThreads * 4;
+        p.f_u_off = off;
+        off += kFusedThreads * 4;
+        p.f_thr_off = off;
+        off += waves * 8 * 4;
+        p.f_wtot_off = off;
+        off += (waves + 1) * 4;
+        p.f_lds_bytes = off;
+        p.fused = d.rows * p.fpitch * 4 <= 64 * 1024 && off <= 160 * 1024;
+    }
+    p.workspace_bytes = static_cast<size_t>(d.tables) * d.items * (p.fused ? sizeof(uint64_t) : sizeof(float));
     return p;
 }
 
@@ -736,6 +1119,48 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
     const uint64_t *rec64 = reinterpret_cast<const uint64_t *>(rec);
     const int esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
     const uint32_t g_bytes = static_cast<uint32_t>(static_cast<size_t>(d.items) * d.out_f * 4);
+    if (p.fused) {
+        if (grad_x == nullptr && grad_thr == nullptr && grad_lut == nullptr) return hipSuccess;
+        uint64_t *gurec = grad_x != nullptr ? reinterpret_cast<uint64_t *>(workspace) : nullptr;
+        FusedArgs f{};
+        f.grad_out = grad_out;
+        f.lut = lut;
+        f.rec = rec64;
+        f.scale = scale;
+        f.grad_lut = grad_lut;
+        f.grad_thr = grad_thr;
+        f.gurec = gurec;
+        f.lut_bytes = static_cast<uint32_t>(static_cast<size_t>(d.tables) * d.rows * d.out_f * esize);
+        f.g_bytes = g_bytes;
+        f.items = d.items;
+        f.out_f = d.out_f;
+        f.tables = d.tables;
+        f.comps = d.comps;
+        f.rows = d.rows;
+        f.pitch = p.fpitch;
+        f.lut_off = p.f_lut_off;
+        f.cnt_off = p.f_cnt_off;
+        f.off_off = p.f_off_off;
+        f.sorted_off = p.f_sorted_off;
+        f.u_off = p.f_u_off;
+        f.rowbuf_off = p.f_rowbuf_off;
+        f.thr_off = p.f_thr_off;
+        f.wtot_off = p.f_wtot_off;
+        hipError_t e = d.lut_dtype == TROPNN_LUT_F16 ? launch_fused_typed<_Float16>(f, p, stream)
+                                                      : launch_fused_typed<float>(f, p, stream);
+        if (e != hipSuccess || grad_x == nullptr) return e;
+        ScatterArgs s{};
+        s.gurec = gurec;
+        s.index_offsets = index_offsets;
+        s.index_entries = index_entries;
+        s.grad_x = grad_x;
+        s.items = d.items;
+        s.in_f = d.in_f;
+        s.tables = d.tables;
+        s.comps = d.comps;
+        return launch_kernel(TROPNN_KERNEL_BACKWARD_SCATTER, pairwise_bwd_scatter_kernel, dim3(d.items),
+                             dim3(kScatterThreads), p.scatter_lds_bytes, stream, s);
+    }
     if (grad_x != nullptr || grad_thr != nullptr) {
         ItemArgs a{};
         a.grad_out = grad_out;

@@ -56,7 +56,18 @@ struct BackwardPlan {
     int item_waves;     // waves per workgroup (one item per workgroup)
     int item_threads;
     int item_lds_bytes; // the item's gu slots [T * C] f32 + the inverse anchor index
-    size_t workspace_bytes;  // gu [T][B] f32
+    // fused path (O a multiple of 4 up to 64, or of 8 up to 256, a table's LUT
+    // rows within 64 KB as f32): one kernel per table does the LUT gradient, the
+    // STE dots and the threshold gradient; a scatter kernel per item the input
+    // gradient. Otherwise the item and table kernels above.
+    bool fused;
+    int fvec;           // V: columns per lane
+    int fslices;        // S: lanes per row group, S * V >= O
+    int fpitch;         // S * V: LDS row pitch in floats
+    int f_lut_off, f_cnt_off, f_off_off, f_sorted_off, f_u_off, f_rowbuf_off, f_thr_off, f_wtot_off;  // LDS bytes
+    int f_lds_bytes;
+    int scatter_lds_bytes;   // gu slots [T * C] f32 + the inverse anchor index
+    size_t workspace_bytes;  // fused: {gu, r} [T][B] u64; else gu [T][B] f32
 };
 
 // Row loads a forward wave keeps in flight (its gather chunk), by LUT element
