@@ -583,8 +583,10 @@ struct FusedArgs {
     float *grad_thr;  // or null
     uint64_t *gurec;  // [T][B] {gu bits, r} for the scatter kernel, or null
     uint32_t lut_bytes, g_bytes;
-    int items, out_f, tables, comps, rows, pitch;
-    int lut_off, cnt_off, off_off, sorted_off, u_off, rowbuf_off, thr_off, wtot_off;  // LDS byte offsets
+    uint32_t g_slice;     // bytes of G one workgroup touches (8 XCDs share the table workgroups)
+    uint64_t quad_magic;  // ceil(2^32 / (out_f / 4)): chunk index -> LUT row
+    int items, out_f, tables, comps, rows;
+    int lut_off, cnt_off, off_off, sorted_off, u_off, rowbuf_off, thr_off, wtot_off, map_off;  // LDS byte offsets
 };
 
 // One workgroup per table; the row group of S lanes x V columns spans the
@@ -602,8 +604,8 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
     constexpr int kWaves = kFusedThreads / kWave;
     constexpr int NG = kFusedThreads / S;  // row groups
     constexpr int K = kFusedFloats / V;  // items per batch
-    constexpr int kCodesPerLane = (1 << TROPNN_MAX_COMPARISONS) / kWave;
     constexpr int kStage = 4;  // LUT chunks (4 elements) a thread stages, R * O <= 16384
+    constexpr int P = S * V;   // LDS row pitch in floats
     static_assert(K <= S, "a batch's dots are scattered over the row group");
     extern __shared__ __align__(16) unsigned char lds[];
     float *lut_s = reinterpret_cast<float *>(lds + a.lut_off);             // [R][pitch] table rows, f32
@@ -614,98 +616,100 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
     float *rowbuf = reinterpret_cast<float *>(lds + a.rowbuf_off);         // [R][pitch] (several tiles)
     float *tp = reinterpret_cast<float *>(lds + a.thr_off);                // [waves][8]
     int *wtot = reinterpret_cast<int *>(lds + a.wtot_off);                 // [waves] scan carries, [1] sink
+    int *rowmap = reinterpret_cast<int *>(lds + a.map_off);                // [R] rows in walk order (R <= 64)
 
     const int t = blockIdx.x;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int R = a.rows, C = a.comps, O = a.out_f, P = a.pitch;
+    const int R = a.rows, C = a.comps, O = a.out_f;
     const bool single = a.items <= kFusedThreads;
     const bool need_gu = a.grad_thr != nullptr || a.gurec != nullptr;
     const uint64_t *rec_t = a.rec + static_cast<size_t>(t) * a.items;
     const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.grad_out, a.g_bytes);
     const __amdgpu_buffer_rsrc_t lut_rsrc = buffer_rsrc(a.lut, a.lut_bytes);
 
-    // 0. first tile's record, the table's LUT rows (all loads in flight, then
-    //    LDS as f32 with zero columns past O), and a touch of one slice of G
-    //    per XCD as in the table kernel
-    uint64_t r_next = tid < a.items ? rec_t[tid] : 0ull;
-    uint32_t pf = 0u;
-    {
-        const int quads = R * O / 4;  // O % 4 == 0: no chunk crosses a row
-        const int tbase = t * R * O * static_cast<int>(sizeof(T));
-        float v[kStage][4];
-#pragma unroll
-        for (int i = 0; i < kStage; ++i) {
-            const int q = tid + i * kFusedThreads;
-            buffer_row<T, 4>(lut_rsrc, q < quads ? static_cast<uint32_t>(q) * 4u * sizeof(T) : kOutOfRange, tbase, v[i]);
-        }
-        {
-            const int nwg = gridDim.x;
-            const int lin = blockIdx.x;
-            const int share = (nwg - (lin & 7) + 7) >> 3;
-            const uint32_t slice = ((a.g_bytes + share - 1) / share + 127u) & ~127u;
-            const uint32_t o = tid * 128u;
-            if (o < slice) pf = __builtin_amdgcn_raw_buffer_load_b32(g_rsrc, (lin >> 3) * slice + o, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < kStage; ++i) {
-            const int q = tid + i * kFusedThreads;
-            if (q < quads) {
-                const int row = (q * 4) / O, col = q * 4 - row * O;
-                vec_t<float, 4> w;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) w[e] = v[i][e];
-                *reinterpret_cast<vec_t<float, 4> *>(lut_s + row * P + col) = w;
-            }
-        }
-        const int pad = P - O;
-        for (int k = tid; k < R * pad; k += kFusedThreads) lut_s[(k / pad) * P + O + k % pad] = 0.f;
-    }
-    if (!single)
-        for (int k = tid; k < R * P; k += kFusedThreads) rowbuf[k] = 0.f;
-
-    if (tid < kWaves * 8) tp[tid] = 0.f;
-
-    for (int tile0 = 0; tile0 < a.items; tile0 += kFusedThreads) {
-        const int n_tile = min(kFusedThreads, a.items - tile0);
-        const uint64_t r0 = r_next;
+    // 1. one ballot per code bit gives each item the mask of equal codes in
+    //    its wave: its rank is the count below it, and the first item of
+    //    each code writes the code's count to cnt[wave][code] after the wave
+    //    has zeroed its counts (one wave's LDS operations complete in order)
+    auto ballots = [&](uint64_t rr, int n_tile) -> int {
         const bool valid = tid < n_tile;
-        const int code = rec_code(r0) & (R - 1);  // masks keep a corrupt record in range
-
-        // 1. one ballot per code bit: the item's rank among equal codes of
-        //    its wave, lane l's count of codes l, l + 64, ... in the wave
-        const uint64_t vmask = __ballot(valid);
-        uint64_t same = vmask;
-        uint64_t cm[kCodesPerLane];
-#pragma unroll
-        for (int i = 0; i < kCodesPerLane; ++i) cm[i] = vmask;
+        const int code = rec_code(rr) & (R - 1);  // masks keep a corrupt record in range
+        for (int k = lane; k < R; k += kWave) cnt[wave * R + k] = 0;
+        if (wave * kWave >= n_tile) return 0;
+        uint64_t same = __ballot(valid);
         for (int c = 0; c < C; ++c) {
             const uint64_t bc = __ballot(valid && ((code >> c) & 1));
             same &= ((code >> c) & 1) ? bc : ~bc;
-#pragma unroll
-            for (int i = 0; i < kCodesPerLane; ++i)
-                if (i * kWave < R) cm[i] &= (((lane + i * kWave) >> c) & 1) ? bc : ~bc;
         }
         const int rank = __popcll(same & ((1ull << lane) - 1ull));
+        if (valid && rank == 0) cnt[wave * R + code] = __popcll(same);
+        return rank;
+    };
+
+    // 0. first tile's record, the table's LUT rows and a touch of one slice
+    //    of G per XCD (workgroups are dealt to the 8 XCDs in turn, so the
+    //    grad rows the walk gathers are L2 hits by then); the first ballots
+    //    need the record only, and the LUT rows go to LDS after them
+    uint64_t r0 = tid < a.items ? rec_t[tid] : 0ull;
+    float lv[kStage][4];
+    const int quads = R * O / 4;  // 4-element chunks; O % 4 == 0, so none crosses a row
+    {
+        const int tbase = t * R * O * static_cast<int>(sizeof(T));
 #pragma unroll
-        for (int i = 0; i < kCodesPerLane; ++i)
-            if (lane + i * kWave < R) cnt[wave * R + lane + i * kWave] = __popcll(cm[i]);
-        __syncthreads();
+        for (int i = 0; i < kStage; ++i) {
+            const int q = tid + i * kFusedThreads;
+            buffer_row<T, 4>(lut_rsrc, q < quads ? static_cast<uint32_t>(q) * 4u * sizeof(T) : kOutOfRange, tbase, lv[i]);
+        }
+    }
+    const uint32_t touch = static_cast<uint32_t>(t >> 3) * a.g_slice + tid * 128u;
+    const uint32_t pf = tid * 128u < a.g_slice ? __builtin_amdgcn_raw_buffer_load_b32(g_rsrc, touch, 0, 0) : 0u;
+    int rank = ballots(r0, min(kFusedThreads, a.items));
+#pragma unroll
+    for (int i = 0; i < kStage; ++i) {
+        const int q = tid + i * kFusedThreads;
+        if (q < quads) {
+            // row = q / (O / 4) by a host-computed reciprocal (exact for q < 2^16)
+            const int row = static_cast<int>((static_cast<uint64_t>(q) * a.quad_magic) >> 32);
+            const int col = q * 4 - row * O;
+            vec_t<float, 4> w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = lv[i][e];
+            *reinterpret_cast<vec_t<float, 4> *>(lut_s + row * P + col) = w;
+        }
+    }
+    if (tid < R)
+        for (int e = O; e < P; e += 4) *reinterpret_cast<vec_t<float, 4> *>(lut_s + tid * P + e) = 0.f;
+    if (!single)
+        for (int k = tid * 4; k < R * P; k += kFusedThreads * 4) *reinterpret_cast<vec_t<float, 4> *>(rowbuf + k) = 0.f;
+    if (tid < kWaves * 8) tp[tid] = 0.f;
+    __syncthreads();
+
+    for (int tile0 = 0;;) {
+        const int n_tile = min(kFusedThreads, a.items - tile0);
+        // per-lane values inside the loop come from an opaque copy of the
+        // thread id: hoisted out of the loop (the scan's 32 LDS addresses,
+        // the walk's lane offsets) they would stay live across the walk
+        int tidl = tid;
+        __asm__ volatile("" : "+v"(tidl));
 
         // 2. thread k: row k's per-wave counts -> offsets inside the row,
-        //    row totals -> exclusive scan over rows
+        //    row totals -> exclusive scan over rows. With at most 64 rows the
+        //    scanning wave also orders the rows by batch count (most batches
+        //    first, then row order), so that the four row groups of a wave
+        //    get rows of similar length.
         const int nscan = ((R + kWave - 1) / kWave) * kWave;  // whole waves
         int h[kWaves];
         int total = 0;
         int incl = 0;
-        if (tid < nscan) {  // whole waves
-            const int kr = min(tid, R - 1);  // in-bounds reads, zeroed past R
+        if (tid < nscan) {
+            const int kr = min(tidl, R - 1);  // in-bounds reads, zeroed past R
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) {
                 const int x = cnt[w * R + kr];
                 h[w] = total;
-                total += tid < R ? x : 0;
+                total += tidl < R ? x : 0;
             }
             incl = wave_inclusive_scan(total);
         }
@@ -714,35 +718,42 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
             __syncthreads();
             if (tid < nscan)
                 for (int w = 0; w < wave; ++w) incl += wtot[w];
+        } else if (wave == 0) {
+            const int key = tid < R ? min((total + K - 1) / K, 15) : -1;  // batches, capped
+            int placed = 0;
+            for (int v = 0; placed < R; ++v) {  // ascending keys fill the order from its end
+                const uint64_t m = __ballot(key == v);
+                const int nv = __popcll(m);
+                if (key == v) rowmap[R - placed - nv + __popcll(m & ((1ull << lane) - 1ull))] = tid;
+                placed += nv;
+            }
         }
         if (tid < R) {
             const int excl = incl - total;
-            off[tid] = excl;
+            off[tidl] = excl;
             if (tid == R - 1) off[R] = incl;
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) cnt[w * R + tid] = excl + h[w];
+            for (int w = 0; w < kWaves; ++w) cnt[w * R + tidl] = excl + h[w];
         }
         __syncthreads();
 
         // 3. stable placement: item order inside every row
-        if (valid) {
-            const int pos = cnt[wave * R + code] + rank;
-            sorted[pos] = static_cast<uint32_t>(tid) | (static_cast<uint32_t>(rec_r(r0) & 7) << 10);
+        if (tid < n_tile) {
+            const int pos = cnt[wave * R + (rec_code(r0) & (R - 1))] + rank;
+            sorted[pos] = static_cast<uint32_t>(tidl) | (static_cast<uint32_t>(rec_r(r0) & 7) << 10);
             us[pos] = rec_u(r0);
         }
         __syncthreads();
         // the G touch's only use: a word of its own after the scan carries
         if (tile0 == 0 && tid == 0) wtot[kWaves] = static_cast<int>(pf);
 
-        // 4. row walk. Per-lane values come from an opaque copy of the thread
-        //    id: hoisted out of the tile loop they would stay live across it.
-        int tidl = tid;
-        __asm__ volatile("" : "+v"(tidl));
+        // 4. row walk
         const int g = tidl / S, j = tidl % S;
         const int col = j * V;
         const bool col_ok = col < O;
         const uint32_t gcol = static_cast<uint32_t>(col) * 4u;
-        for (int k = g; k < R; k += NG) {
+        for (int kk = g; kk < R; kk += NG) {
+            const int k = R <= kWave ? rowmap[kk] : kk;
             const int k0 = off[k], nk = off[k + 1] - k0;
             const vec_t<float, V> lkv = *reinterpret_cast<const vec_t<float, V> *>(lut_s + k * P + col);
             float acc[V];
@@ -752,12 +763,15 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
                 uint32_t ent[K];
                 float gv[K][V];
 #pragma unroll
-                for (int i = 0; i < K; ++i) {
-                    const bool live = p + i < nk;
+                for (int i = 0; i < K; ++i)
                     ent[i] = sorted[(k0 + p + i) & (kFusedThreads - 1)];  // in bounds; dead ones masked below
+#pragma unroll
+                for (int i = 0; i < K; ++i) {
+                    // dead lanes set bit 31 (G is at most 2 GiB, so live
+                    // offsets stay below it): an out-of-range load of zeros
                     const uint32_t item = static_cast<uint32_t>(tile0) + (ent[i] & 1023u);
-                    buffer_row<float, V>(g_rsrc, live && col_ok ? item * static_cast<uint32_t>(O) * 4u + gcol : kOutOfRange,
-                                         0, gv[i]);
+                    const uint32_t dead = p + i < nk && col_ok ? 0u : kOutOfRange;
+                    buffer_row<float, V>(g_rsrc, (item * static_cast<uint32_t>(O) * 4u + gcol) | dead, 0, gv[i]);
                 }
                 float d[K];
 #pragma unroll
@@ -788,7 +802,8 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
                 }
             }
             // row k's sum over this tile: scaled and stored (one tile), or
-            // added to the row buffer (this group owns row k in every tile)
+            // added to the row buffer (rows of a tile are disjoint across
+            // groups, and tiles are separated by barriers)
             if (a.grad_lut != nullptr) {
                 if (single) {
                     if (col_ok) {
@@ -806,30 +821,32 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
                 }
             }
         }
-        if (tile0 + kFusedThreads < a.items) {
-            const bool nv = tile0 + kFusedThreads + tid < a.items;
-            r_next = nv ? rec_t[tile0 + kFusedThreads + tid] : 0ull;
-        }
+        const int next = tile0 + kFusedThreads;
+        if (next < a.items) r0 = next + tid < a.items ? rec_t[next + tid] : 0ull;
         __syncthreads();
         // 5. threshold gradient of the tile: -gu at each sorted position's
         //    min-margin comparison, a fixed tree per wave (lane 8c ends with
         //    the wave's sum for comparison c) added to the wave's slots. The
         //    next placement rewrites the sorted list only after two barriers.
-        if (a.grad_thr != nullptr) {
+        if (a.grad_thr != nullptr && wave * kWave < n_tile) {
             float tv[8];
             const bool has = tid < n_tile;
-            const int r = has ? static_cast<int>((sorted[tid] >> 10) & 7u) : 0;
-            const float gu = has ? us[tid] : 0.f;
+            const int r = has ? static_cast<int>((sorted[tidl] >> 10) & 7u) : 0;
+            const float gu = has ? us[tidl] : 0.f;
 #pragma unroll
             for (int c = 0; c < 8; ++c) tv[c] = r == c ? -gu : 0.f;
             const float tot = reduce_scatter<kWave, 8>(tv, lane);
             if ((lane & 7) == 0) tp[wave * 8 + (lane >> 3)] += tot;
         }
+        if (next >= a.items) break;
+        tile0 = next;
+        rank = ballots(r0, min(kFusedThreads, a.items - tile0));
+        __syncthreads();
     }
 
     // 6. several tiles: the row buffer, scaled, written once
     if (!single && a.grad_lut != nullptr) {
-        const int qp = P / 4;
+        constexpr int qp = P / 4;
         for (int unit = tid; unit < R * qp; unit += kFusedThreads) {
             const int k = unit / qp, c0 = (unit % qp) * 4;
             if (c0 < O) {
@@ -1105,6 +1122,8 @@ BackwardPlan plan_backward(const Dims &d) {
         off += waves * 8 * 4;
         p.f_wtot_off = off;
         off += (waves + 1) * 4;
+        p.f_map_off = off;
+        off += d.rows * 4;
         p.f_lds_bytes = off;
         p.fused = d.rows * p.fpitch * 4 <= 64 * 1024 && off <= 160 * 1024;
     }
@@ -1137,7 +1156,9 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
         f.tables = d.tables;
         f.comps = d.comps;
         f.rows = d.rows;
-        f.pitch = p.fpitch;
+        f.g_slice = static_cast<uint32_t>(((g_bytes + (d.tables + 7) / 8 - 1) / ((d.tables + 7) / 8) + 127) & ~127u);
+        f.quad_magic = ((uint64_t{1} << 32) + d.out_f / 4 - 1) / (d.out_f / 4);
+        f.map_off = p.f_map_off;
         f.lut_off = p.f_lut_off;
         f.cnt_off = p.f_cnt_off;
         f.off_off = p.f_off_off;
