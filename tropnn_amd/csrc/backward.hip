@@ -573,6 +573,7 @@ __global__ __launch_bounds__(kLutThreads) void pairwise_bwd_table_kernel(LutArgs
 
 constexpr int kFusedThreads = 1024;  // threads of a fused workgroup = items per sort tile
 constexpr int kFusedFloats = 32;     // grad-row floats a lane has in flight: 32 / V items per batch
+constexpr uint32_t kPadSlot = 0x80000000u;  // sorted-entry flag of a row's padding slot
 
 struct FusedArgs {
     const float *grad_out;
@@ -586,6 +587,7 @@ struct FusedArgs {
     uint32_t g_slice;     // bytes of G one workgroup touches (8 XCDs share the table workgroups)
     uint64_t quad_magic;  // ceil(2^32 / (out_f / 4)): chunk index -> LUT row
     int items, out_f, tables, comps, rows;
+    int slots;  // sorted-list capacity: a tile's items plus K - 1 padding slots per row
     int lut_off, cnt_off, off_off, sorted_off, u_off, rowbuf_off, thr_off, wtot_off, map_off;  // LDS byte offsets
 };
 
@@ -611,8 +613,8 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
     float *lut_s = reinterpret_cast<float *>(lds + a.lut_off);             // [R][pitch] table rows, f32
     int *cnt = reinterpret_cast<int *>(lds + a.cnt_off);                   // [waves][R] counts -> offsets
     int *off = reinterpret_cast<int *>(lds + a.off_off);                   // [R + 1] row starts
-    uint32_t *sorted = reinterpret_cast<uint32_t *>(lds + a.sorted_off);  // [tile] item | r << 10
-    float *us = reinterpret_cast<float *>(lds + a.u_off);                  // [tile] margin u, by position
+    uint2 *ent = reinterpret_cast<uint2 *>(lds + a.sorted_off);           // [slots] sorted entries (see below)
+    float *us = reinterpret_cast<float *>(lds + a.u_off);                  // [slots] margin u, by position
     float *rowbuf = reinterpret_cast<float *>(lds + a.rowbuf_off);         // [R][pitch] (several tiles)
     float *tp = reinterpret_cast<float *>(lds + a.thr_off);                // [waves][8]
     int *wtot = reinterpret_cast<int *>(lds + a.wtot_off);                 // [waves] scan carries, [1] sink
@@ -684,6 +686,10 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
     if (!single)
         for (int k = tid * 4; k < R * P; k += kFusedThreads * 4) *reinterpret_cast<vec_t<float, 4> *>(rowbuf + k) = 0.f;
     if (tid < kWaves * 8) tp[tid] = 0.f;
+    if (tid < K) {  // sentinel slots for row groups past their row
+        ent[a.slots + tid] = make_uint2(kOutOfRange, kPadSlot);
+        us[a.slots + tid] = 0.f;
+    }
     __syncthreads();
 
     for (int tile0 = 0;;) {
@@ -703,6 +709,7 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
         int h[kWaves];
         int total = 0;
         int incl = 0;
+        int padded = 0;  // row length rounded up to whole batches
         if (tid < nscan) {
             const int kr = min(tidl, R - 1);  // in-bounds reads, zeroed past R
 #pragma unroll
@@ -711,7 +718,8 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
                 h[w] = total;
                 total += tidl < R ? x : 0;
             }
-            incl = wave_inclusive_scan(total);
+            padded = (total + K - 1) / K * K;
+            incl = wave_inclusive_scan(padded);
         }
         if (R > kWave) {
             if (tid < nscan && lane == kWave - 1) wtot[wave] = incl;
@@ -719,7 +727,7 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
             if (tid < nscan)
                 for (int w = 0; w < wave; ++w) incl += wtot[w];
         } else if (wave == 0) {
-            const int key = tid < R ? min((total + K - 1) / K, 15) : -1;  // batches, capped
+            const int key = tid < R ? min(padded / K, 15) : -1;  // batches, capped
             int placed = 0;
             for (int v = 0; placed < R; ++v) {  // ascending keys fill the order from its end
                 const uint64_t m = __ballot(key == v);
@@ -729,18 +737,28 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
             }
         }
         if (tid < R) {
-            const int excl = incl - total;
+            const int excl = incl - padded;
             off[tidl] = excl;
             if (tid == R - 1) off[R] = incl;
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) cnt[w * R + tidl] = excl + h[w];
+            // the row's padding slots: grad rows out of range (zeros), no gu
+            for (int q = excl + total; q < excl + padded; ++q) {
+                ent[q] = make_uint2(kOutOfRange, kPadSlot);
+                us[q] = 0.f;
+            }
         }
         __syncthreads();
 
-        // 3. stable placement: item order inside every row
+        // 3. stable placement: item order inside every row. An entry holds
+        //    the item's grad-row byte offset, and the LDS byte offset of its
+        //    neighbour row nb | r << 18 | item << 21.
         if (tid < n_tile) {
-            const int pos = cnt[wave * R + (rec_code(r0) & (R - 1))] + rank;
-            sorted[pos] = static_cast<uint32_t>(tidl) | (static_cast<uint32_t>(rec_r(r0) & 7) << 10);
+            const int code = rec_code(r0) & (R - 1), r = rec_r(r0) & 7;
+            const int pos = cnt[wave * R + code] + rank;
+            const uint32_t nbo = static_cast<uint32_t>((code ^ (1 << r)) & (R - 1)) * (P * 4u);
+            ent[pos] = make_uint2(static_cast<uint32_t>(tile0 + tidl) * static_cast<uint32_t>(O) * 4u,
+                                  nbo | (static_cast<uint32_t>(r) << 18) | (static_cast<uint32_t>(tidl) << 21));
             us[pos] = rec_u(r0);
         }
         __syncthreads();
@@ -752,32 +770,31 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
         const int col = j * V;
         const bool col_ok = col < O;
         const uint32_t gcol = static_cast<uint32_t>(col) * 4u;
+        const uint32_t coldead = col_ok ? 0u : kOutOfRange;
+        const unsigned char *lut_b = reinterpret_cast<const unsigned char *>(lut_s) + col * 4;
         for (int kk = g; kk < R; kk += NG) {
             const int k = R <= kWave ? rowmap[kk] : kk;
-            const int k0 = off[k], nk = off[k + 1] - k0;
+            const int k0 = off[k], np = off[k + 1] - k0;  // np: whole batches
             const vec_t<float, V> lkv = *reinterpret_cast<const vec_t<float, V> *>(lut_s + k * P + col);
             float acc[V];
 #pragma unroll
             for (int e = 0; e < V; ++e) acc[e] = 0.f;
-            for (int p = 0; __ballot(p < nk) != 0; p += K) {  // wave-uniform trip count
-                uint32_t ent[K];
+            for (int p = 0; __ballot(p < np) != 0; p += K) {  // wave-uniform trip count
+                // a group past its row reads the K sentinel slots after the
+                // list: every load out of range, no gu
+                const bool gdone = p >= np;
+                const int base = gdone ? a.slots : k0 + p;
+                const uint32_t dead = coldead;
+                uint2 en[K];
+#pragma unroll
+                for (int i = 0; i < K; ++i) en[i] = ent[base + i];
                 float gv[K][V];
 #pragma unroll
-                for (int i = 0; i < K; ++i)
-                    ent[i] = sorted[(k0 + p + i) & (kFusedThreads - 1)];  // in bounds; dead ones masked below
-#pragma unroll
-                for (int i = 0; i < K; ++i) {
-                    // dead lanes set bit 31 (G is at most 2 GiB, so live
-                    // offsets stay below it): an out-of-range load of zeros
-                    const uint32_t item = static_cast<uint32_t>(tile0) + (ent[i] & 1023u);
-                    const uint32_t dead = p + i < nk && col_ok ? 0u : kOutOfRange;
-                    buffer_row<float, V>(g_rsrc, (item * static_cast<uint32_t>(O) * 4u + gcol) | dead, 0, gv[i]);
-                }
+                for (int i = 0; i < K; ++i) buffer_row<float, V>(g_rsrc, (en[i].x + gcol) | dead, 0, gv[i]);
                 float d[K];
 #pragma unroll
                 for (int i = 0; i < K; ++i) {
-                    const int nb = (k ^ (1 << ((ent[i] >> 10) & 7u))) & (R - 1);
-                    const vec_t<float, V> lnv = *reinterpret_cast<const vec_t<float, V> *>(lut_s + nb * P + col);
+                    const vec_t<float, V> lnv = *reinterpret_cast<const vec_t<float, V> *>(lut_b + (en[i].y & 0x3ffffu));
                     float s = 0.f;
 #pragma unroll
                     for (int e = 0; e < V; ++e) {
@@ -789,15 +806,15 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
                 if (need_gu) {
                     const float dot = reduce_scatter<S, K>(d, j) * a.scale;
                     const int q = (j / (S / K)) & (K - 1);  // the item whose dot this lane holds
-                    if (j % (S / K) == 0 && p + q < nk) {
-                        const uint32_t e = sorted[k0 + p + q];
-                        const int r = static_cast<int>((e >> 10) & 7u);
-                        const float gu = dot * fast_sigmoid_odd(us[k0 + p + q]);
+                    const uint32_t y = ent[base + q].y;
+                    if (j % (S / K) == 0 && (y & kPadSlot) == 0) {
+                        const int r = static_cast<int>((y >> 18) & 7u);
+                        const float gu = dot * fast_sigmoid_odd(us[base + q]);
                         if (a.gurec != nullptr)
-                            a.gurec[static_cast<size_t>(t) * a.items + tile0 + (e & 1023u)] =
+                            a.gurec[static_cast<size_t>(t) * a.items + tile0 + ((y >> 21) & 1023u)] =
                                 static_cast<uint64_t>(__builtin_bit_cast(uint32_t, gu)) |
                                 (static_cast<uint64_t>(r) << 32);
-                        us[k0 + p + q] = gu;  // the position's margin is spent: it now holds gu
+                        us[base + q] = gu;  // the position's margin is spent: it now holds gu
                     }
                 }
             }
@@ -828,15 +845,21 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
         //    min-margin comparison, a fixed tree per wave (lane 8c ends with
         //    the wave's sum for comparison c) added to the wave's slots. The
         //    next placement rewrites the sorted list only after two barriers.
-        if (a.grad_thr != nullptr && wave * kWave < n_tile) {
-            float tv[8];
-            const bool has = tid < n_tile;
-            const int r = has ? static_cast<int>((sorted[tidl] >> 10) & 7u) : 0;
-            const float gu = has ? us[tidl] : 0.f;
+        if (a.grad_thr != nullptr) {  // padding slots hold gu = 0
+            const int slots = off[R];
+            if (wave * kWave < slots) {
+                float tv[8];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) tv[c] = r == c ? -gu : 0.f;
-            const float tot = reduce_scatter<kWave, 8>(tv, lane);
-            if ((lane & 7) == 0) tp[wave * 8 + (lane >> 3)] += tot;
+                for (int c = 0; c < 8; ++c) tv[c] = 0.f;
+                for (int q = tidl; q < slots; q += kFusedThreads) {
+                    const int r = static_cast<int>((ent[q].y >> 18) & 7u);
+                    const float gu = us[q];
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) tv[c] += r == c ? -gu : 0.f;
+                }
+                const float tot = reduce_scatter<kWave, 8>(tv, lane);
+                if ((lane & 7) == 0) tp[wave * 8 + (lane >> 3)] += tot;
+            }
         }
         if (next >= a.items) break;
         tile0 = next;
@@ -1114,10 +1137,13 @@ BackwardPlan plan_backward(const Dims &d) {
         off += waves * d.rows * 4;
         p.f_off_off = off;
         off += ((d.rows + 1) * 4 + 15) & ~15;
+        const int batch = kFusedFloats / p.fvec;
+        p.f_slots = kFusedThreads + d.rows * (batch - 1);
+        off = (off + 7) & ~7;
         p.f_sorted_off = off;
-        off += kFusedThreads * 4;
+        off += (p.f_slots + batch) * 8;  // entries, then the sentinel slots
         p.f_u_off = off;
-        off += kFusedThreads * 4;
+        off += (p.f_slots + batch) * 4;
         p.f_thr_off = off;
         off += waves * 8 * 4;
         p.f_wtot_off = off;
@@ -1159,6 +1185,7 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
         f.g_slice = static_cast<uint32_t>(((g_bytes + (d.tables + 7) / 8 - 1) / ((d.tables + 7) / 8) + 127) & ~127u);
         f.quad_magic = ((uint64_t{1} << 32) + d.out_f / 4 - 1) / (d.out_f / 4);
         f.map_off = p.f_map_off;
+        f.slots = p.f_slots;
         f.lut_off = p.f_lut_off;
         f.cnt_off = p.f_cnt_off;
         f.off_off = p.f_off_off;
