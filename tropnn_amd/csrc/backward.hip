@@ -588,7 +588,7 @@ struct FusedArgs {
     uint64_t quad_magic;  // ceil(2^32 / (out_f / 4)): chunk index -> LUT row
     int items, out_f, tables, comps, rows;
     int slots;  // sorted-list capacity: a tile's items plus K - 1 padding slots per row
-    int lut_off, cnt_off, off_off, sorted_off, u_off, rowbuf_off, thr_off, wtot_off, map_off;  // LDS byte offsets
+    int lut_off, cnt_off, off_off, sorted_off, u_off, rowbuf_off, thr_off, wtot_off, part_off, brow_off;  // LDS bytes
 };
 
 // One workgroup per table; the row group of S lanes x V columns spans the
@@ -618,7 +618,8 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
     float *rowbuf = reinterpret_cast<float *>(lds + a.rowbuf_off);         // [R][pitch] (several tiles)
     float *tp = reinterpret_cast<float *>(lds + a.thr_off);                // [waves][8]
     int *wtot = reinterpret_cast<int *>(lds + a.wtot_off);                 // [waves] scan carries, [1] sink
-    int *rowmap = reinterpret_cast<int *>(lds + a.map_off);                // [R] rows in walk order (R <= 64)
+    float *part = reinterpret_cast<float *>(lds + a.part_off);             // [groups][2][pitch] split rows
+    int *brow = reinterpret_cast<int *>(lds + a.brow_off);                 // [slots / K] row of each batch
 
     const int t = blockIdx.x;
     const int tid = threadIdx.x;
@@ -701,15 +702,14 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
         __asm__ volatile("" : "+v"(tidl));
 
         // 2. thread k: row k's per-wave counts -> offsets inside the row,
-        //    row totals -> exclusive scan over rows. With at most 64 rows the
-        //    scanning wave also orders the rows by batch count (most batches
-        //    first, then row order), so that the four row groups of a wave
-        //    get rows of similar length.
+        //    row totals rounded up to whole batches of K slots -> exclusive
+        //    scan over rows. The row's padding slots get sentinels (grad rows
+        //    out of range, no gu) and its batches are recorded in brow.
         const int nscan = ((R + kWave - 1) / kWave) * kWave;  // whole waves
         int h[kWaves];
         int total = 0;
         int incl = 0;
-        int padded = 0;  // row length rounded up to whole batches
+        int padded = 0;
         if (tid < nscan) {
             const int kr = min(tidl, R - 1);  // in-bounds reads, zeroed past R
 #pragma unroll
@@ -726,15 +726,6 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
             __syncthreads();
             if (tid < nscan)
                 for (int w = 0; w < wave; ++w) incl += wtot[w];
-        } else if (wave == 0) {
-            const int key = tid < R ? min(padded / K, 15) : -1;  // batches, capped
-            int placed = 0;
-            for (int v = 0; placed < R; ++v) {  // ascending keys fill the order from its end
-                const uint64_t m = __ballot(key == v);
-                const int nv = __popcll(m);
-                if (key == v) rowmap[R - placed - nv + __popcll(m & ((1ull << lane) - 1ull))] = tid;
-                placed += nv;
-            }
         }
         if (tid < R) {
             const int excl = incl - padded;
@@ -742,11 +733,11 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
             if (tid == R - 1) off[R] = incl;
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) cnt[w * R + tidl] = excl + h[w];
-            // the row's padding slots: grad rows out of range (zeros), no gu
             for (int q = excl + total; q < excl + padded; ++q) {
                 ent[q] = make_uint2(kOutOfRange, kPadSlot);
                 us[q] = 0.f;
             }
+            for (int bb = excl / K; bb < incl / K; ++bb) brow[bb] = tidl;
         }
         __syncthreads();
 
@@ -765,83 +756,133 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
         // the G touch's only use: a word of its own after the scan carries
         if (tile0 == 0 && tid == 0) wtot[kWaves] = static_cast<int>(pf);
 
-        // 4. row walk
+        // 4. walk. The batches (rows in order, K slots each) are dealt out as
+        //    contiguous ranges of lo or lo + 1 batches, the longer ones to the
+        //    first row groups, so the four groups of a wave get equal counts
+        //    except in one wave, however the codes are spread. A group sums
+        //    each row's grad rows over its batches in registers: a row lying
+        //    wholly in the range is finished there, a row crossing the
+        //    range's start (end) leaves its partial sum in the group's slot 0
+        //    (1) for the combine step.
+        const int nb_all = off[R] / K;
+        const int lo = nb_all / NG, extra = nb_all - lo * NG;
         const int g = tidl / S, j = tidl % S;
+        const int b_begin = g * lo + min(g, extra), b_end = b_begin + lo + (g < extra ? 1 : 0);
         const int col = j * V;
         const bool col_ok = col < O;
         const uint32_t gcol = static_cast<uint32_t>(col) * 4u;
         const uint32_t coldead = col_ok ? 0u : kOutOfRange;
         const unsigned char *lut_b = reinterpret_cast<const unsigned char *>(lut_s) + col * 4;
-        for (int kk = g; kk < R; kk += NG) {
-            const int k = R <= kWave ? rowmap[kk] : kk;
-            const int k0 = off[k], np = off[k + 1] - k0;  // np: whole batches
-            const vec_t<float, V> lkv = *reinterpret_cast<const vec_t<float, V> *>(lut_s + k * P + col);
-            float acc[V];
+        int cur = -1;  // row being summed
+        vec_t<float, V> lkv = 0.f;
+        float acc[V];
 #pragma unroll
-            for (int e = 0; e < V; ++e) acc[e] = 0.f;
-            for (int p = 0; __ballot(p < np) != 0; p += K) {  // wave-uniform trip count
-                // a group past its row reads the K sentinel slots after the
-                // list: every load out of range, no gu
-                const bool gdone = p >= np;
-                const int base = gdone ? a.slots : k0 + p;
-                const uint32_t dead = coldead;
-                uint2 en[K];
+        for (int e = 0; e < V; ++e) acc[e] = 0.f;
+        auto finish = [&](int k) {  // row k's sum over this range
+            const int fb = off[k] / K, lb = off[k + 1] / K - 1;
+            if (fb >= b_begin && lb < b_end) {
+                if (a.grad_lut != nullptr) {
+                    if (single) {
+                        if (col_ok) {
+                            float y[V];
 #pragma unroll
-                for (int i = 0; i < K; ++i) en[i] = ent[base + i];
-                float gv[K][V];
+                            for (int e = 0; e < V; ++e) y[e] = acc[e] * a.scale;
+                            store_f32<V>(a.grad_lut + (static_cast<size_t>(t) * R + k) * O + col, y);
+                        }
+                    } else {
+                        vec_t<float, V> *rb = reinterpret_cast<vec_t<float, V> *>(rowbuf + k * P + col);
+                        vec_t<float, V> w = *rb;
 #pragma unroll
-                for (int i = 0; i < K; ++i) buffer_row<float, V>(g_rsrc, (en[i].x + gcol) | dead, 0, gv[i]);
-                float d[K];
-#pragma unroll
-                for (int i = 0; i < K; ++i) {
-                    const vec_t<float, V> lnv = *reinterpret_cast<const vec_t<float, V> *>(lut_b + (en[i].y & 0x3ffffu));
-                    float s = 0.f;
-#pragma unroll
-                    for (int e = 0; e < V; ++e) {
-                        s += gv[i][e] * (lnv[e] - lkv[e]);
-                        acc[e] += gv[i][e];
+                        for (int e = 0; e < V; ++e) w[e] += acc[e];
+                        *rb = w;
                     }
-                    d[i] = s;
                 }
-                if (need_gu) {
-                    const float dot = reduce_scatter<S, K>(d, j) * a.scale;
-                    const int q = (j / (S / K)) & (K - 1);  // the item whose dot this lane holds
-                    const uint32_t y = ent[base + q].y;
-                    if (j % (S / K) == 0 && (y & kPadSlot) == 0) {
-                        const int r = static_cast<int>((y >> 18) & 7u);
-                        const float gu = dot * fast_sigmoid_odd(us[base + q]);
-                        if (a.gurec != nullptr)
-                            a.gurec[static_cast<size_t>(t) * a.items + tile0 + ((y >> 21) & 1023u)] =
-                                static_cast<uint64_t>(__builtin_bit_cast(uint32_t, gu)) |
-                                (static_cast<uint64_t>(r) << 32);
-                        us[base + q] = gu;  // the position's margin is spent: it now holds gu
-                    }
+            } else {
+                vec_t<float, V> w;
+#pragma unroll
+                for (int e = 0; e < V; ++e) w[e] = acc[e];
+                *reinterpret_cast<vec_t<float, V> *>(part + (g * 2 + (fb < b_begin ? 0 : 1)) * P + col) = w;
+            }
+        };
+        for (int i = 0; __ballot(b_begin + i < b_end) != 0; ++i) {  // wave-uniform trip count
+            const int bt = b_begin + i;
+            const bool live = bt < b_end;
+            const int k = live ? brow[bt] : cur;
+            if (k != cur) {
+                if (cur >= 0) finish(cur);
+                cur = k;
+                lkv = *reinterpret_cast<const vec_t<float, V> *>(lut_s + k * P + col);
+#pragma unroll
+                for (int e = 0; e < V; ++e) acc[e] = 0.f;
+            }
+            // a group past its range reads the K sentinel slots after the
+            // list: every load out of range, no gu
+            const int base = live ? bt * K : a.slots;
+            uint2 en[K];
+#pragma unroll
+            for (int q = 0; q < K; ++q) en[q] = ent[base + q];
+            float gv[K][V];
+#pragma unroll
+            for (int q = 0; q < K; ++q) buffer_row<float, V>(g_rsrc, (en[q].x + gcol) | coldead, 0, gv[q]);
+            float d[K];
+#pragma unroll
+            for (int q = 0; q < K; ++q) {
+                const vec_t<float, V> lnv = *reinterpret_cast<const vec_t<float, V> *>(lut_b + (en[q].y & 0x3ffffu));
+                float sd = 0.f;
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    sd += gv[q][e] * (lnv[e] - lkv[e]);
+                    acc[e] += gv[q][e];
+                }
+                d[q] = sd;
+            }
+            if (need_gu) {
+                const float dot = reduce_scatter<S, K>(d, j) * a.scale;
+                const int q = (j / (S / K)) & (K - 1);  // the item whose dot this lane holds
+                const uint32_t y = ent[base + q].y;
+                if (j % (S / K) == 0 && (y & kPadSlot) == 0) {
+                    const int r = static_cast<int>((y >> 18) & 7u);
+                    const float gu = dot * fast_sigmoid_odd(us[base + q]);
+                    if (a.gurec != nullptr)
+                        a.gurec[static_cast<size_t>(t) * a.items + tile0 + ((y >> 21) & 1023u)] =
+                            static_cast<uint64_t>(__builtin_bit_cast(uint32_t, gu)) | (static_cast<uint64_t>(r) << 32);
+                    us[base + q] = gu;  // the position's margin is spent: it now holds gu
                 }
             }
-            // row k's sum over this tile: scaled and stored (one tile), or
-            // added to the row buffer (rows of a tile are disjoint across
-            // groups, and tiles are separated by barriers)
-            if (a.grad_lut != nullptr) {
+        }
+        if (cur >= 0) finish(cur);
+        const int next = tile0 + kFusedThreads;
+        if (next < a.items) r0 = next + tid < a.items ? rec_t[next + tid] : 0ull;
+        __syncthreads();
+        // 5. combine: group g finishes rows g, g + groups, ...: an empty row is
+        //    zero; a row split over ranges sums its pieces in range order
+        //    (slot 1 of its first range, slot 0 of the others)
+        if (a.grad_lut != nullptr) {
+            const int bl = lo + 1;  // ranges of the first `extra` groups
+            auto range_of = [&](int bt) { return bt < extra * bl ? bt / bl : extra + (bt - extra * bl) / max(lo, 1); };
+            for (int k = g; k < R; k += NG) {
+                const int fb = off[k] / K, nbk = off[k + 1] / K - fb;
+                const int gf = nbk > 0 ? range_of(fb) : 0, gl = nbk > 0 ? range_of(fb + nbk - 1) : 0;
+                if (nbk > 0 && gf == gl) continue;  // finished in the walk
+                vec_t<float, V> w = 0.f;
+                if (nbk > 0) {
+                    w = *reinterpret_cast<const vec_t<float, V> *>(part + (gf * 2 + 1) * P + col);
+                    for (int gg = gf + 1; gg <= gl; ++gg) w += *reinterpret_cast<const vec_t<float, V> *>(part + gg * 2 * P + col);
+                }
                 if (single) {
                     if (col_ok) {
                         float y[V];
 #pragma unroll
-                        for (int e = 0; e < V; ++e) y[e] = acc[e] * a.scale;
+                        for (int e = 0; e < V; ++e) y[e] = w[e] * a.scale;
                         store_f32<V>(a.grad_lut + (static_cast<size_t>(t) * R + k) * O + col, y);
                     }
                 } else {
                     vec_t<float, V> *rb = reinterpret_cast<vec_t<float, V> *>(rowbuf + k * P + col);
-                    vec_t<float, V> w = *rb;
-#pragma unroll
-                    for (int e = 0; e < V; ++e) w[e] += acc[e];
-                    *rb = w;
+                    *rb += w;
                 }
             }
         }
-        const int next = tile0 + kFusedThreads;
-        if (next < a.items) r0 = next + tid < a.items ? rec_t[next + tid] : 0ull;
-        __syncthreads();
-        // 5. threshold gradient of the tile: -gu at each sorted position's
+        // 6. threshold gradient of the tile: -gu at each sorted position's
         //    min-margin comparison, a fixed tree per wave (lane 8c ends with
         //    the wave's sum for comparison c) added to the wave's slots. The
         //    next placement rewrites the sorted list only after two barriers.
@@ -867,8 +908,10 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
         __syncthreads();
     }
 
-    // 6. several tiles: the row buffer, scaled, written once
+    // 7. several tiles: the row buffer (its last rows came from the combine
+    //    step of the last tile), scaled, written once
     if (!single && a.grad_lut != nullptr) {
+        __syncthreads();
         constexpr int qp = P / 4;
         for (int unit = tid; unit < R * qp; unit += kFusedThreads) {
             const int k = unit / qp, c0 = (unit % qp) * 4;
@@ -880,7 +923,7 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
             }
         }
     }
-    // 7. threshold gradient: the waves' sums in wave order
+    // 8. threshold gradient: the waves' sums in wave order
     if (a.grad_thr != nullptr) {
         __syncthreads();
         if (tid < C) {
@@ -1148,8 +1191,11 @@ BackwardPlan plan_backward(const Dims &d) {
         off += waves * 8 * 4;
         p.f_wtot_off = off;
         off += (waves + 1) * 4;
-        p.f_map_off = off;
-        off += d.rows * 4;
+        off = (off + 15) & ~15;  // 16-byte vector accesses
+        p.f_part_off = off;
+        off += (kFusedThreads / p.fslices) * 2 * p.fpitch * 4;
+        p.f_brow_off = off;
+        off += (p.f_slots / batch + 1) * 4;
         p.f_lds_bytes = off;
         p.fused = d.rows * p.fpitch * 4 <= 64 * 1024 && off <= 160 * 1024;
     }
@@ -1184,7 +1230,8 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
         f.rows = d.rows;
         f.g_slice = static_cast<uint32_t>(((g_bytes + (d.tables + 7) / 8 - 1) / ((d.tables + 7) / 8) + 127) & ~127u);
         f.quad_magic = ((uint64_t{1} << 32) + d.out_f / 4 - 1) / (d.out_f / 4);
-        f.map_off = p.f_map_off;
+        f.part_off = p.f_part_off;
+        f.brow_off = p.f_brow_off;
         f.slots = p.f_slots;
         f.lut_off = p.f_lut_off;
         f.cnt_off = p.f_cnt_off;

@@ -64,7 +64,8 @@ struct BackwardPlan {
     int fvec;           // V: columns per lane
     int fslices;        // S: lanes per row group, S * V >= O
     int fpitch;         // S * V: LDS row pitch in floats
-    int f_lut_off, f_cnt_off, f_off_off, f_sorted_off, f_u_off, f_rowbuf_off, f_thr_off, f_wtot_off, f_map_off;  // LDS bytes
+    int f_lut_off, f_cnt_off, f_off_off, f_sorted_off, f_u_off, f_rowbuf_off, f_thr_off, f_wtot_off;  // LDS bytes
+    int f_part_off, f_brow_off;
     int f_slots;        // sorted-list capacity of a tile (items + padding to whole batches)
     int f_lds_bytes;
     int scatter_lds_bytes;   // gu slots [T * C] f32 + the inverse anchor index
