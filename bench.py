@@ -97,21 +97,31 @@ KERNEL_SOURCES = (
 )
 
 
+def source_digest() -> str:
+    """sha256 of the kernel sources with comments and whitespace removed, so
+    that a comment edit does not invalidate a profile of the same code."""
+    import hashlib
+    import re
+
+    h = hashlib.sha256()
+    for src in KERNEL_SOURCES:
+        text = (ROOT / src).read_text()
+        text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", " ", text)
+        h.update(" ".join(text.split()).encode())
+    return h.hexdigest()
+
+
 def measured_traffic(kernel: str) -> int | None:
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
     summary (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE scaled by a
-    calibration copy), used only while the kernel sources still hash to the
-    profiled ones; otherwise None."""
-    import hashlib
-
+    calibration copy), used only while the kernel sources (comments aside)
+    still hash to the profiled ones; otherwise None."""
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
         return None
     rec = json.loads(path.read_text())
-    h = hashlib.sha256()
-    for src in KERNEL_SOURCES:
-        h.update((ROOT / src).read_bytes())
-    if rec.get("source_sha256") != h.hexdigest() or kernel not in rec.get("kernels", {}):
+    if rec.get("source_digest") != source_digest() or kernel not in rec.get("kernels", {}):
         return None
     k = rec["kernels"][kernel]
     return int(k["fetch_bytes"] + k["write_bytes"])

@@ -9,7 +9,27 @@
 // with g = output_scale * grad_output (layers/base.py:76-77).
 //
 // No float atomics anywhere (LDS float atomics serialise badly on gfx950, and
-// fixed summation orders make every gradient deterministic). Two launches:
+// fixed summation orders make every gradient deterministic).
+//
+// Narrow rows (O a multiple of 4 up to 64, or of 8 up to 256, one table's LUT
+// rows within 64 KB as f32; c2 is one) take the fused path, two launches:
+//  (F) fused kernel, one workgroup per table. The table's LUT rows are staged
+//      in LDS as f32; each tile of 1024 items is counting-sorted by code (one
+//      ballot per code bit, per-wave counts written by each code's first item,
+//      a DPP scan), every row padded to whole batches of 32 / V slots whose
+//      entries carry the item's grad-row offset and the LDS offset of its
+//      neighbour row nb. The batches are dealt to row groups (S lanes x V
+//      columns spanning the row) as contiguous balanced ranges. One grad-row
+//      load per item serves the row's LUT-gradient sum (registers; rows that
+//      cross a range boundary are combined in range order afterwards) and the
+//      item's STE dot against L[nb] - L[code], completed by one
+//      reduce-scatter per batch: gu is stored as a {gu, r} record per
+//      (table, item) and summed per comparison into the threshold gradient.
+//  (S) scatter kernel, one workgroup per item: expands the item's records into
+//      (table, comparison) slots and walks the inverse anchor index into
+//      grad_latent, as the item kernel's last phase does.
+//
+// Other shapes take the general path, two launches:
 //  (1) item kernel, one workgroup per item, shaped like the forward: each wave
 //      takes up to 16 consecutive tables. A lane holds the record of table
 //      lane / 4; the wave moves each table's code and min-margin comparison to
