@@ -182,7 +182,7 @@ __device__ __forceinline__ void feature_walk(const float *gud, const int *idx_s,
             for (int q = 0; q < kEntries; ++q)
                 if (eb + q < f1) gx = (en[q] & 1) ? gx - v[q] : gx + v[q];
         }
-        grad_x_row[f] = gx;
+        __builtin_nontemporal_store(gx, grad_x_row + f);
     }
 }
 
@@ -807,7 +807,7 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
                             float y[V];
 #pragma unroll
                             for (int e = 0; e < V; ++e) y[e] = acc[e] * a.scale;
-                            store_f32<V>(a.grad_lut + (static_cast<size_t>(t) * R + k) * O + col, y);
+                            store_f32_nt<V>(a.grad_lut + (static_cast<size_t>(t) * R + k) * O + col, y);
                         }
                     } else {
                         vec_t<float, V> *rb = reinterpret_cast<vec_t<float, V> *>(rowbuf + k * P + col);
@@ -894,7 +894,7 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
                         float y[V];
 #pragma unroll
                         for (int e = 0; e < V; ++e) y[e] = w[e] * a.scale;
-                        store_f32<V>(a.grad_lut + (static_cast<size_t>(t) * R + k) * O + col, y);
+                        store_f32_nt<V>(a.grad_lut + (static_cast<size_t>(t) * R + k) * O + col, y);
                     }
                 } else {
                     vec_t<float, V> *rb = reinterpret_cast<vec_t<float, V> *>(rowbuf + k * P + col);
@@ -939,7 +939,7 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
                 float y[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) y[e] = rowbuf[k * P + c0 + e] * a.scale;
-                store_f32<4>(a.grad_lut + (static_cast<size_t>(t) * R + k) * O + c0, y);
+                store_f32_nt<4>(a.grad_lut + (static_cast<size_t>(t) * R + k) * O + c0, y);
             }
         }
     }

@@ -44,6 +44,29 @@ __device__ __forceinline__ void store_f32(float *__restrict__ p, const float (&d
     }
 }
 
+// Non-temporal (streaming) store of V floats: for outputs that the kernel does
+// not read again, so that they do not sit dirty in this XCD's L2 until the
+// kernel-end write-back.
+template <int V>
+__device__ __forceinline__ void store_f32_nt(float *__restrict__ p, const float (&d)[V]) {
+    if constexpr (V == 1) {
+        __builtin_nontemporal_store(d[0], p);
+    } else if constexpr (V <= 4) {
+        vec_t<float, V> v;
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[i] = d[i];
+        __builtin_nontemporal_store(v, reinterpret_cast<vec_t<float, V> *>(p));
+    } else {
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q) {
+            vec_t<float, 4> v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = d[4 * q + i];
+            __builtin_nontemporal_store(v, reinterpret_cast<vec_t<float, 4> *>(p + 4 * q));
+        }
+    }
+}
+
 // Butterfly sum over the lanes whose ids differ only in bits [lo, hi).
 // Every lane of a group ends with the group's total.
 __device__ __forceinline__ float xor_sum(float v, int lo, int hi) {

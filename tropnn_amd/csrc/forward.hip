@@ -236,7 +236,7 @@ __global__ __launch_bounds__(1024) void pairwise_forward_kernel(FwdArgs a) {
         float y[N];
 #pragma unroll
         for (int e = 0; e < N; ++e) y[e] = acc[e] * a.scale;
-        store_f32<N>(a.out + static_cast<size_t>(item) * a.out_f + col, y);
+        store_f32_nt<N>(a.out + static_cast<size_t>(item) * a.out_f + col, y);
     }
 }
 
