@@ -72,15 +72,10 @@ def algorithmic_bytes(fused: bool) -> dict[str, int]:
 def fused_backward() -> bool:
     """Whether the library runs c2's backward as the fused table kernel plus
     the scatter kernel (its workspace then holds 8-byte {gu, r} records)."""
-    import ctypes
+    from tropnn_amd.backends.pairwise_hip import LUT_F32, STE_MIN_MARGIN, load_library
 
-    from tropnn_amd.backends.pairwise_hip import load_library
-
-    lib = load_library()
-    fn = lib.tropnn_hip_pairwise_backward_workspace_size
-    fn.restype = ctypes.c_size_t
-    fn.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int]
-    return fn(B, I, O, T, C, 0) == 8 * T * B
+    lib = load_library()  # declares the C signatures
+    return lib.tropnn_hip_pairwise_backward_workspace_size(B, I, O, T, C, LUT_F32, STE_MIN_MARGIN) == 8 * T * B
 
 
 def log(msg: str) -> None:

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TROPNN_HIP_ABI_VERSION 3
+#define TROPNN_HIP_ABI_VERSION 4
 
 /* status codes */
 #define TROPNN_OK 0
@@ -106,9 +106,10 @@ int tropnn_hip_pairwise_forward(int64_t items, int64_t in_features, int64_t out_
                                 float *output, tropnn_route_record *route_record, int64_t *indices, float *margins,
                                 tropnn_stream_t stream);
 
-/* Bytes of device workspace tropnn_hip_pairwise_backward needs for these dims. */
+/* Bytes of device workspace tropnn_hip_pairwise_backward needs for these dims
+ * and STE mode (0 and an error message for invalid arguments). */
 size_t tropnn_hip_pairwise_backward_workspace_size(int64_t items, int64_t in_features, int64_t out_features,
-                                                   int64_t tables, int64_t comparisons, int lut_dtype);
+                                                   int64_t tables, int64_t comparisons, int lut_dtype, int ste_mode);
 
 /*
  * Inverse anchor index used by the input-gradient backward: for every input
@@ -125,31 +126,38 @@ int tropnn_hip_build_anchor_index(int64_t in_features, int64_t tables, int64_t c
                                   int32_t *offsets, int32_t *entries, tropnn_stream_t stream);
 
 /*
- * Backward of the training forward with the min-margin STE. Replaces
- * _PairwiseTileLangFunction.backward and its LUT-scatter and min-STE kernels
- * (backends/pairwise_tilelang.py:118-288, 481-534); the math is the autograd
- * of the torch path (layers/pairwise.py:137-166, layers/surrogate.py:16-38):
+ * Backward of the training forward. Replaces _PairwiseTileLangFunction.backward
+ * and its LUT-scatter, min-STE and full-STE kernels
+ * (backends/pairwise_tilelang.py:118-410, 481-534); the math is the autograd
+ * of the torch path (layers/pairwise.py:137-200, layers/surrogate.py:9-38):
  *   g[b,:]            = output_scale * grad_output[b,:]
  *   grad_lut[t,r,:]   = sum_{b: code[b,t]=r} g[b,:]                      (fully overwritten)
+ * ste_mode = TROPNN_STE_MIN_MARGIN (r = the record's min-margin comparison,
+ * u = its margin):
  *   D[b,t]            = sum_o g[b,o] * (lut[t,nb,o] - lut[t,code,o]),   nb = code ^ (1 << r)
  *   gu[b,t]           = D[b,t] * surrogate'(u[b,t])
  *   grad_latent[b,i]  = sum_t gu[b,t] * ([i = a(t,r)] - [i = b'(t,r)])   (fully overwritten)
  *   grad_thresholds[t,c] = -sum_b [r[b,t] = c] * gu[b,t]                (fully overwritten)
+ * ste_mode = TROPNN_STE_FULL: every comparison c contributes, with its own
+ * margin margins[b,t,c] (the forward's margins output, required when
+ * grad_latent or grad_thresholds is asked for) and nb = code ^ (1 << c):
+ *   gu[b,t,c] = D[b,t,c] * surrogate'(margins[b,t,c]); grad_latent and
+ *   grad_thresholds sum gu[b,t,c] over every c.
+ * surrogate: TROPNN_SURROGATE_FAST_SIGMOID_ODD or TROPNN_SURROGATE_IZHIKEVICH.
  * Every sum runs in a fixed order: the results are deterministic.
  * Any of the three gradient pointers may be NULL to skip that gradient;
  * grad_latent needs the anchor index (index_offsets / index_entries from
  * tropnn_hip_build_anchor_index), the others accept NULL index pointers.
- * Only ste_mode = TROPNN_STE_MIN_MARGIN and surrogate =
- * TROPNN_SURROGATE_FAST_SIGMOID_ODD are implemented; the others return
- * TROPNN_ERR_UNSUPPORTED. workspace: device memory of at least
- * tropnn_hip_pairwise_backward_workspace_size() bytes, 16-byte aligned.
+ * workspace: device memory of at least
+ * tropnn_hip_pairwise_backward_workspace_size() bytes (same ste_mode), 16-byte
+ * aligned.
  */
 int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out_features, int64_t tables,
                                  int64_t comparisons, const float *grad_output, const void *lut, int lut_dtype,
-                                 const tropnn_route_record *route_record, const int32_t *index_offsets,
-                                 const int32_t *index_entries, float output_scale, int ste_mode, int surrogate,
-                                 float *grad_latent, float *grad_thresholds, float *grad_lut, void *workspace,
-                                 size_t workspace_bytes, tropnn_stream_t stream);
+                                 const tropnn_route_record *route_record, const float *margins,
+                                 const int32_t *index_offsets, const int32_t *index_entries, float output_scale,
+                                 int ste_mode, int surrogate, float *grad_latent, float *grad_thresholds,
+                                 float *grad_lut, void *workspace, size_t workspace_bytes, tropnn_stream_t stream);
 
 /*
  * Profiling hook (no counterpart in the reference, whose harness times whole

@@ -52,13 +52,22 @@ def test_constants_match_header():
     assert header_define("TROPNN_SURROGATE_FAST_SIGMOID_ODD") == ph.SURROGATE_IDS["fast_sigmoid_odd"]
     assert header_define("TROPNN_SURROGATE_IZHIKEVICH") == ph.SURROGATE_IDS["izhikevich"]
     assert header_define("TROPNN_MAX_COMPARISONS") == ph.MAX_COMPARISONS
-    assert header_define("TROPNN_KERNEL_FORWARD") == ph.KERNEL_IDS["forward"]
+    assert header_define("TROPNN_STE_MIN_MARGIN") == ph.STE_MIN_MARGIN
+    assert header_define("TROPNN_STE_FULL") == ph.STE_FULL
+    for name, kid in ph.KERNEL_IDS.items():
+        assert header_define("TROPNN_KERNEL_" + name.upper()) == kid
 
 
 def test_workspace_size(lib):
-    n = lib.tropnn_hip_pairwise_backward_workspace_size(512, 128, 128, 136, 6, ph.LUT_F32)
-    assert n > 0 and n % (136 * 512 * 4) == 0  # whole [chunks][T][B] f32 planes
-    assert lib.tropnn_hip_pairwise_backward_workspace_size(512, 128, 128, 136, 9, ph.LUT_F32) == 0
+    ws = lib.tropnn_hip_pairwise_backward_workspace_size
+    # c2, min-margin: the fused path's {gu, r} records [T][B] x 8 bytes
+    assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_MIN_MARGIN) == 136 * 512 * 8
+    # general path (O = 4096): gu [T][B] f32
+    assert ws(64, 1024, 4096, 512, 8, ph.LUT_F16, ph.STE_MIN_MARGIN) == 512 * 64 * 4
+    # full STE: gu [T][C][B] f32
+    assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_FULL) == 136 * 6 * 512 * 4
+    assert ws(512, 128, 128, 136, 9, ph.LUT_F32, ph.STE_MIN_MARGIN) == 0
+    assert ws(512, 128, 128, 136, 6, ph.LUT_F32, 7) == 0 and "ste_mode" in _err(lib)
 
 
 def _err(lib) -> str:
@@ -85,18 +94,25 @@ def test_forward_rejects_bad_arguments(lib):
 
 def test_backward_rejects_bad_arguments(lib):
     bwd = lib.tropnn_hip_pairwise_backward
-    args = [4, 8, 5, 3, 3, 16, 16, 0, 16, 16, 16, 1.0, 0, 0, 16, 16, 16, 16, 1 << 20, None]
+    # items, in, out, tables, comps, G, lut, dtype, record, margins, offsets,
+    # entries, scale, ste_mode, surrogate, grad_x, grad_thr, grad_lut,
+    # workspace, workspace_bytes, stream (pointers are never dereferenced:
+    # every case fails validation before a launch)
+    args = [4, 8, 5, 3, 3, 16, 16, 0, 16, None, 16, 16, 1.0, 0, 0, 16, 16, 16, 16, 1 << 20, None]
     bad_mode = list(args)
-    bad_mode[12] = 1  # full STE: not implemented
-    assert bwd(*bad_mode) == 2 and "min-margin" in _err(lib)
+    bad_mode[13] = 2
+    assert bwd(*bad_mode) == 1 and "ste_mode" in _err(lib)
     bad_surr = list(args)
-    bad_surr[13] = 1  # izhikevich: not implemented
-    assert bwd(*bad_surr) == 2 and "fast_sigmoid_odd" in _err(lib)
+    bad_surr[14] = 5
+    assert bwd(*bad_surr) == 1 and "surrogate" in _err(lib)
+    full_no_margins = list(args)
+    full_no_margins[13] = 1
+    assert bwd(*full_no_margins) == 1 and "margins" in _err(lib)
     no_index = list(args)
-    no_index[9] = None
+    no_index[10] = None
     assert bwd(*no_index) == 1 and "anchor index" in _err(lib)
     small_ws = list(args)
-    small_ws[18] = 4
+    small_ws[19] = 4
     assert bwd(*small_ws) == 1 and "workspace" in _err(lib)
 
 

@@ -45,9 +45,9 @@ def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
     return diff / scale if scale > 0 else diff
 
 
-def make_pair(i, o, t, c, *, seed=0, thr_std=0.0, lut_dtype="f32", gen_seed=1234):
-    ref = orc.OraclePairwiseLinear(i, o, tables=t, comparisons=c, seed=seed)
-    hip = PairwiseLinear(i, o, tables=t, comparisons=c, seed=seed, device_lut_dtype=lut_dtype)
+def make_pair(i, o, t, c, *, seed=0, thr_std=0.0, lut_dtype="f32", gen_seed=1234, **ste):
+    ref = orc.OraclePairwiseLinear(i, o, tables=t, comparisons=c, seed=seed, **ste)
+    hip = PairwiseLinear(i, o, tables=t, comparisons=c, seed=seed, device_lut_dtype=lut_dtype, **ste)
     with torch.no_grad():
         if thr_std:
             g = torch.Generator().manual_seed(gen_seed)
@@ -199,11 +199,18 @@ def test_pairwise_hip_forward_matches_zig_restatement():
 
 
 # ---------------------------------------------------------------- train fwd + bwd
-def test_reference_case_square_mean():
-    """test_backend_parity.py:348-369 (min-margin STE): PairwiseLinear(8, 5,
-    tables=3, comparisons=3, seed=1), x = randn(4, 8), loss = square().mean()."""
+@pytest.mark.parametrize(
+    "min_margin,surrogate,seed",
+    [(True, "fast_sigmoid_odd", 1), (False, "fast_sigmoid_odd", 1), (True, "izhikevich", 2)],
+)
+def test_reference_case_square_mean(min_margin, surrogate, seed):
+    """test_backend_parity.py:348-392: PairwiseLinear(8, 5, tables=3,
+    comparisons=3), min-margin and full STE (seed 1) and the izhikevich
+    surrogate (seed 2), x = randn(4, 8), loss = square().mean(), at the
+    reference's atol 1e-6 (x is drawn on the CPU: the reference draws it from
+    the CUDA generator)."""
     torch.manual_seed(0)
-    ref, hip = make_pair(8, 5, 3, 3, seed=1)
+    ref, hip = make_pair(8, 5, 3, 3, seed=seed, use_min_margin_ste=min_margin, surrogate=surrogate)
     x = torch.randn(4, 8)
     x_ref = x.clone().requires_grad_(True)
     x_hip = x.to(DEV).requires_grad_(True)
@@ -248,6 +255,48 @@ def test_train_parity(i, o, t, c, b, thr_std):
     x = seeded((b, i), seed=b)
     g = seeded((b, 1, o), seed=b + 1)
     assert_train_parity(ref, hip, *train_step(ref, hip, x, g))
+
+
+@pytest.mark.parametrize(
+    "i,o,t,c,b,min_margin,surrogate,lut_dtype",
+    [
+        (128, 128, 136, 6, 512, True, "izhikevich", "f32"),  # fused path
+        (40, 10, 33, 4, 70, True, "izhikevich", "f32"),  # general path
+        (128, 128, 136, 6, 256, False, "fast_sigmoid_odd", "f32"),  # full STE
+        (64, 96, 20, 8, 50, False, "izhikevich", "f32"),
+        (16, 7, 5, 1, 19, False, "fast_sigmoid_odd", "f32"),
+        (48, 128, 12, 6, 2100, False, "izhikevich", "f32"),  # several table-kernel tiles
+        (128, 256, 40, 5, 64, False, "fast_sigmoid_odd", "f32"),  # 4 columns per lane
+        (128, 128, 136, 6, 256, False, "izhikevich", "f16"),
+        (100, 1000, 12, 7, 40, False, "fast_sigmoid_odd", "f16"),  # 8 f16 columns per lane
+    ],
+)
+def test_train_parity_ste_variants(i, o, t, c, b, min_margin, surrogate, lut_dtype):
+    """Full STE (use_min_margin_ste=False, layers/pairwise.py:168-200) and the
+    izhikevich surrogate (layers/surrogate.py:9-13), against the oracle."""
+    ref, hip = make_pair(
+        i, o, t, c, seed=i + t, thr_std=0.2, lut_dtype=lut_dtype, use_min_margin_ste=min_margin, surrogate=surrogate
+    )
+    x = seeded((b, i), seed=b)
+    g = seeded((b, 1, o), seed=b + 1)
+    tol = F16_TOL if lut_dtype == "f16" else F32_TOL
+    assert_train_parity(ref, hip, *train_step(ref, hip, x, g), tol=tol)
+
+
+def test_full_ste_without_route_debug():
+    """With the route debug cache off the forward still keeps the margins the
+    full STE needs."""
+    ref, hip = make_pair(32, 16, 9, 5, seed=3, thr_std=0.2, use_min_margin_ste=False)
+    hip.cache_route_debug = False
+    x = seeded((40, 32), seed=5)
+    g = seeded((40, 1, 16), seed=6)
+    x_ref = x.clone().requires_grad_(True)
+    x_hip = x.to(DEV).requires_grad_(True)
+    ref.train()(x_ref).backward(g)
+    hip.train()(x_hip).backward(g.to(DEV))
+    assert rel_err(x_hip.grad, x_ref.grad) <= F32_TOL
+    assert rel_err(hip.thresholds.grad, ref.thresholds.grad) <= F32_TOL
+    assert rel_err(hip.lut.grad, ref.lut.grad) <= F32_TOL
 
 
 def test_train_without_input_grad():

@@ -26,7 +26,7 @@ from typing import Any
 import torch
 from torch import Tensor
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 LUT_F32, LUT_F16 = 0, 1
 SURROGATE_IDS = {"fast_sigmoid_odd": 0, "izhikevich": 1}
 STE_MIN_MARGIN, STE_FULL = 0, 1
@@ -76,11 +76,11 @@ def _declare(lib: ctypes.CDLL) -> None:
         fn.restype = i
     lib.tropnn_hip_pairwise_forward.argtypes = [i64, i64, i64, i64, i64, p, p, p, p, i, f, p, p, p, p, p]
     lib.tropnn_hip_pairwise_forward.restype = i
-    lib.tropnn_hip_pairwise_backward_workspace_size.argtypes = [i64, i64, i64, i64, i64, i]
+    lib.tropnn_hip_pairwise_backward_workspace_size.argtypes = [i64, i64, i64, i64, i64, i, i]
     lib.tropnn_hip_pairwise_backward_workspace_size.restype = sz
     lib.tropnn_hip_build_anchor_index.argtypes = [i64, i64, i64, p, p, p, p]
     lib.tropnn_hip_build_anchor_index.restype = i
-    lib.tropnn_hip_pairwise_backward.argtypes = [i64, i64, i64, i64, i64, p, p, i, p, p, p, f, i, i, p, p, p, p, sz, p]
+    lib.tropnn_hip_pairwise_backward.argtypes = [i64, i64, i64, i64, i64, p, p, i, p, p, p, p, f, i, i, p, p, p, p, sz, p]
     lib.tropnn_hip_pairwise_backward.restype = i
     lib.tropnn_hip_arm_kernel_events.argtypes = [i, p, p]
     lib.tropnn_hip_arm_kernel_events.restype = i
@@ -234,8 +234,11 @@ def _route_forward(
     output_scale: float,
     want_record: bool,
     return_route: bool,
-) -> tuple[Tensor, Tensor | None, Tensor, Tensor]:
-    """One fused forward launch. Returns (output, record, indices, margins)."""
+    want_margins: bool = False,
+) -> tuple[Tensor, Tensor | None, Tensor, Tensor, Tensor | None]:
+    """One fused forward launch. Returns (output, record, indices, margins,
+    saved_margins); saved_margins [items, tables, comparisons] is the margins
+    tensor the full-STE backward reads (want_margins), else None."""
     batch, steps, in_features, tables, comps, out_features = _validate(latent, anchors, thresholds, lut_read)
     check_anchors(anchors, in_features)
     items = batch * steps
@@ -250,6 +253,9 @@ def _route_forward(
     else:
         indices = torch.empty((items, 0), device=dev, dtype=torch.int64)
         margins = torch.empty((items, 0), device=dev, dtype=torch.float32)
+    saved = None  # margins the full-STE backward reads
+    if want_margins:
+        saved = margins if return_route else torch.empty((items, tables, comps), device=dev, dtype=torch.float32)
     lib = load_library()
     rc = lib.tropnn_hip_pairwise_forward(
         items,
@@ -266,7 +272,7 @@ def _route_forward(
         _ptr(out),
         _ptr(record),
         _ptr(indices) if return_route else None,
-        _ptr(margins) if return_route else None,
+        _ptr(margins) if return_route else _ptr(saved),
         _stream(dev),
     )
     _check(rc, "tropnn_hip_pairwise_forward")
@@ -276,12 +282,14 @@ def _route_forward(
     else:
         idx_view = indices.view(batch, steps, 0)
         mar_view = margins.view(batch, steps, 0)
-    return out.view(batch, steps, out_features), record, idx_view, mar_view
+    return out.view(batch, steps, out_features), record, idx_view, mar_view, saved
 
 
 class _PairwiseHipFunction(torch.autograd.Function):
     """Forward: fused route + gather + scale. Backward: table-major LUT
-    gradient + min-margin STE, then input / threshold gradients. Contract of
+    gradient + min-margin or full STE (fast_sigmoid_odd or izhikevich
+    surrogate), then input / threshold gradients. The full STE needs every
+    comparison's margin, which the forward then keeps. Contract of
     _PairwiseTileLangFunction (backends/pairwise_tilelang.py:460-534): the
     gradient tuple is (latent, None, thresholds, lut, None, ...), indices and
     margins are non-differentiable."""
@@ -295,6 +303,7 @@ class _PairwiseHipFunction(torch.autograd.Function):
         lut: Tensor,
         lut_read: Tensor,
         ste: bool,
+        min_margin: bool,
         surrogate: str,
         output_scale: float,
         return_route: bool,
@@ -302,7 +311,7 @@ class _PairwiseHipFunction(torch.autograd.Function):
         needs_lut = ctx.needs_input_grad[3]
         needs_route = ste and (ctx.needs_input_grad[0] or ctx.needs_input_grad[2])
         want_record = needs_lut or needs_route
-        out, record, indices, margins = _route_forward(
+        out, record, indices, margins, saved_margins = _route_forward(
             latent,
             anchors,
             thresholds,
@@ -310,13 +319,15 @@ class _PairwiseHipFunction(torch.autograd.Function):
             output_scale=output_scale,
             want_record=want_record,
             return_route=return_route,
+            want_margins=needs_route and not min_margin,
         )
         # the anchor index is built (once per anchors version) at forward
         # time, outside any backward-pass graph capture
         ctx.index = anchor_index(anchors, latent.shape[2]) if (ste and ctx.needs_input_grad[0]) else None
-        ctx.save_for_backward(record, anchors, lut_read)
+        ctx.save_for_backward(record, anchors, lut_read, saved_margins)
         ctx.dims = tuple(latent.shape) + (lut_read.shape[2],)
         ctx.ste = ste
+        ctx.ste_mode = STE_MIN_MARGIN if min_margin else STE_FULL
         ctx.surrogate = surrogate
         ctx.output_scale = float(output_scale)
         ctx.mark_non_differentiable(indices, margins)
@@ -325,7 +336,7 @@ class _PairwiseHipFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx: Any, grad_output: Tensor, grad_indices: Tensor | None, grad_margins: Tensor | None):  # type: ignore[override]
         del grad_indices, grad_margins
-        record, anchors, lut_read = ctx.saved_tensors
+        record, anchors, lut_read, saved_margins = ctx.saved_tensors
         batch, steps, in_features, out_features = ctx.dims
         tables, comps, _ = anchors.shape
         items = batch * steps
@@ -334,14 +345,16 @@ class _PairwiseHipFunction(torch.autograd.Function):
         want_thr = ctx.ste and ctx.needs_input_grad[2]
         want_lut = ctx.needs_input_grad[3]
         if not (want_x or want_thr or want_lut):
-            return (None,) * 9
+            return (None,) * 10
         g = grad_output.reshape(items, out_features).to(torch.float32).contiguous()
         grad_x = torch.empty((items, in_features), device=dev, dtype=torch.float32) if want_x else None
         grad_thr = torch.empty((tables, comps), device=dev, dtype=torch.float32) if want_thr else None
         grad_lut = torch.empty((tables, 1 << comps, out_features), device=dev, dtype=torch.float32) if want_lut else None
         lib = load_library()
         lut_dtype = LUT_F16 if lut_read.dtype == torch.float16 else LUT_F32
-        ws_bytes = lib.tropnn_hip_pairwise_backward_workspace_size(items, in_features, out_features, tables, comps, lut_dtype)
+        ws_bytes = lib.tropnn_hip_pairwise_backward_workspace_size(
+            items, in_features, out_features, tables, comps, lut_dtype, ctx.ste_mode
+        )
         workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8) if (want_x or want_thr) else None
         offsets, entries = ctx.index if want_x else (None, None)
         rc = lib.tropnn_hip_pairwise_backward(
@@ -354,10 +367,11 @@ class _PairwiseHipFunction(torch.autograd.Function):
             _ptr(lut_read),
             lut_dtype,
             _ptr(record),
+            _ptr(saved_margins),
             _ptr(offsets),
             _ptr(entries),
             ctx.output_scale,
-            STE_MIN_MARGIN,
+            ctx.ste_mode,
             SURROGATE_IDS[ctx.surrogate],
             _ptr(grad_x),
             _ptr(grad_thr),
@@ -368,7 +382,7 @@ class _PairwiseHipFunction(torch.autograd.Function):
         )
         _check(rc, "tropnn_hip_pairwise_backward")
         gx = grad_x.view(batch, steps, in_features) if grad_x is not None else None
-        return gx, None, grad_thr, grad_lut, None, None, None, None, None
+        return gx, None, grad_thr, grad_lut, None, None, None, None, None, None
 
 
 def pairwise_hip(
@@ -393,7 +407,8 @@ def pairwise_hip(
     [B,S,0] tensors, as the Zig path returns (layers/pairwise.py:223-225).
 
     lut_read: the tensor the kernels read, e.g. an f16 copy of lut (f32 by
-    default = lut itself). ste: carry the min-margin STE gradient to latent and
+    default = lut itself). ste: carry the STE gradient (min-margin, or every
+    comparison with use_min_margin_ste=False) to latent and
     thresholds (the torch path does so only in training,
     layers/pairwise.py:245-247). output_scale defaults to 1.0, the
     pairwise_tilelang contract (the module scales afterwards); the package's
@@ -402,15 +417,19 @@ def pairwise_hip(
     if surrogate not in SURROGATE_IDS:
         raise ValueError(f"Pairwise HIP backend does not support surrogate={surrogate!r}")
     _require_gpu(latent, anchors, thresholds, lut)
-    if ste and torch.is_grad_enabled() and (latent.requires_grad or thresholds.requires_grad):
-        if not use_min_margin_ste:
-            raise NotImplementedError("Pairwise HIP backend: the full STE (use_min_margin_ste=False) is not implemented yet")
-        if surrogate != "fast_sigmoid_odd":
-            raise NotImplementedError(f"Pairwise HIP backend: the {surrogate!r} surrogate backward is not implemented yet")
     if lut_read is None:
         lut_read = lut
     return _PairwiseHipFunction.apply(
-        latent, anchors, thresholds, lut, lut_read.detach(), bool(ste), surrogate, float(output_scale), bool(return_route)
+        latent,
+        anchors,
+        thresholds,
+        lut,
+        lut_read.detach(),
+        bool(ste),
+        bool(use_min_margin_ste),
+        surrogate,
+        float(output_scale),
+        bool(return_route),
     )
 
 

@@ -163,11 +163,15 @@ int tropnn_hip_lut_forward_batch_f16(size_t batch, size_t tables, size_t compari
 }
 
 size_t tropnn_hip_pairwise_backward_workspace_size(int64_t items, int64_t in_features, int64_t out_features,
-                                                   int64_t tables, int64_t comparisons, int lut_dtype) {
+                                                   int64_t tables, int64_t comparisons, int lut_dtype, int ste_mode) {
     tropnn::Dims d{};
     if (make_dims(items, in_features, out_features, tables, comparisons, lut_dtype, d) != TROPNN_OK) return 0;
+    if (ste_mode != TROPNN_STE_MIN_MARGIN && ste_mode != TROPNN_STE_FULL) {
+        fail(TROPNN_ERR_INVALID_ARGUMENT, "ste_mode must be TROPNN_STE_MIN_MARGIN or TROPNN_STE_FULL");
+        return 0;
+    }
     ok();
-    return tropnn::plan_backward(d).workspace_bytes;
+    return tropnn::plan_backward(d, ste_mode).workspace_bytes;
 }
 
 int tropnn_hip_build_anchor_index(int64_t in_features, int64_t tables, int64_t comparisons, const int64_t *anchors,
@@ -188,21 +192,17 @@ int tropnn_hip_build_anchor_index(int64_t in_features, int64_t tables, int64_t c
 
 int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out_features, int64_t tables,
                                  int64_t comparisons, const float *grad_output, const void *lut, int lut_dtype,
-                                 const tropnn_route_record *route_record, const int32_t *index_offsets,
-                                 const int32_t *index_entries, float output_scale, int ste_mode, int surrogate,
-                                 float *grad_latent, float *grad_thresholds, float *grad_lut, void *workspace,
-                                 size_t workspace_bytes, tropnn_stream_t stream) {
+                                 const tropnn_route_record *route_record, const float *margins,
+                                 const int32_t *index_offsets, const int32_t *index_entries, float output_scale,
+                                 int ste_mode, int surrogate, float *grad_latent, float *grad_thresholds,
+                                 float *grad_lut, void *workspace, size_t workspace_bytes, tropnn_stream_t stream) {
     tropnn::Dims d{};
     if (int rc = make_dims(items, in_features, out_features, tables, comparisons, lut_dtype, d)) return rc;
     if (ste_mode != TROPNN_STE_MIN_MARGIN && ste_mode != TROPNN_STE_FULL)
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "ste_mode must be TROPNN_STE_MIN_MARGIN or TROPNN_STE_FULL");
     if (surrogate != TROPNN_SURROGATE_FAST_SIGMOID_ODD && surrogate != TROPNN_SURROGATE_IZHIKEVICH)
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "surrogate must be a TROPNN_SURROGATE_* value");
-    if (ste_mode != TROPNN_STE_MIN_MARGIN)
-        return fail(TROPNN_ERR_UNSUPPORTED, "only the min-margin STE backward is implemented");
-    if (surrogate != TROPNN_SURROGATE_FAST_SIGMOID_ODD)
-        return fail(TROPNN_ERR_UNSUPPORTED, "only the fast_sigmoid_odd surrogate is implemented");
-    const tropnn::BackwardPlan p = tropnn::plan_backward(d);
+    const tropnn::BackwardPlan p = tropnn::plan_backward(d, ste_mode);
     if (d.items == 0) {
         // no items: the parameter gradients are zero (a fill kernel, not a
         // memset, so the call stays capturable in a HIP graph)
@@ -220,6 +220,10 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "grad_output, lut and route_record must be non-NULL");
     if (grad_latent && (!index_offsets || !index_entries))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "grad_latent needs the anchor index (tropnn_hip_build_anchor_index)");
+    if (ste_mode == TROPNN_STE_FULL && (grad_latent || grad_thresholds) && !margins)
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "the full STE needs the forward's margins [items, tables, comparisons]");
+    if (margins && misaligned(margins, 4))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "margins must be 4-byte aligned");
     const size_t esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
     // fused path: LUT chunks of 4 elements, 16-byte grad rows and LUT-grad rows
     const size_t lut_align = p.fused ? 4 * esize : p.item_vec * esize;
@@ -242,9 +246,9 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
     if (lut_bytes > (int64_t{1} << 31) || g_bytes > (int64_t{1} << 31))
         return fail(TROPNN_ERR_UNSUPPORTED, "LUT (%lld bytes) or grad_output (%lld bytes) exceeds the 2 GiB limit",
                     (long long)lut_bytes, (long long)g_bytes);
-    hipError_t e = tropnn::launch_backward(d, p, grad_output, lut, route_record, index_offsets, index_entries,
-                                           output_scale, grad_latent, grad_thresholds, grad_lut,
-                                           static_cast<float *>(workspace), static_cast<hipStream_t>(stream));
+    hipError_t e = tropnn::launch_backward(d, p, grad_output, lut, route_record, margins, index_offsets,
+                                           index_entries, output_scale, surrogate, grad_latent, grad_thresholds,
+                                           grad_lut, static_cast<float *>(workspace), static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail("pairwise backward launch", e);
     return ok();
 }

@@ -75,11 +75,13 @@ struct ItemArgs {
     const float *grad_out;
     const void *lut;
     const uint64_t *rec;
+    const float *margins;          // [B][T][C] (full STE)
     const int32_t *index_offsets;  // [in_f + 1]
     const int32_t *index_entries;  // ((t * C + c) << 1) | side
     float scale;
+    int surrogate;  // TROPNN_SURROGATE_*
     float *grad_x;
-    float *gu;  // [T][B]
+    float *gu;  // min-margin: [T][B]; full STE: [T][C][B]
     uint32_t lut_bytes, g_bytes;
     int items, in_f, out_f, tables, comps, rows, row_bytes, table_bytes, per_wave, o_tiles;
 };
@@ -87,7 +89,8 @@ struct ItemArgs {
 struct LutArgs {
     const float *grad_out;
     const uint64_t *rec;
-    const float *gu;  // [T][B], for the threshold gradient
+    const float *gu;  // for the threshold gradient: [T][B] (min-margin) or [T][C][B] (full STE)
+    int full;         // full STE: every comparison carries its own gu
     float scale;
     float *grad_lut;
     float *grad_thr;
@@ -270,7 +273,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void 
         // 3. lane 4i completes table i's dot: gu, stored and expanded into slots
         const float dot = reduce_scatter<kWave, kItemTables>(d, lane) * a.scale;
         if (has && (lane & 3) == 0) {
-            const float gu = dot * fast_sigmoid_odd(rec_u(rr));
+            const float gu = dot * surrogate_grad(rec_u(rr), a.surrogate);
             if (a.gu != nullptr) a.gu[static_cast<size_t>(tb + ti) * a.items + b] = gu;
             float *slot = gud + (tb + ti) * C;
             for (int c = 0; c < C; ++c) slot[c] = c == r_v ? gu : 0.f;
@@ -284,6 +287,88 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void 
     __syncthreads();
 
     // 4. one thread per input feature: its signed slots in entry order
+    feature_walk(gud, idx_s, a.in_f, a.grad_x + static_cast<size_t>(b) * a.in_f, tid, nthr);
+}
+
+// ------------------------------------------------------------------ full-STE item kernel
+
+// Full STE (layers/pairwise.py:168-200): every comparison c of (item, table)
+// carries gu_c = s * sum_o G[b,o] (L[code ^ 2^c, o] - L[code, o]) * sg'(m_c),
+// m_c being that comparison's own margin. One workgroup per item; each wave
+// takes its block of tables F at a time (F = 4, 2 or 1 as the lane's row
+// piece widens, so that the F (C + 1) rows in flight fit the registers): lane
+// l holds the record of table l % F of the block, the block's current and
+// neighbour rows are loaded with scalar row offsets (64 lanes spanning the
+// row), and one reduce-scatter over the wave completes its 8 F dots (8
+// comparison slots per table). Then the item kernel's feature walk.
+template <typename T, int N>
+__global__ __launch_bounds__(1024) void pairwise_bwd_full_kernel(ItemArgs a) {
+    constexpr int kFullTables = N <= 2 ? 4 : (N == 4 ? 2 : 1);
+    extern __shared__ __align__(16) unsigned char lds[];
+    float *gud = reinterpret_cast<float *>(lds);  // [T * C] this item's gu slots
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = blockIdx.x;
+    const int C = a.comps, R = a.rows;
+    const int t0 = wave * a.per_wave;
+    const int nt = max(0, min(a.tables, t0 + a.per_wave) - t0);
+    const int nidx = a.grad_x != nullptr ? a.in_f + 1 + 2 * a.tables * C : 0;
+    int *idx_s = reinterpret_cast<int *>(gud + a.tables * C);  // [in_f + 1 + 2 T C]
+    for (int k = tid; k < nidx; k += nthr)
+        idx_s[k] = k <= a.in_f ? a.index_offsets[k] : a.index_entries[k - a.in_f - 1];
+
+    const __amdgpu_buffer_rsrc_t lut_rsrc = buffer_rsrc(a.lut, a.lut_bytes);
+    const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.grad_out, a.g_bytes);
+    constexpr int kSlots = kFullTables * TROPNN_MAX_COMPARISONS;  // dots per block
+    for (int tb = t0; tb < t0 + nt; tb += kFullTables) {
+        const int ntb = min(kFullTables, t0 + nt - tb);
+        const int tq = lane & (kFullTables - 1);
+        const uint64_t rr = tq < ntb ? a.rec[static_cast<size_t>(tb + tq) * a.items + b] : 0ull;
+        const int code_v = rec_code(rr) & (R - 1);
+        float d[kSlots];
+#pragma unroll
+        for (int i = 0; i < kSlots; ++i) d[i] = 0.f;
+        for (int ct = 0; ct < a.o_tiles; ++ct) {
+            const int col = ct * (kWave * N) + lane * N;
+            const bool col_ok = col < a.out_f;
+            float g[N];
+            buffer_row<float, N>(g_rsrc, col_ok ? static_cast<uint32_t>(b * a.out_f + col) * 4u : kOutOfRange, 0, g);
+            const uint32_t voff = col_ok ? static_cast<uint32_t>(col) * static_cast<uint32_t>(sizeof(T)) : kOutOfRange;
+#pragma unroll
+            for (int q = 0; q < kFullTables; ++q) {
+                const bool live = q < ntb;
+                const int code = __builtin_amdgcn_readlane(code_v, q);
+                const int trow = live ? (tb + q) * a.table_bytes : 0;
+                float lk[N];
+                buffer_row<T, N>(lut_rsrc, live ? voff : kOutOfRange, trow + code * a.row_bytes, lk);
+#pragma unroll
+                for (int c = 0; c < TROPNN_MAX_COMPARISONS; ++c) {
+                    const bool on = live && c < C;
+                    float ln[N];
+                    buffer_row<T, N>(lut_rsrc, on ? voff : kOutOfRange,
+                                     on ? trow + ((code ^ (1 << c)) & (R - 1)) * a.row_bytes : 0, ln);
+#pragma unroll
+                    for (int e = 0; e < N; ++e) d[q * TROPNN_MAX_COMPARISONS + c] += g[e] * (ln[e] - lk[e]);
+                }
+            }
+        }
+        // lane l completes dot (l / (64 / slots)) % slots: table q = dot / 8,
+        // comparison c = dot % 8
+        const float dot = reduce_scatter<kWave, kSlots>(d, lane) * a.scale;
+        constexpr int kSpread = kWave / kSlots;
+        const int slot = (lane / kSpread) & (kSlots - 1);
+        const int q = slot / TROPNN_MAX_COMPARISONS, c = slot % TROPNN_MAX_COMPARISONS;
+        if (lane % kSpread == 0 && q < ntb && c < C) {
+            const int t = tb + q;
+            const float gu =
+                dot * surrogate_grad(a.margins[(static_cast<size_t>(b) * a.tables + t) * C + c], a.surrogate);
+            gud[t * C + c] = gu;
+            if (a.gu != nullptr) a.gu[(static_cast<size_t>(t) * C + c) * a.items + b] = gu;
+        }
+    }
+    if (a.grad_x == nullptr) return;
+    __syncthreads();
     feature_walk(gud, idx_s, a.in_f, a.grad_x + static_cast<size_t>(b) * a.in_f, tid, nthr);
 }
 
@@ -363,8 +448,8 @@ __global__ __launch_bounds__(kLutThreads) void pairwise_bwd_table_kernel(LutArgs
     // workgroups to the 8 XCDs in turn) each touch one slice, one dword per
     // 128-byte line, so the grad rows the walk gathers are L2 hits by then
     uint64_t r_next = tid < a.items ? rec_t[tid] : 0ull;
-    const float *gu_t = a.gu + static_cast<size_t>(t) * a.items;
-    float gu_next = thr && tid < a.items ? gu_t[tid] : 0.f;
+    const float *gu_t = a.gu + static_cast<size_t>(t) * (a.full ? C : 1) * a.items;
+    float gu_next = thr && !a.full && tid < a.items ? gu_t[tid] : 0.f;
     uint32_t pf = 0u;
     {
         const int nwg = gridDim.x * gridDim.y;
@@ -526,15 +611,21 @@ __global__ __launch_bounds__(kLutThreads) void pairwise_bwd_table_kernel(LutArgs
 #pragma unroll
             for (int e = 0; e < V; ++e) dst[e] = entry_inside(cur) ? dst[e] + acc[e] : acc[e];
         }
-        // threshold gradient: -gu at the item's min-margin comparison, summed
-        // per wave (fixed tree) into the wave's slots; lane 8c ends with the
-        // wave's sum for comparison c
+        // threshold gradient: -gu at the item's min-margin comparison (full
+        // STE: at every comparison), summed per wave (fixed tree) into the
+        // wave's slots; lane 8c ends with the wave's sum for comparison c
         if (thr) {
-            const float gu = valid ? gu0 : 0.f;
-            const int rr = rec_r(r0) & 7;
             float tv[TROPNN_MAX_COMPARISONS];
+            if (a.full) {
 #pragma unroll
-            for (int c = 0; c < TROPNN_MAX_COMPARISONS; ++c) tv[c] = rr == c ? -gu : 0.f;
+                for (int c = 0; c < TROPNN_MAX_COMPARISONS; ++c)
+                    tv[c] = valid && c < C ? -gu_t[static_cast<size_t>(c) * a.items + tile0 + tidl] : 0.f;
+            } else {
+                const float gu = valid ? gu0 : 0.f;
+                const int rr = rec_r(r0) & 7;
+#pragma unroll
+                for (int c = 0; c < TROPNN_MAX_COMPARISONS; ++c) tv[c] = rr == c ? -gu : 0.f;
+            }
             const float tot = reduce_scatter<kWave, TROPNN_MAX_COMPARISONS>(tv, lane);
             const int c = lane >> 3;
             if ((lane & 7) == 0 && c < C) tp[wave * TROPNN_MAX_COMPARISONS + c] += tot;
@@ -563,7 +654,7 @@ __global__ __launch_bounds__(kLutThreads) void pairwise_bwd_table_kernel(LutArgs
         if (tile0 + nthr < a.items) {
             const bool nv = tile0 + nthr + tidl < a.items;
             r_next = nv ? rec_t[tile0 + nthr + tidl] : 0ull;
-            gu_next = thr && nv ? gu_t[tile0 + nthr + tidl] : 0.f;
+            gu_next = thr && !a.full && nv ? gu_t[tile0 + nthr + tidl] : 0.f;
         }
         __syncthreads();  // LDS is reused by the next tile
     }
@@ -605,6 +696,7 @@ struct FusedArgs {
     uint64_t *gurec;  // [T][B] {gu bits, r} for the scatter kernel, or null
     uint32_t lut_bytes, g_bytes;
     uint32_t g_slice;     // bytes of G one workgroup touches (8 XCDs share the table workgroups)
+    int surrogate;        // TROPNN_SURROGATE_*
     uint64_t quad_magic;  // ceil(2^32 / (out_f / 4)): chunk index -> LUT row
     int items, out_f, tables, comps, rows;
     int slots;  // sorted-list capacity: a tile's items plus K - 1 padding slots per row
@@ -862,7 +954,7 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
                 const uint32_t y = ent[base + q].y;
                 if (j % (S / K) == 0 && (y & kPadSlot) == 0) {
                     const int r = static_cast<int>((y >> 18) & 7u);
-                    const float gu = dot * fast_sigmoid_odd(us[base + q]);
+                    const float gu = dot * surrogate_grad(us[base + q], a.surrogate);
                     if (a.gurec != nullptr)
                         a.gurec[static_cast<size_t>(t) * a.items + tile0 + ((y >> 21) & 1023u)] =
                             static_cast<uint64_t>(__builtin_bit_cast(uint32_t, gu)) | (static_cast<uint64_t>(r) << 32);
@@ -1065,6 +1157,9 @@ hipError_t launch_table(const LutArgs &args, const BackwardPlan &p, hipStream_t 
 
 template <typename T, int N>
 hipError_t launch_item_typed(const ItemArgs &args, const BackwardPlan &p, hipStream_t stream) {
+    if (p.full)
+        return launch_kernel(TROPNN_KERNEL_BACKWARD_ITEM, pairwise_bwd_full_kernel<T, N>, dim3(args.items),
+                             dim3(p.item_threads), p.item_lds_bytes, stream, args);
     return launch_kernel(TROPNN_KERNEL_BACKWARD_ITEM, pairwise_bwd_item_kernel<T, N>, dim3(args.items),
                          dim3(p.item_threads), p.item_lds_bytes, stream, args);
 }
@@ -1140,8 +1235,9 @@ hipError_t launch_anchor_index(const int64_t *anchors, int in_f, int tables, int
     return hipGetLastError();
 }
 
-BackwardPlan plan_backward(const Dims &d) {
+BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     BackwardPlan p{};
+    p.full = ste_mode == TROPNN_STE_FULL;
     const int esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
     // table kernel: V columns per lane (a divisor of the row, at most 4), S
     // lanes per row group: the smallest of 4, 8, 16, 32 whose S * V columns
@@ -1185,7 +1281,7 @@ BackwardPlan plan_backward(const Dims &d) {
     // pieces of it (V = 4 up to 64 columns, else V = 8 and O % 8 == 0), and
     // the table's rows fit in LDS
     p.fused = false;
-    if (d.out_f % 4 == 0 && (d.out_f <= 64 || (d.out_f % 8 == 0 && d.out_f <= 256))) {
+    if (!p.full && d.out_f % 4 == 0 && (d.out_f <= 64 || (d.out_f % 8 == 0 && d.out_f <= 256))) {
         p.fvec = d.out_f <= 64 ? 4 : 8;
         p.fslices = d.out_f <= 128 ? 16 : 32;
         p.fpitch = p.fvec * p.fslices;
@@ -1219,14 +1315,15 @@ BackwardPlan plan_backward(const Dims &d) {
         p.f_lds_bytes = off;
         p.fused = d.rows * p.fpitch * 4 <= 64 * 1024 && off <= 160 * 1024;
     }
-    p.workspace_bytes = static_cast<size_t>(d.tables) * d.items * (p.fused ? sizeof(uint64_t) : sizeof(float));
+    p.workspace_bytes = static_cast<size_t>(d.tables) * d.items *
+                        (p.fused ? sizeof(uint64_t) : (p.full ? d.comps * sizeof(float) : sizeof(float)));
     return p;
 }
 
 hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *grad_out, const void *lut,
-                           const tropnn_route_record *rec, const int32_t *index_offsets,
-                           const int32_t *index_entries, float scale, float *grad_x, float *grad_thr,
-                           float *grad_lut, float *workspace, hipStream_t stream) {
+                           const tropnn_route_record *rec, const float *margins, const int32_t *index_offsets,
+                           const int32_t *index_entries, float scale, int surrogate, float *grad_x,
+                           float *grad_thr, float *grad_lut, float *workspace, hipStream_t stream) {
     const uint64_t *rec64 = reinterpret_cast<const uint64_t *>(rec);
     const int esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
     const uint32_t g_bytes = static_cast<uint32_t>(static_cast<size_t>(d.items) * d.out_f * 4);
@@ -1241,6 +1338,7 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
         f.grad_lut = grad_lut;
         f.grad_thr = grad_thr;
         f.gurec = gurec;
+        f.surrogate = surrogate;
         f.lut_bytes = static_cast<uint32_t>(static_cast<size_t>(d.tables) * d.rows * d.out_f * esize);
         f.g_bytes = g_bytes;
         f.items = d.items;
@@ -1281,9 +1379,11 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
         a.grad_out = grad_out;
         a.lut = lut;
         a.rec = rec64;
+        a.margins = margins;
         a.index_offsets = index_offsets;
         a.index_entries = index_entries;
         a.scale = scale;
+        a.surrogate = surrogate;
         a.grad_x = grad_x;
         a.gu = grad_thr != nullptr ? workspace : nullptr;
         a.lut_bytes = static_cast<uint32_t>(static_cast<size_t>(d.tables) * d.rows * d.out_f * esize);
@@ -1320,6 +1420,7 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
     b.grad_out = grad_out;
     b.rec = rec64;
     b.gu = workspace;
+    b.full = p.full ? 1 : 0;
     b.scale = scale;
     b.grad_lut = grad_lut;
     b.grad_thr = grad_thr;

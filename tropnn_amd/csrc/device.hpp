@@ -119,6 +119,22 @@ __device__ __forceinline__ float fast_sigmoid_odd(float u) {
     return num / den;
 }
 
+// izhikevich surrogate, sign * 2 * sig * (1 - sig) with sig = sigmoid(|u|)
+// and sign = -1 for u > 0, else +1 (so u = 0 gives 0.5), in the reference's op
+// order (layers/surrogate.py:9-13). The logistic is 1 / (1 + exp(-|u|)) with
+// the device expf; the reference's vectorised CPU sigmoid may differ in the
+// last bit.
+__device__ __forceinline__ float izhikevich(float u) {
+    const float sig = 1.0f / (1.0f + expf(-fabsf(u)));
+    const float sign = u > 0.f ? -1.0f : 1.0f;
+    return sign * 2.0f * sig * (1.0f - sig);
+}
+
+// The surrogate derivative selected by TROPNN_SURROGATE_* (wave-uniform).
+__device__ __forceinline__ float surrogate_grad(float u, int surrogate) {
+    return surrogate == TROPNN_SURROGATE_IZHIKEVICH ? izhikevich(u) : fast_sigmoid_odd(u);
+}
+
 // Buffer-resource access (raw buffers, 32-bit offsets). An offset at or past
 // the resource's byte range reads as zero, so masked lanes just pass
 // kOutOfRange instead of branching.

@@ -56,6 +56,7 @@ struct BackwardPlan {
     int item_waves;     // waves per workgroup (one item per workgroup)
     int item_threads;
     int item_lds_bytes; // the item's gu slots [T * C] f32 + the inverse anchor index
+    bool full;          // full STE (every comparison): item kernel variant, general path only
     // fused path (O a multiple of 4 up to 64, or of 8 up to 256, a table's LUT
     // rows within 64 KB as f32): one kernel per table does the LUT gradient, the
     // STE dots and the threshold gradient; a scatter kernel per item the input
@@ -69,7 +70,7 @@ struct BackwardPlan {
     int f_slots;        // sorted-list capacity of a tile (items + padding to whole batches)
     int f_lds_bytes;
     int scatter_lds_bytes;   // gu slots [T * C] f32 + the inverse anchor index
-    size_t workspace_bytes;  // fused: {gu, r} [T][B] u64; else gu [T][B] f32
+    size_t workspace_bytes;  // fused: {gu, r} [T][B] u64; full STE: gu [T][C][B] f32; else gu [T][B] f32
 };
 
 // Row loads a forward wave keeps in flight (its gather chunk), by LUT element
@@ -84,16 +85,17 @@ constexpr int item_wave_tables(int esize, int vec) {
     return esize * vec <= 4 ? 16 : (esize * vec == 8 ? 12 : (esize == 4 ? 6 : 3));
 }
 
-BackwardPlan plan_backward(const Dims &d);
+// ste_mode: TROPNN_STE_MIN_MARGIN or TROPNN_STE_FULL (general path only).
+BackwardPlan plan_backward(const Dims &d, int ste_mode);
 
 hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, const int64_t *anchors,
                           const float *thr, const void *lut, float scale, float *out, tropnn_route_record *rec,
                           int64_t *indices, float *margins, hipStream_t stream);
 
 hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *grad_out, const void *lut,
-                           const tropnn_route_record *rec, const int32_t *index_offsets,
-                           const int32_t *index_entries, float scale, float *grad_x, float *grad_thr,
-                           float *grad_lut, float *workspace, hipStream_t stream);
+                           const tropnn_route_record *rec, const float *margins, const int32_t *index_offsets,
+                           const int32_t *index_entries, float scale, int surrogate, float *grad_x,
+                           float *grad_thr, float *grad_lut, float *workspace, hipStream_t stream);
 
 // Inverse anchor index (see tropnn_hip_build_anchor_index).
 hipError_t launch_anchor_index(const int64_t *anchors, int in_f, int tables, int comps, int32_t *offsets,
