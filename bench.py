@@ -158,9 +158,142 @@ def cpu_baseline(budget_s: float) -> dict:
     }
 
 
+C5_LAYER_BYTES = 313_619_648  # the three layers' FwdBwd algorithmic bytes per c5 step (CE and Adam not counted)
+
+
+def cpu_baseline_c5(budget_s: float) -> dict:
+    """The oracle classifier (the three oracle layers, seeds 0, 1, 2) with
+    torch Adam on the host cores: the same c5 training step, full batch."""
+    import torch
+    import torch.nn.functional as F
+
+    from oracle.pairwise_torch import OraclePairwiseLinear
+    from tropnn_amd.examples import make_c5_batch
+
+    threads = torch.get_num_threads()
+    dims = (784, 128, 128, 10)
+    layers = torch.nn.ModuleList(
+        [OraclePairwiseLinear(a, b, tables=T, comparisons=C, seed=k) for k, (a, b) in enumerate(zip(dims[:-1], dims[1:]))]
+    )
+    opt = torch.optim.Adam(layers.parameters(), lr=1e-3)
+    x, y = make_c5_batch(512, seed=0)
+
+    def step() -> None:
+        opt.zero_grad(set_to_none=True)
+        h = x.unsqueeze(1)
+        for layer in layers:
+            h = layer(h)
+        F.cross_entropy(h.squeeze(1), y).backward()
+        opt.step()
+
+    step()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": 512 / med,
+        "unit": "samples/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"c5 train step (3 oracle layers + CE + torch Adam), batch 512, {len(times)} steps "
+        f"(median {med * 1e3:.1f} ms/step), torch.set_num_threads={threads}",
+    }
+
+
+def bench_c5(args, dev) -> dict:
+    """c5: the pairwise EMNIST classifier
+    784 -> 128 -> 128 -> 10 (T = 136, C = 6, seeds 0, 1, 2), batch 512 of
+    synthetic sparse inputs, one training step = zero_grad, forward, cross
+    entropy, backward, Adam (lr 1e-3) step, captured in one HIP graph per
+    resident batch (4, round-robin) and timed over replays like c2."""
+    import torch
+    import torch.nn.functional as F
+
+    from tropnn_amd.examples import EmnistPairwiseClassifier, make_c5_batch
+
+    model = EmnistPairwiseClassifier().to(dev).train()
+    for layer in model.layers:
+        layer.cache_route_debug = False
+    opt = torch.optim.Adam(model.parameters(), lr=1e-3, fused=True, capturable=True)  # one kernel, step on the device
+    nb = 4
+    batches = [tuple(t.to(dev) for t in make_c5_batch(512, seed=k)) for k in range(nb)]
+
+    def step(k: int) -> None:
+        x, y = batches[k]
+        F.cross_entropy(model(x), y).backward()
+        opt.step()
+
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for w in range(max(3, args.warmup)):
+            opt.zero_grad(set_to_none=True)
+            step(w % nb)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graphs = []
+    for k in range(nb):
+        opt.zero_grad(set_to_none=True)
+        gph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gph):
+            step(k)
+        graphs.append(gph)
+    torch.cuda.synchronize()
+    t0, w = time.perf_counter(), 0
+    while w < args.warmup or time.perf_counter() - t0 < 0.3:
+        graphs[w % nb].replay()
+        w += 1
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        graphs[k % nb].replay()
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) * 1e6 / args.steps
+    log(f"c5 graph {us:.1f} us/step")
+    cpu = cpu_baseline_c5(args.cpu_budget) if args.cpu_budget > 0 else None
+    value = 512 / (us * 1e-6)
+    out = {
+        "metric": "EmnistPairwiseClassifier c5 training samples/s (3 PairwiseLinear layers + CE + Adam)",
+        "value": round(value, 1),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us * 1e-3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: x = rand * (rand >= 0.8), labels randint(0, 10), 4 resident batches round-robin; "
+        "seeded layer init (seeds 0, 1, 2)",
+        "config": {
+            "workload": "c5: EmnistPairwiseClassifier 784->128->128->10, tables 136, comparisons 6, batch 512, "
+            "cross entropy + Adam lr 1e-3, one HIP graph per training step",
+            "batch": 512,
+        },
+        "layer_algorithmic_bytes_per_step": C5_LAYER_BYTES,
+        "layer_algorithmic_GBs": round(C5_LAYER_BYTES / (us * 1e-6) / 1e9, 1),
+        "cpu_baseline": cpu,
+    }
+    if cpu:
+        out["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument(
+        "--workload",
+        choices=("c2", "c5"),
+        default="c2",
+        help="c2: the BASELINE metric (default); c5: the EMNIST classifier training step",
+    )
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work (0 = skip)")
@@ -191,6 +324,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_name(dev)}, library {library_path()}")
+    if args.workload == "c5":
+        print(json.dumps(bench_c5(args, dev)))
+        return 0
 
     layer = PairwiseLinear(I, O, tables=T, comparisons=C, seed=0).to(dev).train()
     layer.cache_route_debug = False  # route debug tensors are not part of the step
