@@ -205,6 +205,89 @@ def cpu_baseline_c5(budget_s: float) -> dict:
     }
 
 
+def bench_c3(args, dev) -> dict:
+    """c3: the c2 layer (128 -> 128, T = 136,
+    C = 6) as eval forward only with f16 LUT reads, at batch 1, 64 and 8192:
+    time per call (one HIP graph per call, replayed back to back over 4
+    resident inputs; at small batches this is the host launch path), the
+    forward kernel's own duration (events its dispatch stamps; the device
+    latency), and the algorithmic-byte rate, F_eval = 4BI + 20TC + 2BTO + 4BO
+    per call."""
+    import torch
+
+    from tropnn_amd import PairwiseLinear
+    from tropnn_amd.backends.pairwise_hip import arm_kernel_events
+
+    layer = PairwiseLinear(I, O, tables=T, comparisons=C, seed=0, device_lut_dtype="f16").to(dev).eval()
+    layer.cache_route_debug = False
+    results = {}
+    for b in (1, 64, 8192):
+        gen = torch.Generator().manual_seed(0)
+        xs = [torch.randn(b, I, generator=gen).to(dev) for _ in range(4)]
+        with torch.no_grad():
+            for x in xs:  # warm the f16 read copy and the allocator
+                layer(x)
+            torch.cuda.synchronize()
+            graphs = []
+            for x in xs:
+                gph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gph):
+                    layer(x)
+                graphs.append(gph)
+        torch.cuda.synchronize()
+        t0, w = time.perf_counter(), 0
+        while w < args.warmup or time.perf_counter() - t0 < 0.3:
+            graphs[w % 4].replay()
+            w += 1
+        torch.cuda.synchronize()
+        n = args.steps
+        t0 = time.perf_counter()
+        for k in range(n):
+            graphs[k % 4].replay()
+        torch.cuda.synchronize()
+        us = (time.perf_counter() - t0) * 1e6 / n
+        # the kernel's own duration over eager calls
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(100)]
+        stream = torch.cuda.current_stream(dev)
+        for e0, e1 in evs:
+            e0.record(stream)
+            e1.record(stream)
+        with torch.no_grad():
+            for k, (e0, e1) in enumerate(evs):
+                arm_kernel_events("forward", e0, e1)
+                layer(xs[k % 4])
+        torch.cuda.synchronize()
+        kus = sorted(1e3 * e0.elapsed_time(e1) for e0, e1 in evs)[len(evs) // 2]
+        algo = 4 * b * I + 20 * T * C + 2 * b * T * O + 4 * b * O
+        results[str(b)] = {
+            "kernel_us": round(kus, 3),
+            "us_per_call": round(us, 3),
+            "samples_per_s": round(b / (us * 1e-6), 1),
+            "algorithmic_bytes": algo,
+            "algorithmic_GBs": round(algo / (us * 1e-6) / 1e9, 1),
+        }
+        log(f"c3 batch {b}: {us:.2f} us/call, kernel {kus:.2f} us")
+    big = results["8192"]
+    return {
+        "metric": "PairwiseLinear c3 eval forward, f16 LUT reads (128->128, T=136, C=6): samples/s at batch 8192, latency at 1 and 64",
+        "value": big["samples_per_s"],
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(big["us_per_call"] * 1e-3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 LUT reads, f32 accumulate",
+        "data": "synthetic: x ~ N(0,1), 4 resident inputs per batch size; seeded module init (seed 0)",
+        "config": {"workload": "c3: PairwiseLinear(128->128, tables=136, comparisons=6) eval forward, f16 LUT [136,64,128]", "batches": [1, 64, 8192]},
+        "per_batch": results,
+        "roofline_8192": {"bound": "hbm", "achieved": big["algorithmic_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(big["algorithmic_GBs"] / HBM_PEAK_GBS, 4)},
+    }
+
+
 def bench_c5(args, dev) -> dict:
     """c5: the pairwise EMNIST classifier
     784 -> 128 -> 128 -> 10 (T = 136, C = 6, seeds 0, 1, 2), batch 512 of
@@ -290,9 +373,10 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument(
         "--workload",
-        choices=("c2", "c5"),
+        choices=("c2", "c3", "c5"),
         default="c2",
-        help="c2: the BASELINE metric (default); c5: the EMNIST classifier training step",
+        help="c2: the BASELINE metric (default); c3: f16 eval forward at batch 1 / 64 / 8192; "
+        "c5: the EMNIST classifier training step",
     )
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
@@ -324,8 +408,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_name(dev)}, library {library_path()}")
-    if args.workload == "c5":
-        print(json.dumps(bench_c5(args, dev)))
+    if args.workload in ("c3", "c5"):
+        print(json.dumps(bench_c3(args, dev) if args.workload == "c3" else bench_c5(args, dev)))
         return 0
 
     layer = PairwiseLinear(I, O, tables=T, comparisons=C, seed=0).to(dev).train()
