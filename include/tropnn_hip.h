@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TROPNN_HIP_ABI_VERSION 4
+#define TROPNN_HIP_ABI_VERSION 5
 
 /* status codes */
 #define TROPNN_OK 0
@@ -98,13 +98,30 @@ int tropnn_hip_lut_forward_batch_f16(size_t batch, size_t tables, size_t compari
  *   route_record      = per (table, item) record above, or NULL         [tables, items]
  *   indices[b,t]      = code as int64, or NULL                          [items, tables]
  *   margins[b,t,c]    = (x[b,a] - x[b,b']) - thr[t,c], or NULL          [items, tables, comparisons]
+ *   codes[b,t]        = code as uint8, or NULL                          [items, tables]
  * lut_dtype selects float (TROPNN_LUT_F32) or binary16 (TROPNN_LUT_F16) rows.
+ * indices and margins are the route-debug tensors of the reference's shell
+ * (layers/base.py:78-83); codes is their compact form (comparisons <= 8), one
+ * byte per (item, table) instead of 8 + 4 * comparisons.
  */
 int tropnn_hip_pairwise_forward(int64_t items, int64_t in_features, int64_t out_features, int64_t tables,
                                 int64_t comparisons, const float *latent, const int64_t *anchors,
                                 const float *thresholds, const void *lut, int lut_dtype, float output_scale,
                                 float *output, tropnn_route_record *route_record, int64_t *indices, float *margins,
-                                tropnn_stream_t stream);
+                                uint8_t *codes, tropnn_stream_t stream);
+
+/*
+ * Route only: the comparator codes and margins of every (item, table), with
+ * no LUT access. Replaces PairwiseLinear._compute_indices
+ * (layers/pairwise.py:127-135), which returns (indices, margins). Writes any
+ * of codes (uint8 [items, tables]), indices (int64 [items, tables]) and
+ * margins (f32 [items, tables, comparisons]); NULL skips one. The margins are
+ * bit-identical to the forward's. Used to materialise route-debug tensors
+ * after a forward that wrote only codes.
+ */
+int tropnn_hip_pairwise_route(int64_t items, int64_t in_features, int64_t tables, int64_t comparisons,
+                              const float *latent, const int64_t *anchors, const float *thresholds, uint8_t *codes,
+                              int64_t *indices, float *margins, tropnn_stream_t stream);
 
 /* Bytes of device workspace tropnn_hip_pairwise_backward needs for these dims
  * and STE mode (0 and an error message for invalid arguments). */

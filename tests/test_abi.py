@@ -77,19 +77,38 @@ def _err(lib) -> str:
 def test_forward_rejects_bad_arguments(lib):
     fwd = lib.tropnn_hip_pairwise_forward
     # tables < 1
-    assert fwd(4, 8, 5, 0, 3, 8, 8, 8, 8, 0, 1.0, 8, None, None, None, None) == 1
+    assert fwd(4, 8, 5, 0, 3, 8, 8, 8, 8, 0, 1.0, 8, None, None, None, None, None) == 1
     assert "tables" in _err(lib)
     # comparisons above the supported maximum: unsupported, not invalid
-    assert fwd(4, 8, 5, 3, 9, 8, 8, 8, 8, 0, 1.0, 8, None, None, None, None) == 2
+    assert fwd(4, 8, 5, 3, 9, 8, 8, 8, 8, 0, 1.0, 8, None, None, None, None, None) == 2
     assert "comparisons" in _err(lib)
     # unknown LUT dtype
-    assert fwd(4, 8, 5, 3, 3, 8, 8, 8, 8, 7, 1.0, 8, None, None, None, None) == 1
+    assert fwd(4, 8, 5, 3, 3, 8, 8, 8, 8, 7, 1.0, 8, None, None, None, None, None) == 1
     # NULL buffers
-    assert fwd(4, 8, 5, 3, 3, None, 8, 8, 8, 0, 1.0, 8, None, None, None, None) == 1
+    assert fwd(4, 8, 5, 3, 3, None, 8, 8, 8, 0, 1.0, 8, None, None, None, None, None) == 1
     assert "non-NULL" in _err(lib)
     # empty batch is a no-op success
-    assert fwd(0, 8, 5, 3, 3, None, None, None, None, 0, 1.0, None, None, None, None, None) == 0
+    assert fwd(0, 8, 5, 3, 3, None, None, None, None, 0, 1.0, None, None, None, None, None, None) == 0
     assert _err(lib) == ""
+
+
+def test_forward_rejects_misaligned_debug_outputs(lib):
+    fwd = lib.tropnn_hip_pairwise_forward
+    # int64 indices at an odd address (never dereferenced: validation fails first)
+    assert fwd(4, 8, 8, 3, 3, 16, 16, 16, 16, 0, 1.0, 16, None, 12, None, None, None) == 1
+    assert "aligned" in _err(lib)
+
+
+def test_route_rejects_bad_arguments(lib):
+    route = lib.tropnn_hip_pairwise_route
+    # items, in, tables, comps, latent, anchors, thresholds, codes, indices, margins, stream
+    assert route(4, 8, 0, 3, 16, 16, 16, 16, None, None, None) == 1 and "tables" in _err(lib)
+    assert route(4, 8, 3, 9, 16, 16, 16, 16, None, None, None) == 2 and "comparisons" in _err(lib)
+    assert route(4, 8, 3, 3, None, 16, 16, 16, None, None, None) == 1 and "non-NULL" in _err(lib)
+    assert route(4, 8, 3, 3, 16, 16, 16, None, 12, None, None) == 1 and "aligned" in _err(lib)
+    # nothing asked for, or an empty batch: a no-op success without a launch
+    assert route(4, 8, 3, 3, None, None, None, None, None, None, None) == 0 and _err(lib) == ""
+    assert route(0, 8, 3, 3, None, None, None, 16, 16, 16, None) == 0 and _err(lib) == ""
 
 
 def test_backward_rejects_bad_arguments(lib):

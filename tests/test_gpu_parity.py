@@ -381,6 +381,77 @@ def test_route_debug_cache_off():
     assert hip._last_indices is None and hip._last_margins is None
 
 
+# ---------------------------------------------------------------- route-debug codes format
+@pytest.mark.parametrize(
+    "i,o,t,c,b",
+    [(16, 8, 4, 3, 5), (128, 128, 136, 6, 512), (64, 300, 17, 8, 40), (300, 4, 70, 1, 33), (1024, 1100, 64, 5, 3)],
+)
+def test_lazy_route_debug_codes(i, o, t, c, b):
+    """cache_route_debug='lazy': the forward writes uint8 codes only; int64
+    codes and margins materialise on first access, bit-identical to the
+    eager cache and to the oracle's route. Output widths of 300 and 1100
+    span several column tiles, of which only the first writes."""
+    ref, hip = make_pair(i, o, t, c, seed=t + c, thr_std=0.5)
+    x = seeded((b, i), seed=i + b)
+    xd = x.to(DEV)
+    hip.eval()
+    with torch.no_grad():
+        y_eager = hip(xd)
+        eager_idx, eager_mar = hip._last_indices.clone(), hip._last_margins.clone()
+        hip.cache_route_debug = "lazy"
+        y_lazy = hip(xd)
+    assert torch.equal(y_lazy, y_eager)
+    codes = hip._last_codes
+    assert codes.dtype == torch.uint8 and codes.shape == (b, 1, t)
+    expect = routing_np.route_codes(x.numpy(), ref.anchors.numpy(), ref.thresholds.detach().numpy())
+    np.testing.assert_array_equal(codes.cpu().reshape(b, t).numpy(), expect)
+    assert torch.equal(hip._last_indices, eager_idx)
+    assert hip._last_margins.shape == (b, 1, t, c)
+    assert torch.equal(hip._last_margins.view(torch.int32), eager_mar.view(torch.int32))
+
+
+def test_route_only_entry_point():
+    """pairwise_hip_route against the oracle's codes and margins, at an item x
+    table count that is not a multiple of the launch's 256 threads."""
+    from tropnn_amd import pairwise_hip_route
+
+    ref, hip = make_pair(40, 4, 13, 7, seed=5, thr_std=0.4)
+    x = seeded((3, 7, 40), seed=11)
+    codes, idx, mar = pairwise_hip_route(x.to(DEV), hip.anchors, hip.thresholds, codes=True)
+    torch.cuda.synchronize()
+    xs = x.reshape(21, 40).numpy()
+    expect = routing_np.route_codes(xs, ref.anchors.numpy(), ref.thresholds.detach().numpy())
+    margins = routing_np.margins_f32(xs, ref.anchors.numpy(), ref.thresholds.detach().numpy())
+    assert codes.shape == (3, 7, 13) and idx.shape == (3, 7, 13) and mar.shape == (3, 7, 13, 7)
+    np.testing.assert_array_equal(codes.cpu().reshape(21, 13).numpy(), expect)
+    np.testing.assert_array_equal(idx.cpu().reshape(21, 13).numpy(), expect)
+    np.testing.assert_array_equal(mar.cpu().reshape(21, 13, 7).numpy().view(np.uint32), margins.view(np.uint32))
+    c0, i0, m0 = pairwise_hip_route(torch.zeros(0, 1, 40, device=DEV), hip.anchors, hip.thresholds, codes=True)
+    assert c0.shape == (0, 1, 13) and i0.shape == (0, 1, 13) and m0.shape == (0, 1, 13, 7)
+
+
+@pytest.mark.parametrize("min_margin", [True, False])
+def test_lazy_route_debug_training(min_margin):
+    """Training with the lazy codes format gives the eager path's gradients;
+    its margins are refused once an in-place update has touched the
+    thresholds they were computed from."""
+    ref, hip = make_pair(32, 16, 9, 5, seed=3, thr_std=0.3, use_min_margin_ste=min_margin)
+    hip.cache_route_debug = "lazy"
+    x = seeded((20, 32), 7)
+    g = seeded((20, 1, 16), 8)
+    yx_ref, yx_hip = train_step(ref, hip, x, g)
+    assert_train_parity(ref, hip, yx_ref, yx_hip)
+    margins = routing_np.margins_f32(x.numpy(), ref.anchors.numpy(), ref.thresholds.detach().numpy())
+    got = hip._last_margins.cpu().reshape(20, 9, 5).numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), margins.view(np.uint32))
+    hip(x.to(DEV))
+    with torch.no_grad():
+        hip.thresholds.add_(0.1)
+    with pytest.raises(RuntimeError, match="lazy"):
+        _ = hip._last_margins
+    assert hip._last_codes.shape == (20, 1, 9)
+
+
 def test_single_hip_runtime_in_process():
     """libtropnn_hip.so must bind the HIP runtime torch already loaded."""
     from tropnn_amd.backends.pairwise_hip import load_library

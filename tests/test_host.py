@@ -87,3 +87,46 @@ def test_bench_refuses_more_than_one_gpu():
     assert proc.returncode == 2
     assert "one GPU" in proc.stderr
     assert proc.stdout == ""
+
+
+def test_route_debug_mode_is_validated():
+    layer = PairwiseLinear(8, 5, tables=3, comparisons=2)
+    layer.cache_route_debug = "codes"
+    with pytest.raises(ValueError, match="cache_route_debug"):
+        layer(torch.zeros(2, 8))
+
+
+def test_lazy_route_debug_materialises_once():
+    """The lazy record widens uint8 codes to int64 on first access and calls
+    the margin recomputation exactly once."""
+    from tropnn_amd.layers.base import RouteDebug
+
+    calls = []
+
+    def recompute():
+        calls.append(1)
+        return torch.full((2, 1, 3, 2), 0.5)
+
+    codes = torch.tensor([[[0, 3, 255]], [[1, 2, 128]]], dtype=torch.uint8)
+    rec = RouteDebug(codes=codes, recompute_margins=recompute)
+    assert rec.codes is codes and not calls
+    idx = rec.indices
+    assert idx.dtype == torch.int64 and idx.tolist() == codes.long().tolist()
+    assert rec.indices is idx
+    m1, m2 = rec.margins, rec.margins
+    assert m1 is m2 and len(calls) == 1
+    eager = RouteDebug(indices=idx, margins=m1)
+    assert torch.equal(eager.codes, codes) and eager.margins is m1
+
+
+def test_route_debug_attributes_are_settable():
+    """The reference shell assigns _last_indices / _last_margins directly
+    (layers/base.py:78-83); the properties accept that."""
+    layer = PairwiseLinear(8, 5, tables=3, comparisons=2)
+    idx = torch.zeros(2, 1, 3, dtype=torch.long)
+    layer._last_indices = idx
+    layer._last_margins = torch.ones(2, 1, 3, 2)
+    assert layer._last_indices is idx and float(layer._last_margins.sum()) == 12.0
+    layer._last_indices = None
+    layer._last_margins = None
+    assert layer._last_indices is None and layer._last_margins is None and layer._last_codes is None

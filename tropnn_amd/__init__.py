@@ -1,7 +1,14 @@
 """MI355X-native PairwiseLinear: `PairwiseLinear(..., backend="hip")` runs the
 comparator route, LUT gather-sum and min-margin STE backward as gfx950 HIP
 kernels in libtropnn_hip.so (C ABI: include/tropnn_hip.h)."""
-from .backends import has_pairwise_hip, pairwise_hip, pairwise_hip_forward
+from .backends import has_pairwise_hip, pairwise_hip, pairwise_hip_forward, pairwise_hip_route
 from .layers import PairwiseLinear, RoutedLinearBase
 
-__all__ = ["PairwiseLinear", "RoutedLinearBase", "has_pairwise_hip", "pairwise_hip", "pairwise_hip_forward"]
+__all__ = [
+    "PairwiseLinear",
+    "RoutedLinearBase",
+    "has_pairwise_hip",
+    "pairwise_hip",
+    "pairwise_hip_forward",
+    "pairwise_hip_route",
+]

@@ -1,3 +1,3 @@
-from .pairwise_hip import has_pairwise_hip, pairwise_hip, pairwise_hip_forward
+from .pairwise_hip import has_pairwise_hip, pairwise_hip, pairwise_hip_forward, pairwise_hip_route
 
-__all__ = ["has_pairwise_hip", "pairwise_hip", "pairwise_hip_forward"]
+__all__ = ["has_pairwise_hip", "pairwise_hip", "pairwise_hip_forward", "pairwise_hip_route"]

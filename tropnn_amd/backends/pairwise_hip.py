@@ -26,7 +26,7 @@ from typing import Any
 import torch
 from torch import Tensor
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 LUT_F32, LUT_F16 = 0, 1
 SURROGATE_IDS = {"fast_sigmoid_odd": 0, "izhikevich": 1}
 STE_MIN_MARGIN, STE_FULL = 0, 1
@@ -50,6 +50,7 @@ EXPORTED_SYMBOLS = (
     "tropnn_hip_lut_forward_batch_f32",
     "tropnn_hip_lut_forward_batch_f16",
     "tropnn_hip_pairwise_forward",
+    "tropnn_hip_pairwise_route",
     "tropnn_hip_pairwise_backward_workspace_size",
     "tropnn_hip_pairwise_backward",
     "tropnn_hip_build_anchor_index",
@@ -74,8 +75,10 @@ def _declare(lib: ctypes.CDLL) -> None:
         fn = getattr(lib, name)
         fn.argtypes = [sz, sz, sz, sz, sz, p, p, p, p, p, f, p]
         fn.restype = i
-    lib.tropnn_hip_pairwise_forward.argtypes = [i64, i64, i64, i64, i64, p, p, p, p, i, f, p, p, p, p, p]
+    lib.tropnn_hip_pairwise_forward.argtypes = [i64, i64, i64, i64, i64, p, p, p, p, i, f, p, p, p, p, p, p]
     lib.tropnn_hip_pairwise_forward.restype = i
+    lib.tropnn_hip_pairwise_route.argtypes = [i64, i64, i64, i64, p, p, p, p, p, p, p]
+    lib.tropnn_hip_pairwise_route.restype = i
     lib.tropnn_hip_pairwise_backward_workspace_size.argtypes = [i64, i64, i64, i64, i64, i, i]
     lib.tropnn_hip_pairwise_backward_workspace_size.restype = sz
     lib.tropnn_hip_build_anchor_index.argtypes = [i64, i64, i64, p, p, p, p]
@@ -233,12 +236,14 @@ def _route_forward(
     *,
     output_scale: float,
     want_record: bool,
-    return_route: bool,
+    return_route: bool | str,
     want_margins: bool = False,
 ) -> tuple[Tensor, Tensor | None, Tensor, Tensor, Tensor | None]:
     """One fused forward launch. Returns (output, record, indices, margins,
     saved_margins); saved_margins [items, tables, comparisons] is the margins
-    tensor the full-STE backward reads (want_margins), else None."""
+    tensor the full-STE backward reads (want_margins), else None.
+    return_route: True = int64 indices and f32 margins; "codes" = uint8 codes
+    in place of indices and empty margins; False = both empty."""
     batch, steps, in_features, tables, comps, out_features = _validate(latent, anchors, thresholds, lut_read)
     check_anchors(anchors, in_features)
     items = batch * steps
@@ -247,7 +252,9 @@ def _route_forward(
     anc, thr, lut_c = anchors.contiguous(), thresholds.contiguous(), lut_read.contiguous()
     out = torch.empty((items, out_features), device=dev, dtype=torch.float32)
     record = torch.empty((tables, items), device=dev, dtype=torch.int64) if want_record else None
-    if return_route:
+    full_route = return_route is True
+    codes = torch.empty((items, tables), device=dev, dtype=torch.uint8) if return_route == "codes" else None
+    if full_route:
         indices = torch.empty((items, tables), device=dev, dtype=torch.int64)
         margins = torch.empty((items, tables, comps), device=dev, dtype=torch.float32)
     else:
@@ -255,7 +262,7 @@ def _route_forward(
         margins = torch.empty((items, 0), device=dev, dtype=torch.float32)
     saved = None  # margins the full-STE backward reads
     if want_margins:
-        saved = margins if return_route else torch.empty((items, tables, comps), device=dev, dtype=torch.float32)
+        saved = margins if full_route else torch.empty((items, tables, comps), device=dev, dtype=torch.float32)
     lib = load_library()
     rc = lib.tropnn_hip_pairwise_forward(
         items,
@@ -271,14 +278,18 @@ def _route_forward(
         float(output_scale),
         _ptr(out),
         _ptr(record),
-        _ptr(indices) if return_route else None,
-        _ptr(margins) if return_route else _ptr(saved),
+        _ptr(indices) if full_route else None,
+        _ptr(margins) if full_route else _ptr(saved),
+        _ptr(codes),
         _stream(dev),
     )
     _check(rc, "tropnn_hip_pairwise_forward")
-    if return_route:
+    if full_route:
         idx_view = indices.view(batch, steps, tables)
         mar_view = margins.view(batch, steps, tables, comps)
+    elif codes is not None:
+        idx_view = codes.view(batch, steps, tables)
+        mar_view = margins.view(batch, steps, 0)
     else:
         idx_view = indices.view(batch, steps, 0)
         mar_view = margins.view(batch, steps, 0)
@@ -306,7 +317,7 @@ class _PairwiseHipFunction(torch.autograd.Function):
         min_margin: bool,
         surrogate: str,
         output_scale: float,
-        return_route: bool,
+        return_route: bool | str,
     ) -> tuple[Tensor, Tensor, Tensor]:
         needs_lut = ctx.needs_input_grad[3]
         needs_route = ste and (ctx.needs_input_grad[0] or ctx.needs_input_grad[2])
@@ -396,7 +407,7 @@ def pairwise_hip(
     output_scale: float = 1.0,
     lut_read: Tensor | None = None,
     ste: bool = True,
-    return_route: bool = True,
+    return_route: bool | str = True,
 ) -> tuple[Tensor, Tensor, Tensor]:
     """HIP counterpart of pairwise_tilelang (backends/pairwise_tilelang.py:537-549).
 
@@ -404,7 +415,9 @@ def pairwise_hip(
     lut [T,2^C,O] f32 (the parameter gradients flow to). Returns
     (output [B,S,O] = output_scale * sum_t lut[t, code], indices [B,S,T] int64,
     margins [B,S,T,C] f32); with return_route=False the last two are empty
-    [B,S,0] tensors, as the Zig path returns (layers/pairwise.py:223-225).
+    [B,S,0] tensors, as the Zig path returns (layers/pairwise.py:223-225);
+    with return_route="codes" the second is the uint8 codes [B,S,T] and the
+    third is empty (pairwise_hip_route computes margins on demand).
 
     lut_read: the tensor the kernels read, e.g. an f16 copy of lut (f32 by
     default = lut itself). ste: carry the STE gradient (min-margin, or every
@@ -416,6 +429,8 @@ def pairwise_hip(
     """
     if surrogate not in SURROGATE_IDS:
         raise ValueError(f"Pairwise HIP backend does not support surrogate={surrogate!r}")
+    if return_route not in (True, False, "codes"):
+        raise ValueError(f"return_route must be True, False or 'codes', got {return_route!r}")
     _require_gpu(latent, anchors, thresholds, lut)
     if lut_read is None:
         lut_read = lut
@@ -429,8 +444,61 @@ def pairwise_hip(
         bool(use_min_margin_ste),
         surrogate,
         float(output_scale),
-        bool(return_route),
+        return_route if return_route == "codes" else bool(return_route),
     )
+
+
+def pairwise_hip_route(
+    latent: Tensor,
+    anchors: Tensor,
+    thresholds: Tensor,
+    *,
+    codes: bool = False,
+    indices: bool = True,
+    margins: bool = True,
+) -> tuple[Tensor | None, Tensor | None, Tensor | None]:
+    """Route only, the HIP counterpart of PairwiseLinear._compute_indices
+    (layers/pairwise.py:127-135): returns (codes [B,S,T] uint8, indices
+    [B,S,T] int64, margins [B,S,T,C] f32), None for each one not asked for.
+    No LUT access and no autograd; the margins are bit-identical to the
+    forward's."""
+    _require_gpu(latent, anchors, thresholds)
+    if latent.ndim != 3:
+        raise ValueError(f"latent must have shape [batch, steps, in_features], got {tuple(latent.shape)}")
+    if latent.dtype != torch.float32 or thresholds.dtype != torch.float32:
+        raise TypeError(f"Pairwise HIP backend expects float32 latent and thresholds, got {latent.dtype}, {thresholds.dtype}")
+    if anchors.dtype != torch.int64:
+        raise TypeError(f"anchors must be int64, got {anchors.dtype}")
+    if anchors.ndim != 3 or anchors.shape[2] != 2:
+        raise ValueError(f"anchors must have shape [tables, comparisons, 2], got {tuple(anchors.shape)}")
+    batch, steps, in_features = latent.shape
+    tables, comps, _ = anchors.shape
+    if thresholds.shape != (tables, comps):
+        raise ValueError(f"thresholds must have shape {(tables, comps)}, got {tuple(thresholds.shape)}")
+    if comps > MAX_COMPARISONS:
+        raise NotImplementedError(f"Pairwise HIP backend supports comparisons <= {MAX_COMPARISONS}, got {comps}")
+    check_anchors(anchors, in_features)
+    items = batch * steps
+    dev = latent.device
+    x = latent.detach().reshape(items, in_features).contiguous()
+    c_out = torch.empty((batch, steps, tables), device=dev, dtype=torch.uint8) if codes else None
+    i_out = torch.empty((batch, steps, tables), device=dev, dtype=torch.int64) if indices else None
+    m_out = torch.empty((batch, steps, tables, comps), device=dev, dtype=torch.float32) if margins else None
+    rc = load_library().tropnn_hip_pairwise_route(
+        items,
+        in_features,
+        tables,
+        comps,
+        _ptr(x),
+        _ptr(anchors.contiguous()),
+        _ptr(thresholds.detach().contiguous()),
+        _ptr(c_out),
+        _ptr(i_out),
+        _ptr(m_out),
+        _stream(dev),
+    )
+    _check(rc, "tropnn_hip_pairwise_route")
+    return c_out, i_out, m_out
 
 
 def pairwise_hip_forward(

@@ -123,14 +123,15 @@ int tropnn_hip_pairwise_forward(int64_t items, int64_t in_features, int64_t out_
                                 int64_t comparisons, const float *latent, const int64_t *anchors,
                                 const float *thresholds, const void *lut, int lut_dtype, float output_scale,
                                 float *output, tropnn_route_record *route_record, int64_t *indices, float *margins,
-                                tropnn_stream_t stream) {
+                                uint8_t *codes, tropnn_stream_t stream) {
     tropnn::Dims d{};
     if (int rc = make_dims(items, in_features, out_features, tables, comparisons, lut_dtype, d)) return rc;
     const tropnn::ForwardPlan p = tropnn::plan_forward(d);
     if (int rc = check_forward_ptrs(d, p, latent, anchors, thresholds, lut, output)) return rc;
     if (d.items == 0) return ok();
-    if (route_record && misaligned(route_record, 8))
-        return fail(TROPNN_ERR_INVALID_ARGUMENT, "route_record must be 8-byte aligned");
+    if ((route_record && misaligned(route_record, 8)) || (indices && misaligned(indices, 8)) ||
+        (margins && misaligned(margins, 4)))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "route_record, indices and margins must be aligned to their element size");
     if (p.lds_bytes > 64 * 1024)
         return fail(TROPNN_ERR_UNSUPPORTED, "forward needs %d bytes of LDS (tables too large)", p.lds_bytes);
     // the gather addresses the LUT through one buffer resource with 32-bit offsets
@@ -139,7 +140,7 @@ int tropnn_hip_pairwise_forward(int64_t items, int64_t in_features, int64_t out_
         return fail(TROPNN_ERR_UNSUPPORTED, "LUT of %lld bytes exceeds the forward's 2 GiB limit",
                     (long long)lut_bytes);
     hipError_t e = tropnn::launch_forward(d, p, latent, anchors, thresholds, lut, output_scale, output, route_record,
-                                          indices, margins, static_cast<hipStream_t>(stream));
+                                          indices, margins, codes, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail("pairwise forward launch", e);
     return ok();
 }
@@ -150,7 +151,7 @@ int tropnn_hip_lut_forward_batch_f32(size_t batch, size_t tables, size_t compari
                                      tropnn_stream_t stream) {
     return tropnn_hip_pairwise_forward((int64_t)batch, (int64_t)input_dim, (int64_t)output_dim, (int64_t)tables,
                                        (int64_t)comparisons, inputs, anchors, offsets, weights, TROPNN_LUT_F32,
-                                       output_scale, outputs, nullptr, nullptr, nullptr, stream);
+                                       output_scale, outputs, nullptr, nullptr, nullptr, nullptr, stream);
 }
 
 int tropnn_hip_lut_forward_batch_f16(size_t batch, size_t tables, size_t comparisons, size_t input_dim,
@@ -159,7 +160,24 @@ int tropnn_hip_lut_forward_batch_f16(size_t batch, size_t tables, size_t compari
                                      tropnn_stream_t stream) {
     return tropnn_hip_pairwise_forward((int64_t)batch, (int64_t)input_dim, (int64_t)output_dim, (int64_t)tables,
                                        (int64_t)comparisons, inputs, anchors, offsets, weights_f16, TROPNN_LUT_F16,
-                                       output_scale, outputs, nullptr, nullptr, nullptr, stream);
+                                       output_scale, outputs, nullptr, nullptr, nullptr, nullptr, stream);
+}
+
+int tropnn_hip_pairwise_route(int64_t items, int64_t in_features, int64_t tables, int64_t comparisons,
+                              const float *latent, const int64_t *anchors, const float *thresholds, uint8_t *codes,
+                              int64_t *indices, float *margins, tropnn_stream_t stream) {
+    tropnn::Dims d{};
+    if (int rc = make_dims(items, in_features, 1, tables, comparisons, TROPNN_LUT_F32, d)) return rc;
+    if (d.items == 0 || (!codes && !indices && !margins)) return ok();
+    if (!latent || !anchors || !thresholds)
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "latent, anchors and thresholds must be non-NULL");
+    if (misaligned(latent, 4) || misaligned(thresholds, 4) || misaligned(anchors, 8) || (indices && misaligned(indices, 8)) ||
+        (margins && misaligned(margins, 4)))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "a device pointer is not aligned to its element size");
+    hipError_t e = tropnn::launch_route(d, latent, anchors, thresholds, codes, indices, margins,
+                                        static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail("pairwise route launch", e);
+    return ok();
 }
 
 size_t tropnn_hip_pairwise_backward_workspace_size(int64_t items, int64_t in_features, int64_t out_features,

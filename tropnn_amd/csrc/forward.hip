@@ -19,7 +19,8 @@
 //      first lane writes to the wave's own LDS code list. Training also picks
 //      argmin |margin| inside each P-lane group with DPP moves on a 64-bit key
 //      and the winning lane writes the route record; the debug path writes
-//      int64 codes and f32 margins;
+//      uint8 codes (one coalesced store per wave from the code list), int64
+//      codes and f32 margins, from the first column tile only;
 //   3. gather: the wave reads its codes back 16 at a time (one broadcast LDS
 //      read), moves them to scalar registers, and loads each table's row with
 //      one buffer load whose row offset is a scalar: lane l reads columns
@@ -45,6 +46,7 @@ struct FwdArgs {
     uint64_t *rec;
     int64_t *indices;
     float *margins;
+    uint8_t *codes;
     uint32_t lut_bytes;  // buffer range of the LUT (<= 2^31)
     int items, in_f, out_f, tables, comps;
     int row_bytes, table_bytes;
@@ -100,8 +102,10 @@ __device__ __forceinline__ RouteOut route_ballot(const FwdArgs &p, const float *
     if (head) my_codes[j] = static_cast<uint8_t>(code);
     if constexpr (DEBUG) {
         const size_t bt = static_cast<size_t>(item) * p.tables + t;
-        if (p.margins != nullptr && q.valid) p.margins[bt * p.comps + c] = m;
-        if (p.indices != nullptr && head) p.indices[bt] = code;
+        if (blockIdx.y == 0) {
+            if (p.margins != nullptr && q.valid) p.margins[bt * p.comps + c] = m;
+            if (p.indices != nullptr && head) p.indices[bt] = code;
+        }
     }
     RouteOut r{0ull, false};
     if constexpr (TRAIN) {
@@ -181,6 +185,10 @@ __global__ __launch_bounds__(1024) void pairwise_forward_kernel(FwdArgs a) {
             if (ro[j].win) a.rec[static_cast<size_t>(t_begin + j * tpb + slot) * a.items + item] = ro[j].rec;
     }
     // LDS operations of one wave complete in order: the code list is ready
+    if constexpr (DEBUG) {
+        if (a.codes != nullptr && blockIdx.y == 0)
+            for (int k = lane; k < n_t; k += kWave) a.codes[static_cast<size_t>(item) * a.tables + t_begin + k] = my_codes[k];
+    }
 
     // 3. gather + sum over the wave's tables
     const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(a.lut, a.lut_bytes);
@@ -240,6 +248,41 @@ __global__ __launch_bounds__(1024) void pairwise_forward_kernel(FwdArgs a) {
     }
 }
 
+// Route only (no gather): one thread per (item, table) evaluates the table's
+// comparisons in order and writes any of uint8 codes, int64 codes and f32
+// margins, laid out [items][tables] and [items][tables][comparisons]. The
+// margin is the same two f32 subtractions as the forward's, so both write
+// identical bits. Restates layers/pairwise.py:127-135.
+struct RouteArgs {
+    const float *x;
+    const int64_t *anchors;
+    const float *thr;
+    uint8_t *codes;
+    int64_t *indices;
+    float *margins;
+    int items, in_f, tables, comps;
+};
+
+constexpr int kRouteThreads = 256;
+
+__global__ __launch_bounds__(kRouteThreads) void pairwise_route_kernel(RouteArgs a) {
+    const int k = blockIdx.x * kRouteThreads + threadIdx.x;  // item * tables + table
+    if (k >= a.items * a.tables) return;
+    const int item = k / a.tables;
+    const int t = k - item * a.tables;
+    const float *xr = a.x + static_cast<size_t>(item) * a.in_f;
+    int code = 0;
+    for (int c = 0; c < a.comps; ++c) {
+        const size_t q = static_cast<size_t>(t) * a.comps + c;
+        const float m = (xr[clamp_index(a.anchors[2 * q], a.in_f)] - xr[clamp_index(a.anchors[2 * q + 1], a.in_f)]) -
+                        a.thr[q];
+        code |= (m > 0.f ? 1 : 0) << c;
+        if (a.margins != nullptr) a.margins[static_cast<size_t>(k) * a.comps + c] = m;
+    }
+    if (a.codes != nullptr) a.codes[k] = static_cast<uint8_t>(code);
+    if (a.indices != nullptr) a.indices[k] = code;
+}
+
 template <typename T, int N>
 hipError_t launch_typed(const FwdArgs &args, const ForwardPlan &p, bool train, bool debug, hipStream_t stream) {
     const dim3 grid(p.blocks, p.o_tiles), block(p.threads);
@@ -296,7 +339,7 @@ ForwardPlan plan_forward(const Dims &d) {
 
 hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, const int64_t *anchors,
                           const float *thr, const void *lut, float scale, float *out, tropnn_route_record *rec,
-                          int64_t *indices, float *margins, hipStream_t stream) {
+                          int64_t *indices, float *margins, uint8_t *codes, hipStream_t stream) {
     const int esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
     FwdArgs a{};
     a.x = x;
@@ -308,6 +351,7 @@ hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, c
     a.rec = reinterpret_cast<uint64_t *>(rec);
     a.indices = indices;
     a.margins = margins;
+    a.codes = codes;
     a.lut_bytes = static_cast<uint32_t>(static_cast<size_t>(d.tables) * d.rows * d.out_f * esize);
     a.items = d.items;
     a.in_f = d.in_f;
@@ -322,7 +366,7 @@ hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, c
     a.codes_off = p.codes_off;
     a.red_off = p.red_off;
     const bool train = rec != nullptr;
-    const bool debug = indices != nullptr || margins != nullptr;
+    const bool debug = indices != nullptr || margins != nullptr || codes != nullptr;
     if (d.lut_dtype == TROPNN_LUT_F16) {
         switch (p.vec) {
             case 8: return launch_typed<_Float16, 8>(a, p, train, debug, stream);
@@ -336,6 +380,15 @@ hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, c
         case 2: return launch_typed<float, 2>(a, p, train, debug, stream);
         default: return launch_typed<float, 1>(a, p, train, debug, stream);
     }
+}
+
+hipError_t launch_route(const Dims &d, const float *x, const int64_t *anchors, const float *thr, uint8_t *codes,
+                        int64_t *indices, float *margins, hipStream_t stream) {
+    RouteArgs a{x, anchors, thr, codes, indices, margins, d.items, d.in_f, d.tables, d.comps};
+    const int units = d.items * d.tables;
+    const dim3 grid((units + kRouteThreads - 1) / kRouteThreads), block(kRouteThreads);
+    hipLaunchKernelGGL(pairwise_route_kernel, grid, block, 0, stream, a);
+    return hipGetLastError();
 }
 
 }  // namespace tropnn

@@ -90,7 +90,11 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode);
 
 hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, const int64_t *anchors,
                           const float *thr, const void *lut, float scale, float *out, tropnn_route_record *rec,
-                          int64_t *indices, float *margins, hipStream_t stream);
+                          int64_t *indices, float *margins, uint8_t *codes, hipStream_t stream);
+
+// Route only: codes (uint8 and / or int64) and margins, no gather.
+hipError_t launch_route(const Dims &d, const float *x, const int64_t *anchors, const float *thr, uint8_t *codes,
+                        int64_t *indices, float *margins, hipStream_t stream);
 
 hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *grad_out, const void *lut,
                            const tropnn_route_record *rec, const float *margins, const int32_t *index_offsets,

@@ -8,14 +8,14 @@ interchange with it; `_route_output` dispatches to the HIP kernels
 from __future__ import annotations
 
 import math
-from typing import Literal
+from typing import Callable, Literal
 
 import torch
 import torch.nn as nn
 from torch import Tensor
 
 from ..backend import REFERENCE_BACKENDS, Backend
-from ..backends.pairwise_hip import pairwise_hip
+from ..backends.pairwise_hip import pairwise_hip, pairwise_hip_route
 from .base import RoutedLinearBase
 from .surrogate import check_surrogate
 
@@ -35,7 +35,11 @@ class PairwiseLinear(RoutedLinearBase):
                         version changes; gradients still go to the f32 LUT.
     Attribute `cache_route_debug` (default True, as the reference's shell
     assumes) keeps `_last_indices` [B,S,T] int64 and `_last_margins`
-    [B,S,T,C] f32 of the last call; set it to False to skip writing them.
+    [B,S,T,C] f32 of the last call; False skips writing them; "lazy" writes
+    only uint8 codes (`_last_codes`, B*T bytes) and materialises the other
+    two on first access, the margins by a route-only launch that reads the
+    call's latent, anchors and thresholds (an error if any of them has been
+    modified in place since, e.g. by an optimizer step).
     """
 
     fuses_output_scale = True
@@ -146,5 +150,28 @@ class PairwiseLinear(RoutedLinearBase):
             output_scale=self.output_scale,
             lut_read=self._lut_for_reading(),
             ste=ste,
-            return_route=bool(getattr(self, "cache_route_debug", True)),
+            return_route=self._route_mode(),
         )
+
+    def _route_mode(self) -> bool | str:
+        mode = getattr(self, "cache_route_debug", True)
+        return "codes" if mode == "lazy" else bool(mode)
+
+    def _recompute_margins(self, latent: Tensor) -> Callable[[], Tensor]:
+        """Margins of the call on `latent`, computed when first asked for by
+        the route-only kernel from the same latent, anchors and thresholds;
+        their version counters (bumped by every in-place write) must not have
+        moved since the call."""
+        inputs = (latent.detach(), self.anchors, self.thresholds.detach())
+        versions = tuple(t._version for t in inputs)
+
+        def recompute() -> Tensor:
+            if tuple(t._version for t in inputs) != versions:
+                raise RuntimeError(
+                    "cache_route_debug='lazy': the latent, anchors or thresholds of the last call were modified in "
+                    "place since (e.g. by an optimizer step), so its margins can no longer be recomputed; read "
+                    "_last_margins before that, or set cache_route_debug=True"
+                )
+            return pairwise_hip_route(*inputs, codes=False, indices=False, margins=True)[2]
+
+        return recompute
