@@ -201,7 +201,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void 
     const int tid = threadIdx.x, nthr = blockDim.x;
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int b = blockIdx.x;
+    const int b = xcd_block_unit(blockIdx.x, gridDim.x);  // [T][B] records of adjacent items share lines
     const int C = a.comps, R = a.rows;
     const int t0 = wave * a.per_wave;
     const int nt = max(0, min(a.tables, t0 + a.per_wave) - t0);
@@ -309,7 +309,7 @@ __global__ __launch_bounds__(1024) void pairwise_bwd_full_kernel(ItemArgs a) {
     const int tid = threadIdx.x, nthr = blockDim.x;
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int b = blockIdx.x;
+    const int b = xcd_block_unit(blockIdx.x, gridDim.x);  // [T][B] records of adjacent items share lines
     const int C = a.comps, R = a.rows;
     const int t0 = wave * a.per_wave;
     const int nt = max(0, min(a.tables, t0 + a.per_wave) - t0);
@@ -1065,7 +1065,7 @@ __global__ __launch_bounds__(kScatterThreads) void pairwise_bwd_scatter_kernel(S
     const int C = a.comps;
     float *gud = reinterpret_cast<float *>(lds);                     // [T * C]
     int *idx_s = reinterpret_cast<int *>(gud + a.tables * C);         // [in_f + 1 + 2 T C]
-    const int b = blockIdx.x, tid = threadIdx.x;
+    const int b = xcd_block_unit(blockIdx.x, gridDim.x), tid = threadIdx.x;  // records of adjacent items share lines
     const int nidx = a.in_f + 1 + 2 * a.tables * C;
     for (int t0 = 0; t0 < a.tables; t0 += kScatterThreads) {
         const int tt = t0 + tid;

@@ -191,6 +191,17 @@ __device__ __forceinline__ void buffer_row(__amdgpu_buffer_rsrc_t rsrc, uint32_t
     }
 }
 
+// The dispatcher deals the workgroups of a grid to the 8 XCDs in turn
+// (workgroup i runs on XCD i % 8). This maps workgroup i of n to unit
+// x * (n / 8) + min(x, n % 8) + i / 8, x = i % 8: a bijection on [0, n) that
+// gives each XCD one contiguous block of units, so per-unit entries of a
+// [*, n] array that share a cache line go through one XCD's L2 (lines are
+// not split between XCDs).
+__device__ __forceinline__ int xcd_block_unit(int i, int n) {
+    const int x = i & 7, k = i >> 3, per = n >> 3, extra = n & 7;
+    return x * per + min(x, extra) + k;
+}
+
 // Clamp an anchor into [0, n) so a corrupt anchor can never address memory
 // outside the staged input row; the host validates anchors before launch.
 __device__ __forceinline__ int clamp_index(int64_t a, int n) {

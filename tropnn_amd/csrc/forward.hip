@@ -54,7 +54,11 @@ struct FwdArgs {
     int codes_off, red_off;
 };
 
-constexpr int kBallots = 4;             // ballots whose comparators a wave prefetches
+// Ballots whose comparators a wave prefetches: two cover 16 tables of up to
+// 8 comparisons, every wave of the configurations of interest; further
+// ballots load their comparators in turn. (Four prefetch slots made the c2
+// forward ~0.4 us slower for the registers and code they take.)
+constexpr int kBallots = 2;
 
 // One lane's comparator: anchors (clamped) and threshold of (table, comparison).
 // Padding lanes load table 0 / comparison 0 so that the loads are issued
@@ -137,7 +141,7 @@ __global__ __launch_bounds__(1024) void pairwise_forward_kernel(FwdArgs a) {
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nwaves = blockDim.x >> 6;
-    const int item = blockIdx.x;
+    const int item = xcd_block_unit(blockIdx.x, gridDim.x);  // route records of adjacent items share lines
     uint8_t *my_codes = lds + a.codes_off + wave * a.codes_pitch;
 
     const int tpb = kWave >> a.lpt_log2;
