@@ -21,6 +21,10 @@ Timed regions (both full fwd+bwd of the module API, no work skipped):
 cpu_baseline: the oracle's torch restatement of the reference torch path, same
 step on the host CPU for a bounded number of steps (rank 0, N=1 only).
 
+Other BASELINE.json configs, each its own JSON line (--workload): c3, the f16
+eval forward sweep at batch 1 / 64 / 8192; c4, the large f16-LUT layer fwd+bwd
+at batch 8192; c5, the EMNIST classifier training step.
+
 Prints ONE JSON line.
 """
 from __future__ import annotations
@@ -44,11 +48,12 @@ R = 1 << C
 E = 4  # f32 LUT element bytes
 
 
-def algorithmic_bytes(fused: bool) -> dict[str, int]:
+def algorithmic_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = T, c: int = C, e: int = E) -> dict[str, int]:
     """Per-launch algorithmic bytes (gather / embedding-bag convention: every
     (item, table) pair moves its LUT row(s) once, streamed tensors and params
-    once), split by the kernel that moves them. Sums to the FwdBwd figure of
-    the c2 plan: 148,548,672 B.
+    once), split by the kernel that moves them; e = LUT element bytes. Sums to
+    the FwdBwd figure of the plan: 148,548,672 B at c2 (the defaults),
+    174,323,843,072 B at c4.
       forward: x, anchors + thresholds, one row per (item, table), y, codes;
     fused backward (narrow rows, c2's path):
       backward_fused: G, codes, current + neighbour rows per (item, table),
@@ -60,10 +65,11 @@ def algorithmic_bytes(fused: bool) -> dict[str, int]:
         (item, table), grad_x, anchors + thresholds;
       backward_table: one f32 grad-row contribution per (item, table),
         grad_lut once, grad_thr."""
-    fwd = 4 * B * I + 20 * T * C + E * B * T * O + 4 * B * O + B * T
-    g_codes_rows = 4 * B * O + B * T + 2 * E * B * T * O
-    x_side = 4 * B * I + 4 * B * I + 20 * T * C
-    lut_side = 4 * B * T * O + 4 * T * R * O + 4 * T * C
+    r = 1 << c
+    fwd = 4 * b * i + 20 * t * c + e * b * t * o + 4 * b * o + b * t
+    g_codes_rows = 4 * b * o + b * t + 2 * e * b * t * o
+    x_side = 4 * b * i + 4 * b * i + 20 * t * c
+    lut_side = 4 * b * t * o + 4 * t * r * o + 4 * t * c
     if fused:
         return {"forward": fwd, "backward_fused": g_codes_rows + lut_side, "backward_scatter": x_side}
     return {"forward": fwd, "backward_item": g_codes_rows + x_side, "backward_table": lut_side}
@@ -107,12 +113,13 @@ def source_digest() -> str:
     return h.hexdigest()
 
 
-def measured_traffic(kernel: str) -> int | None:
+def measured_traffic(kernel: str, workload: str = "c2") -> int | None:
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
-    summary (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE scaled by a
-    calibration copy), used only while the kernel sources (comments aside)
-    still hash to the profiled ones; otherwise None."""
-    path = ROOT / "profiles" / "traffic.json"
+    summary of the workload (profiles/traffic.json for c2,
+    profiles/traffic_<workload>.json otherwise: FETCH_SIZE and WRITE_SIZE
+    scaled by a calibration copy), used only while the kernel sources
+    (comments aside) still hash to the profiled ones; otherwise None."""
+    path = ROOT / "profiles" / ("traffic.json" if workload == "c2" else f"traffic_{workload}.json")
     if not path.exists():
         return None
     rec = json.loads(path.read_text())
@@ -368,18 +375,184 @@ def bench_c5(args, dev) -> dict:
     return out
 
 
+C4 = {"b": 8192, "i": 1024, "o": 4096, "t": 512, "c": 8}
+C4_CPU_BATCH = 8
+
+
+def cpu_baseline_c4(budget_s: float) -> dict:
+    """The oracle's torch restatement of the reference torch path at c4's
+    layer (f32 LUT, as that path reads it) on the host cores, fwd + min-margin
+    STE bwd, at a reduced batch of 8 items: the full batch of 8192 would hold
+    ~64 GiB of saved STE rows (one [B, tables, 4096] f32 neighbour difference
+    per route chunk). Reported per sample."""
+    import torch
+
+    from oracle.pairwise_torch import OraclePairwiseLinear
+
+    threads = torch.get_num_threads()
+    layer = OraclePairwiseLinear(C4["i"], C4["o"], tables=C4["t"], comparisons=C4["c"], seed=0).train()
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(C4_CPU_BATCH, C4["i"], generator=gen).requires_grad_(True)
+    g = torch.randn(C4_CPU_BATCH, 1, C4["o"], generator=gen)
+
+    def step() -> None:
+        layer.zero_grad(set_to_none=True)
+        x.grad = None
+        layer(x).backward(g)
+
+    step()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": C4_CPU_BATCH / med,
+        "unit": "samples/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"c4 layer fwd+bwd at batch {C4_CPU_BATCH} (the full 8192 needs ~64 GiB of saved STE rows), "
+        f"f32 LUT, {len(times)} steps (median {med * 1e3:.0f} ms/step), oracle/pairwise_torch.py "
+        f"torch-CPU restatement, torch.set_num_threads={threads}",
+    }
+
+
+def bench_c4(args, dev) -> dict:
+    """c4: PairwiseLinear(1024 -> 4096, T = 512,
+    C = 8) reading an f16 LUT (the RNE copy of the f32 master; 1 GiB), batch
+    8192, one step = forward + min-margin STE backward with x, thresholds and
+    f32 LUT (2 GiB) gradients. A step takes tens of milliseconds, so plain
+    eager module steps are timed (K steps after the warmup); each kernel's
+    duration comes from events its own dispatch stamps, over the same steps.
+    The backward takes the general path (item kernel, then table kernel)."""
+    import torch
+
+    from tropnn_amd import PairwiseLinear
+    from tropnn_amd.backends.pairwise_hip import arm_kernel_events
+
+    b = C4["b"]
+    layer = PairwiseLinear(C4["i"], C4["o"], tables=C4["t"], comparisons=C4["c"], seed=0, device_lut_dtype="f16")
+    layer = layer.to(dev).train()
+    layer.cache_route_debug = False
+    nb = 2
+    gen = torch.Generator().manual_seed(0)
+    xs = [torch.randn(b, C4["i"], generator=gen).to(dev).requires_grad_(True) for _ in range(nb)]
+    gs = [torch.randn(b, 1, C4["o"], generator=gen).to(dev) for _ in range(nb)]
+
+    def step(k: int) -> None:
+        layer.zero_grad(set_to_none=True)
+        xs[k].grad = None
+        layer(xs[k]).backward(gs[k])
+
+    for w in range(args.warmup):
+        step(w % nb)
+    torch.cuda.synchronize()
+    algo = algorithmic_bytes(False, e=2, **C4)
+    names = tuple(algo)
+    stream = torch.cuda.current_stream(dev)
+    evs = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)] for n in names}
+    for n in names:
+        for e0, e1 in evs[n]:
+            e0.record(stream)
+            e1.record(stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        for n in names:
+            arm_kernel_events(n, *evs[n][k])
+        step(k % nb)
+    torch.cuda.synchronize()
+    step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    kern_us = {n: 1e3 * sum(e0.elapsed_time(e1) for e0, e1 in evs[n]) / args.steps for n in names}
+    log(f"c4 {step_ms:.2f} ms/step; kernels (ms): " + ", ".join(f"{n}={v * 1e-3:.3f}" for n, v in kern_us.items()))
+    dom = max(names, key=lambda n: kern_us[n])
+    achieved = algo[dom] / (kern_us[dom] * 1e-6) / 1e9
+    if args.calibrate_copy_bytes > 0:
+        calibration_copy(args.calibrate_copy_bytes, dev)
+    cpu = None
+    if args.cpu_budget > 0:
+        log("timing the CPU baseline")
+        cpu = cpu_baseline_c4(args.cpu_budget)
+        log(f"cpu baseline {cpu['value']:.1f} samples/s on {cpu['cores']} threads")
+    value = b / (step_ms * 1e-3)
+    total_algo = sum(algo.values())
+    out = {
+        "metric": "PairwiseLinear c4 samples/s fwd+bwd (1024->4096, T=512, C=8, f16 LUT, B=8192) + achieved HBM GB/s vs peak",
+        "value": round(value, 1),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: x, G ~ N(0,1), 2 resident batches alternating; seeded module init (seed 0)",
+        "config": {
+            "workload": "c4: PairwiseLinear(1024->4096, tables=512, comparisons=8), f16 LUT reads [512,256,4096] "
+            "(RNE copy of the f32 master), batch 8192, fwd + fast_sigmoid_odd min-margin STE bwd "
+            "(x, thresholds, f32 LUT grads)",
+            "batch": b,
+            "in_features": C4["i"],
+            "out_features": C4["o"],
+            "tables": C4["t"],
+            "comparisons": C4["c"],
+            "lut_dtype": "f16",
+            "mode": "eager module fwd+bwd",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom,
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(dom, "c4"),
+        },
+        "cpu_baseline": cpu,
+        "step_algorithmic_GBs": round(total_algo / (step_ms * 1e-3) / 1e9, 1),
+        "step_roofline_frac": round(total_algo / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "kernels": {
+            n: {"avg_us": round(kern_us[n], 1), "algorithmic_bytes": algo[n],
+                "achieved_GBs": round(algo[n] / (kern_us[n] * 1e-6) / 1e9, 1)}
+            for n in names
+        },
+    }
+    if cpu:
+        out["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+    return out
+
+
+def calibration_copy(nbytes: int, dev) -> None:
+    """One plain device copy of `nbytes`: the reference dispatch whose
+    rocprofv3 FETCH_SIZE / WRITE_SIZE readings scale the kernels' to bytes."""
+    import torch
+
+    n = nbytes // 4
+    src = torch.ones(n, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"calibration copy of {n * 4} bytes done")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument(
         "--workload",
-        choices=("c2", "c3", "c5"),
+        choices=("c2", "c3", "c4", "c5"),
         default="c2",
         help="c2: the BASELINE metric (default); c3: f16 eval forward at batch 1 / 64 / 8192; "
-        "c5: the EMNIST classifier training step",
+        "c4: the large f16-LUT layer fwd+bwd at batch 8192; c5: the EMNIST classifier training step",
     )
-    ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 500; 20 for c4)")
+    ap.add_argument("--warmup", type=int, default=None, help="warmup steps (default 50; 3 for c4)")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work (0 = skip)")
     ap.add_argument(
         "--calibrate-copy-bytes",
@@ -389,6 +562,10 @@ def main() -> int:
         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)",
     )
     args = ap.parse_args()
+    if args.steps is None:
+        args.steps = 20 if args.workload == "c4" else 500
+    if args.warmup is None:
+        args.warmup = 3 if args.workload == "c4" else 50
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
             "bench.py measures one GPU only: the PairwiseLinear path is built and measured on a single MI355X "
@@ -408,8 +585,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_name(dev)}, library {library_path()}")
-    if args.workload in ("c3", "c5"):
-        print(json.dumps(bench_c3(args, dev) if args.workload == "c3" else bench_c5(args, dev)))
+    if args.workload != "c2":
+        runner = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.workload]
+        print(json.dumps(runner(args, dev)))
         return 0
 
     layer = PairwiseLinear(I, O, tables=T, comparisons=C, seed=0).to(dev).train()
@@ -505,14 +683,7 @@ def main() -> int:
     }
 
     if args.calibrate_copy_bytes > 0:
-        n = args.calibrate_copy_bytes // 4
-        src = torch.ones(n, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"calibration copy of {n * 4} bytes done")
-        del src, dst
+        calibration_copy(args.calibrate_copy_bytes, dev)
 
     cpu = None
     if args.cpu_budget > 0:
