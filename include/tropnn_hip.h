@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TROPNN_HIP_ABI_VERSION 5
+#define TROPNN_HIP_ABI_VERSION 6
 
 /* status codes */
 #define TROPNN_OK 0
@@ -167,7 +167,7 @@ int tropnn_hip_build_anchor_index(int64_t in_features, int64_t tables, int64_t c
  * tropnn_hip_build_anchor_index), the others accept NULL index pointers.
  * workspace: device memory of at least
  * tropnn_hip_pairwise_backward_workspace_size() bytes (same ste_mode), 16-byte
- * aligned.
+ * aligned, whenever a gradient is asked for.
  */
 int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out_features, int64_t tables,
                                  int64_t comparisons, const float *grad_output, const void *lut, int lut_dtype,
@@ -182,13 +182,14 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
  * hipEvent_t handles to be recorded on the launch stream immediately before
  * and after the NEXT launch of one kernel:
  *   TROPNN_KERNEL_FORWARD           the fused route + gather + scale kernel
- *   TROPNN_KERNEL_BACKWARD_TABLE    the per-table LUT-gradient / threshold-gradient kernel
+ *   TROPNN_KERNEL_BACKWARD_TABLE    the per-(table, column chunk) LUT-gradient kernel
  *   TROPNN_KERNEL_BACKWARD_ITEM     the per-item STE-dot / input-gradient kernel
+ *   TROPNN_KERNEL_BACKWARD_SORT     the per-table code sort / threshold-gradient kernel between them
  *   TROPNN_KERNEL_BACKWARD_FUSED    the per-table LUT-gradient / STE-dot / threshold-gradient
  *                                   kernel of narrow rows (out_features a multiple of 4 up to 64
  *                                   or of 8 up to 256, one table's rows within 64 KB as f32)
  *   TROPNN_KERNEL_BACKWARD_SCATTER  the per-item input-gradient kernel that follows it
- * A backward launches either FUSED then SCATTER, or ITEM then TABLE.
+ * A backward launches either FUSED then SCATTER, or ITEM, SORT and TABLE.
  * One-shot and process-global (not for concurrent use from several threads).
  * Passing NULL events disarms. Lets a benchmark time one kernel per step with
  * events on the exact stream the kernel runs on.
@@ -198,6 +199,7 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
 #define TROPNN_KERNEL_BACKWARD_ITEM 2
 #define TROPNN_KERNEL_BACKWARD_FUSED 3
 #define TROPNN_KERNEL_BACKWARD_SCATTER 4
+#define TROPNN_KERNEL_BACKWARD_SORT 5
 int tropnn_hip_arm_kernel_events(int kernel, void *start_event, void *stop_event);
 
 #ifdef __cplusplus

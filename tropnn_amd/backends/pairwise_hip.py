@@ -26,7 +26,7 @@ from typing import Any
 import torch
 from torch import Tensor
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 LUT_F32, LUT_F16 = 0, 1
 SURROGATE_IDS = {"fast_sigmoid_odd": 0, "izhikevich": 1}
 STE_MIN_MARGIN, STE_FULL = 0, 1
@@ -56,7 +56,14 @@ EXPORTED_SYMBOLS = (
     "tropnn_hip_build_anchor_index",
     "tropnn_hip_arm_kernel_events",
 )
-KERNEL_IDS = {"forward": 0, "backward_table": 1, "backward_item": 2, "backward_fused": 3, "backward_scatter": 4}
+KERNEL_IDS = {
+    "forward": 0,
+    "backward_table": 1,
+    "backward_item": 2,
+    "backward_fused": 3,
+    "backward_scatter": 4,
+    "backward_sort": 5,
+}
 
 
 def library_path() -> Path:
@@ -146,7 +153,7 @@ def _check(rc: int, what: str) -> None:
 def arm_kernel_events(kernel: str, start: "torch.cuda.Event | None", stop: "torch.cuda.Event | None") -> None:
     """Record `start` / `stop` (torch.cuda.Event objects that have been
     recorded once, so their handles exist) around the next launch of `kernel`
-    ("forward", "backward_table", "backward_item"); None disarms."""
+    (a key of KERNEL_IDS); None disarms."""
     lib = load_library()
     h0 = None if start is None else start.cuda_event
     h1 = None if stop is None else stop.cuda_event
@@ -366,7 +373,7 @@ class _PairwiseHipFunction(torch.autograd.Function):
         ws_bytes = lib.tropnn_hip_pairwise_backward_workspace_size(
             items, in_features, out_features, tables, comps, lut_dtype, ctx.ste_mode
         )
-        workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8) if (want_x or want_thr) else None
+        workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
         offsets, entries = ctx.index if want_x else (None, None)
         rc = lib.tropnn_hip_pairwise_backward(
             items,

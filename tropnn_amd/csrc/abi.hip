@@ -82,7 +82,7 @@ int check_forward_ptrs(const tropnn::Dims &d, const tropnn::ForwardPlan &p, cons
 }
 
 std::mutex g_events_mu;
-tropnn::ArmedEvents g_armed[TROPNN_KERNEL_BACKWARD_SCATTER + 1];
+tropnn::ArmedEvents g_armed[TROPNN_KERNEL_BACKWARD_SORT + 1];
 
 }  // namespace
 
@@ -106,7 +106,7 @@ void arm_events(int kernel, hipEvent_t start, hipEvent_t stop) {
 extern "C" {
 
 int tropnn_hip_arm_kernel_events(int kernel, void *start_event, void *stop_event) {
-    if (kernel < TROPNN_KERNEL_FORWARD || kernel > TROPNN_KERNEL_BACKWARD_SCATTER)
+    if (kernel < TROPNN_KERNEL_FORWARD || kernel > TROPNN_KERNEL_BACKWARD_SORT)
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "unknown kernel id %d", kernel);
     if ((start_event == nullptr) != (stop_event == nullptr))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "arm both events or neither");
@@ -245,18 +245,18 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
     const size_t esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
     // fused path: LUT chunks of 4 elements, 16-byte grad rows and LUT-grad rows
     const size_t lut_align = p.fused ? 4 * esize : p.item_vec * esize;
-    const size_t gvec = p.fused ? 4 : static_cast<size_t>(p.vec > p.item_vec ? p.vec : p.item_vec);
-    const size_t lut_grad_vec = p.fused ? 4 : static_cast<size_t>(p.vec);
+    const size_t gvec = p.fused ? 4 : static_cast<size_t>(p.rows_vec > p.item_vec ? p.rows_vec : p.item_vec);
+    const size_t lut_grad_vec = p.fused ? 4 : static_cast<size_t>(p.rows_vec);
     if (misaligned(lut, lut_align) || misaligned(grad_output, gvec * 4) ||
         (grad_lut && misaligned(grad_lut, lut_grad_vec * 4)) || misaligned(route_record, 8))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "a device pointer is not aligned to its element/vector size");
-    if (grad_latent || grad_thresholds) {
+    if (grad_latent || grad_thresholds || grad_lut) {
         if (!workspace || workspace_bytes < p.workspace_bytes)
             return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace of %zu bytes required, got %zu", p.workspace_bytes,
                         workspace_bytes);
         if (misaligned(workspace, 16)) return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
     }
-    if ((!p.fused && p.lut_lds_bytes > 160 * 1024) || p.item_lds_bytes > 64 * 1024)
+    if (p.item_lds_bytes > 64 * 1024)
         return fail(TROPNN_ERR_UNSUPPORTED, "backward LDS plan exceeds the workgroup limit (in_features or tables too large)");
     // grad rows and the LUT are addressed through buffer resources with 32-bit offsets
     const int64_t lut_bytes = int64_t{d.tables} * d.rows * d.out_f * esize;

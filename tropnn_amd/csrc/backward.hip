@@ -29,7 +29,7 @@
 //      (table, comparison) slots and walks the inverse anchor index into
 //      grad_latent, as the item kernel's last phase does.
 //
-// Other shapes take the general path, two launches:
+// Other shapes take the general path, three launches:
 //  (1) item kernel, one workgroup per item, shaped like the forward: each wave
 //      takes up to 16 consecutive tables. A lane holds the record of table
 //      lane / 4; the wave moves each table's code and min-margin comparison to
@@ -44,20 +44,20 @@
 //      one thread per input feature sums the signed slots named by the
 //      feature's entries of the inverse anchor index, in entry order, and
 //      writes grad_latent.
-//  (2) table kernel, one workgroup per (table, output chunk of S * V columns).
-//      Items are taken in tiles of 1024; each tile is counting-sorted by LUT
-//      row code in LDS (C wave ballots give every item its rank among equal
-//      codes of its wave and every lane the population of one code, one DPP
-//      scan turns the per-wave counts into bucket offsets), which keeps item
-//      order inside a bucket. Row groups of S lanes (V columns each) then walk
-//      equal contiguous ranges of the sorted list, eight items per step: grad
-//      rows arrive through buffer loads (out-of-range offsets read zeros, so
-//      the walk carries no masks), are summed along runs of equal codes in
-//      registers, and each finished run goes to its LUT row (whole bucket in
-//      the range) or to one of the range's two split slots; a combine pass
-//      adds the split pieces in range order. Rows are scaled and written once.
-//      The workgroup of chunk 0 also reduces table t's threshold gradient
-//      from gu.
+//  (2) sort kernel, one workgroup per table: the stable counting sort of the
+//      table's items by LUT row code (C wave ballots per tile of 1024 items
+//      give each item its rank among equal codes of its wave; per-wave counts
+//      and a DPP scan give row starts), written once to the workspace as the
+//      items' grad-row offsets with every row padded to whole batches of 8
+//      slots, plus each batch's row; and the table's threshold gradient from
+//      gu.
+//  (3) row kernel, one workgroup per (table, 64-column chunk): row groups of
+//      S lanes (V columns each) walk balanced contiguous ranges of the sorted
+//      batches, eight grad-row loads in flight per batch (padding slots read
+//      out of range: zeros), summing each row in registers; a row inside one
+//      range is scaled and written there, a row crossing ranges is combined
+//      from the ranges' LDS slots in range order, and empty rows are written
+//      as zeros. The sort is done once per table instead of once per chunk.
 //  A third, tiny kernel builds the inverse anchor index; callers rebuild it
 //  only when the anchors change.
 #include "device.hpp"
@@ -66,7 +66,10 @@
 namespace tropnn {
 namespace {
 
-constexpr int kLutThreads = 1024;  // items per sort tile
+constexpr int kSortThreads = 1024;  // items per tile of the sort kernel
+constexpr int kRowsThreads = 1024;  // threads of a row-kernel workgroup
+constexpr int kRowsBatch = 8;       // sorted slots per row-kernel batch; rows are padded to whole batches
+constexpr uint32_t kSlotPad = 0x80000000u;  // grad-row offset of a padding slot: past any grad buffer (<= 2 GiB)
 constexpr int kItemTables = 16;    // tables per item-kernel wave (one reduce-scatter)
 constexpr int kEntries = 16;       // index entries a walker reads per batch
 constexpr int kIndexRegs = 4;      // index words per thread loaded with the first record
@@ -86,17 +89,28 @@ struct ItemArgs {
     int items, in_f, out_f, tables, comps, rows, row_bytes, table_bytes, per_wave, o_tiles;
 };
 
-struct LutArgs {
+// Sort kernel (general path), one workgroup per table.
+struct SortArgs {
+    const uint64_t *rec;  // [T][B] route records
+    const float *gu;      // [T][B] (min-margin) or [T][C][B] (full STE); null: no threshold gradient
+    uint32_t *slot_off;   // [T][slots] sorted grad-row byte offsets, kSlotPad in padding; null: no sort
+    int32_t *row_start;   // [T][R + 1] first slot of each LUT row; [R] = the padded length
+    int32_t *batch_row;   // [T][slots / kRowsBatch] the LUT row of each batch of slots
+    float *grad_thr;      // or null
+    int full;             // full STE: gu of every comparison
+    int items, out_f, comps, rows, slots;
+};
+
+// Row kernel (general path), one workgroup per (table, column chunk).
+struct RowsArgs {
     const float *grad_out;
-    const uint64_t *rec;
-    const float *gu;  // for the threshold gradient: [T][B] (min-margin) or [T][C][B] (full STE)
-    int full;         // full STE: every comparison carries its own gu
-    float scale;
+    const uint32_t *slot_off;
+    const int32_t *row_start;
+    const int32_t *batch_row;
     float *grad_lut;
-    float *grad_thr;
+    float scale;
     uint32_t g_bytes;
-    int items, out_f, tables, comps, rows, o_chunk;
-    int hist_off, start_off, sorted_off, rowbuf_off, part_off, thr_off, wtot_off;  // LDS byte offsets
+    int out_f, rows, slots, part_off;
 };
 
 __device__ __forceinline__ int rec_code(uint64_t r) { return static_cast<int>((r >> 32) & 0xffffu); }
@@ -372,7 +386,7 @@ __global__ __launch_bounds__(1024) void pairwise_bwd_full_kernel(ItemArgs a) {
     feature_walk(gud, idx_s, a.in_f, a.grad_x + static_cast<size_t>(b) * a.in_f, tid, nthr);
 }
 
-// ------------------------------------------------------------------ table kernel
+// ------------------------------------------------------------------ sort and row kernels (general path)
 
 // Inclusive prefix sum over the 64 lanes of a wave: DPP shifts inside rows of
 // 16, then the row broadcasts of lanes 15 and 31. All lanes must be active.
@@ -405,278 +419,254 @@ __device__ void wave_exclusive_scan(int *v, int n, int lane) {
     if (lane == 0) v[n] = carry;
 }
 
-// Sorted-list entry: item in the tile (10 bits), code (8), whether the item's
-// bucket lies inside the walk range of its position (1), and else which of
-// that range's two split slots its segment uses (1).
-__device__ __forceinline__ uint32_t pack_entry(int item, int code, bool inside, int slot) {
-    return static_cast<uint32_t>(item) | (static_cast<uint32_t>(code) << 10) | (static_cast<uint32_t>(inside) << 18) |
-           (static_cast<uint32_t>(slot) << 19);
-}
-__device__ __forceinline__ int entry_item(uint32_t e) { return static_cast<int>(e & 0x3ffu); }
-__device__ __forceinline__ int entry_code(uint32_t e) { return static_cast<int>((e >> 10) & 0xffu); }
-__device__ __forceinline__ bool entry_inside(uint32_t e) { return ((e >> 18) & 1u) != 0; }
-__device__ __forceinline__ int entry_slot(uint32_t e) { return static_cast<int>((e >> 19) & 1u); }
-
-template <int V, int S>
-__global__ __launch_bounds__(kLutThreads) void pairwise_bwd_table_kernel(LutArgs a) {
-    constexpr int kK = 8;  // sorted positions per walk step
-    constexpr int kWaves = kLutThreads / kWave;
-    constexpr int nthr = kLutThreads;
-    constexpr int NG = nthr / S;  // row groups
-    extern __shared__ __align__(16) unsigned char lds[];
-    int *hist = reinterpret_cast<int *>(lds + a.hist_off);                   // [R][waves] counts -> offsets
-    int *start = reinterpret_cast<int *>(lds + a.start_off);                 // [R + 1] bucket starts
-    uint32_t *sorted = reinterpret_cast<uint32_t *>(lds + a.sorted_off);    // [tile] packed entries
-    float *rowbuf = reinterpret_cast<float *>(lds + a.rowbuf_off);           // [R][o_chunk] gradient rows
-    float *part = reinterpret_cast<float *>(lds + a.part_off);               // [groups][2][o_chunk] split segments
-    float *tp = reinterpret_cast<float *>(lds + a.thr_off);                  // [waves][MAX_COMPARISONS]
-    int *wtot = reinterpret_cast<int *>(lds + a.wtot_off);                   // [waves] scan carries
-    uint32_t *sink = reinterpret_cast<uint32_t *>(wtot + kWaves);            // [64] prefetch sink
-
-    const int t = blockIdx.x, chunk = blockIdx.y;
-    const int oc = a.o_chunk, o0 = chunk * oc;
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int R = a.rows, C = a.comps;
-    const bool thr = a.grad_thr != nullptr && chunk == 0;
-    const uint64_t *rec_t = a.rec + static_cast<size_t>(t) * a.items;
-    const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.grad_out, a.g_bytes);
-
-    // first tile's record (the sort waits for it), then a slice of
-    // grad_output: the workgroups that share an XCD (the dispatcher deals
-    // workgroups to the 8 XCDs in turn) each touch one slice, one dword per
-    // 128-byte line, so the grad rows the walk gathers are L2 hits by then
-    uint64_t r_next = tid < a.items ? rec_t[tid] : 0ull;
-    const float *gu_t = a.gu + static_cast<size_t>(t) * (a.full ? C : 1) * a.items;
-    float gu_next = thr && !a.full && tid < a.items ? gu_t[tid] : 0.f;
-    uint32_t pf = 0u;
-    {
-        const int nwg = gridDim.x * gridDim.y;
-        const int lin = blockIdx.y * gridDim.x + blockIdx.x;
-        const int share = (nwg - (lin & 7) + 7) >> 3;
-        const uint32_t slice = ((a.g_bytes + share - 1) / share + 127u) & ~127u;
-        const uint32_t off = tid * 128u;
-        if (off < slice) pf = __builtin_amdgcn_raw_buffer_load_b32(g_rsrc, (lin >> 3) * slice + off, 0, 0);
+// Counting-sort step of one wave over its 64 items: zeroes the wave's code
+// counts, gives each valid item its rank among the equal codes of the wave
+// (one ballot per code bit) and has each code's first item write the code's
+// count. One wave's LDS operations complete in order, so the zeroing lands
+// before the counts.
+__device__ __forceinline__ int wave_code_rank(int code, bool valid, int R, int C, int *cnt_w, int lane) {
+    for (int k = lane; k < R; k += kWave) cnt_w[k] = 0;
+    uint64_t same = __ballot(valid);
+    for (int c = 0; c < C; ++c) {
+        const uint64_t bc = __ballot(valid && ((code >> c) & 1));
+        same &= ((code >> c) & 1) ? bc : ~bc;
     }
-    for (int k = tid * 4; k < R * oc; k += nthr * 4) *reinterpret_cast<vec_t<float, 4> *>(rowbuf + k) = 0.f;
-    if (tid < kWaves * TROPNN_MAX_COMPARISONS) tp[tid] = 0.f;
+    const int rank = __popcll(same & ((1ull << lane) - 1ull));
+    if (valid && rank == 0) cnt_w[code] = __popcll(same);
+    return rank;
+}
 
-    for (int tile0 = 0; tile0 < a.items; tile0 += nthr) {
-        const int n_tile = min(nthr, a.items - tile0);
-        // per-lane values are recomputed per tile from an opaque copy of the
-        // thread id: hoisted out of the loop they would stay live across it
-        int tidl = tid;
-        __asm__ volatile("" : "+v"(tidl));
-        const int g = tidl / S, j = tidl % S;  // walker row group and its lane
-        const int col = j * V;
-        const bool col_ok = o0 + col < a.out_f;
-        const uint32_t gcol = static_cast<uint32_t>(o0 + col) * 4u;
+// Sort kernel: the stable counting sort of table t's items by LUT row code,
+// written once for every column chunk of the row kernel. Pass 1 counts each
+// code over tiles of 1024 items (and sums the threshold gradient's partials:
+// -gu at each item's min-margin comparison, or at every comparison with the
+// full STE, a fixed tree per wave, waves in order, tiles in order); the row
+// starts are the counts rounded up to whole batches of kRowsBatch slots,
+// exclusively scanned. Pass 2 places every item at its row's next free slot
+// (tiles, waves and lanes in order, so item order is kept inside a row) as
+// its grad-row byte offset; padding slots get kSlotPad.
+__global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArgs a) {
+    constexpr int kWaves = kSortThreads / kWave;
+    constexpr int K = kRowsBatch;
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int R = a.rows, C = a.comps;
+    int *cnt = reinterpret_cast<int *>(lds);                 // [waves][R] counts -> slots
+    int *base = cnt + kWaves * R;                            // [R] next free slot of each row
+    int *wtot = base + R;                                    // [waves] scan carries
+    float *tp = reinterpret_cast<float *>(wtot + kWaves);    // [waves][8] threshold partials
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint64_t *rec_t = a.rec + static_cast<size_t>(t) * a.items;
+    const bool thr = a.grad_thr != nullptr;
+    const float *gu_t = thr ? a.gu + static_cast<size_t>(t) * (a.full ? C : 1) * a.items : nullptr;
+    if (lane < 8) tp[wave * 8 + lane] = 0.f;  // each wave its own slots
 
-        // 1. this thread's item and code
-        const int b = tile0 + tidl;
+    // 1. per-code totals, threshold partials
+    int tot = 0;  // thread k < R: items of code k
+    for (int tile0 = 0; tile0 < a.items; tile0 += kSortThreads) {
+        const int b = tile0 + tid;
         const bool valid = b < a.items;
-        const uint64_t r0 = r_next;
-        const float gu0 = gu_next;
-        const int code = rec_code(r0) & (R - 1);  // masks keep a corrupt record in range
-
-        // 2. one ballot per code bit: each item's rank among equal codes of
-        //    its wave, and lane l's count of codes l, l + 64, ... in the wave
-        const uint64_t vmask = __ballot(valid);
-        constexpr int kCodesPerLane = (1 << TROPNN_MAX_COMPARISONS) / kWave;
-        uint64_t same = vmask;
-        uint64_t cnt[kCodesPerLane];
-#pragma unroll
-        for (int i = 0; i < kCodesPerLane; ++i) cnt[i] = vmask;
-        for (int c = 0; c < C; ++c) {
-            const uint64_t bc = __ballot(valid && ((code >> c) & 1));
-            same &= ((code >> c) & 1) ? bc : ~bc;
-#pragma unroll
-            for (int i = 0; i < kCodesPerLane; ++i) cnt[i] &= (((lane + i * kWave) >> c) & 1) ? bc : ~bc;
-        }
-        const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-        const int rank = __popcll(same & below);
-#pragma unroll
-        for (int i = 0; i < kCodesPerLane; ++i)
-            if (lane + i * kWave < R) hist[(lane + i * kWave) * kWaves + wave] = __popcll(cnt[i]);
-        __syncthreads();
-
-        // 3. bucket offsets: code k's count per wave -> per-wave offsets
-        //    inside the bucket, bucket totals -> exclusive scan over codes
-        int hw[kWaves];
-        int total = 0;
-        const bool scanner = tidl < ((R + kWave - 1) / kWave) * kWave;  // whole waves
-        if (scanner) {
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) hw[w] = tidl < R ? hist[tidl * kWaves + w] : 0;
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
-                const int h = hw[w];
-                hw[w] = total;
-                total += h;
-            }
-        }
-        int incl = scanner ? wave_inclusive_scan(total) : 0;
-        if (R > kWave) {  // carry across the scanning waves
-            if (scanner && lane == kWave - 1) wtot[wave] = incl;
-            __syncthreads();
-            if (scanner)
-                for (int w = 0; w < wave; ++w) incl += wtot[w];
-        }
-        if (tidl < R) {
-            const int excl = incl - total;
-            start[tidl] = excl;
-            if (tidl == R - 1) start[R] = incl;
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) hist[tidl * kWaves + w] = excl + hw[w];
-        }
-        __syncthreads();
-
-        // 4. stable placement. Row group g walks sorted positions
-        //    [g Lr, g Lr + Lr); a bucket's segment in a range is either the
-        //    whole bucket (summed into its row) or a piece of a bucket split
-        //    across ranges (written to the range's slot 0 if the segment holds
-        //    the range's first position, else slot 1)
-        const int Lr = kK * ((n_tile + NG * kK - 1) / (NG * kK));
-        if (valid) {
-            const int pos = hist[code * kWaves + wave] + rank;
-            const int q0 = (pos / Lr) * Lr, q1 = min(q0 + Lr, n_tile);
-            const int kb = start[code], ke = start[code + 1];
-            sorted[pos] = pack_entry(tidl, code, kb >= q0 && ke <= q1, kb <= q0 ? 0 : 1);
-        }
-        __syncthreads();
-        if (tile0 == 0) sink[lane] = pf;  // the prefetch's only use
-
-        // 5. walk: row group g takes sorted positions [p0, p1), kK per step.
-        //    Within a step the grad rows are summed along runs of equal codes
-        //    in registers; a run is written out when the next code differs,
-        //    and the run open at the end of a step carries into the next.
-        const int p0 = g * Lr, p1 = min(p0 + Lr, n_tile);
-        float acc[V];  // open run
-#pragma unroll
-        for (int e = 0; e < V; ++e) acc[e] = 0.f;
-        uint32_t cur = 0;   // entry of the open run's last item
-        bool open = false;  // uniform in the row group
-        auto dest = [&](uint32_t e) -> float * {
-            return entry_inside(e) ? rowbuf + entry_code(e) * oc + col : part + (g * 2 + entry_slot(e)) * oc + col;
-        };
-        for (int k0 = p0; __ballot(k0 < p1) != 0; k0 += kK) {  // wave-uniform trip count
-            uint32_t ent[kK];
-            float gv[kK][V];
-#pragma unroll
-            for (int u = 0; u < kK; ++u) {
-                const bool live = k0 + u < p1;
-                ent[u] = live ? sorted[k0 + u] : 0u;
-                const uint32_t item = tile0 + entry_item(ent[u]);
-                buffer_row<float, V>(g_rsrc, live && col_ok ? item * static_cast<uint32_t>(a.out_f) * 4u + gcol
-                                                            : kOutOfRange, 0, gv[u]);
-            }
-            // run sums in place: gv[u] += (previous item continues the run) ? gv[u-1] : 0
-#pragma unroll
-            for (int u = 0; u < kK; ++u) {
-                const bool live = k0 + u < p1;
-                const bool cont = live && (u == 0 ? open && entry_code(cur) == entry_code(ent[u])
-                                                  : entry_code(ent[u - 1]) == entry_code(ent[u]));
-#pragma unroll
-                for (int e = 0; e < V; ++e) gv[u][e] = cont ? (u == 0 ? acc[e] : gv[u - 1][e]) + gv[u][e] : gv[u][e];
-            }
-            // the open run ends before item 0 if item 0 starts a new run
-            if (open && k0 < p1 && entry_code(cur) != entry_code(ent[0])) {
-                float *dst = dest(cur);
-#pragma unroll
-                for (int e = 0; e < V; ++e) dst[e] = entry_inside(cur) ? dst[e] + acc[e] : acc[e];
-            }
-            // runs that end inside the step
-#pragma unroll
-            for (int u = 0; u + 1 < kK; ++u) {
-                if (k0 + u + 1 < p1 && entry_code(ent[u]) != entry_code(ent[u + 1])) {
-                    float *dst = dest(ent[u]);
-#pragma unroll
-                    for (int e = 0; e < V; ++e) dst[e] = entry_inside(ent[u]) ? dst[e] + gv[u][e] : gv[u][e];
-                }
-            }
-            // the last live item's run stays open
-#pragma unroll
-            for (int u = 0; u < kK; ++u) {
-                if (k0 + u < p1 && (u + 1 == kK || k0 + u + 1 >= p1)) {
-#pragma unroll
-                    for (int e = 0; e < V; ++e) acc[e] = gv[u][e];
-                    cur = ent[u];
-                    open = true;
-                }
-            }
-        }
-        if (open) {
-            float *dst = dest(cur);
-#pragma unroll
-            for (int e = 0; e < V; ++e) dst[e] = entry_inside(cur) ? dst[e] + acc[e] : acc[e];
-        }
-        // threshold gradient: -gu at the item's min-margin comparison (full
-        // STE: at every comparison), summed per wave (fixed tree) into the
-        // wave's slots; lane 8c ends with the wave's sum for comparison c
+        const uint64_t r = valid ? rec_t[b] : 0ull;
+        wave_code_rank(rec_code(r) & (R - 1), valid, R, C, cnt + wave * R, lane);
         if (thr) {
-            float tv[TROPNN_MAX_COMPARISONS];
+            float tv[8];
             if (a.full) {
 #pragma unroll
-                for (int c = 0; c < TROPNN_MAX_COMPARISONS; ++c)
-                    tv[c] = valid && c < C ? -gu_t[static_cast<size_t>(c) * a.items + tile0 + tidl] : 0.f;
+                for (int c = 0; c < 8; ++c) tv[c] = valid && c < C ? -gu_t[static_cast<size_t>(c) * a.items + b] : 0.f;
             } else {
-                const float gu = valid ? gu0 : 0.f;
-                const int rr = rec_r(r0) & 7;
+                const float gu = valid ? gu_t[b] : 0.f;
+                const int rr = rec_r(r) & 7;
 #pragma unroll
-                for (int c = 0; c < TROPNN_MAX_COMPARISONS; ++c) tv[c] = rr == c ? -gu : 0.f;
+                for (int c = 0; c < 8; ++c) tv[c] = rr == c ? -gu : 0.f;
             }
-            const float tot = reduce_scatter<kWave, TROPNN_MAX_COMPARISONS>(tv, lane);
-            const int c = lane >> 3;
-            if ((lane & 7) == 0 && c < C) tp[wave * TROPNN_MAX_COMPARISONS + c] += tot;
+            const float s = reduce_scatter<kWave, 8>(tv, lane);  // lane 8c: the wave's sum for comparison c
+            if ((lane & 7) == 0) tp[wave * 8 + (lane >> 3)] += s;
+        }
+        __syncthreads();
+        if (tid < R)
+            for (int w = 0; w < kWaves; ++w) tot += cnt[w * R + tid];
+        __syncthreads();
+    }
+
+    if (a.slot_off != nullptr) {
+        // 2. row starts: totals rounded up to whole batches, exclusive scan;
+        //    padding slots and the row of every batch
+        const int nscan = ((R + kWave - 1) / kWave) * kWave;  // whole waves
+        int padded = 0, incl = 0;
+        if (tid < nscan) {
+            padded = tid < R ? (tot + K - 1) / K * K : 0;
+            incl = wave_inclusive_scan(padded);
+        }
+        if (R > kWave) {
+            if (tid < nscan && lane == kWave - 1) wtot[wave] = incl;
+            __syncthreads();
+            if (tid < nscan)
+                for (int w = 0; w < wave; ++w) incl += wtot[w];
+        }
+        uint32_t *so = a.slot_off + static_cast<size_t>(t) * a.slots;
+        if (tid < R) {
+            const int excl = incl - padded;
+            a.row_start[static_cast<size_t>(t) * (R + 1) + tid] = excl;
+            if (tid == R - 1) a.row_start[static_cast<size_t>(t) * (R + 1) + R] = incl;
+            base[tid] = excl;
+            for (int q = excl + tot; q < excl + padded; ++q) so[q] = kSlotPad;
+            int32_t *br = a.batch_row + static_cast<size_t>(t) * (a.slots / K);
+            for (int bb = excl / K; bb < incl / K; ++bb) br[bb] = tid;
         }
         __syncthreads();
 
-        // 6. buckets split across ranges: their segments, in range order
-        for (int unit = tidl; unit < R * S; unit += nthr) {
-            const int k = unit / S, c0 = (unit % S) * V;
-            const int kb = start[k], ke = start[k + 1];
-            if (ke > kb && kb / Lr != (ke - 1) / Lr) {
-                const int glo = kb / Lr, ghi = (ke - 1) / Lr;
-                float sum[V];
-#pragma unroll
-                for (int e = 0; e < V; ++e) sum[e] = 0.f;
-                for (int gg = glo; gg <= ghi; ++gg) {
-                    const float *src = part + (gg * 2 + (gg == glo && kb != glo * Lr ? 1 : 0)) * oc + c0;
-#pragma unroll
-                    for (int e = 0; e < V; ++e) sum[e] += src[e];
+        // 3. stable placement
+        for (int tile0 = 0; tile0 < a.items; tile0 += kSortThreads) {
+            const int b = tile0 + tid;
+            const bool valid = b < a.items;
+            const int code = rec_code(valid ? rec_t[b] : 0ull) & (R - 1);
+            const int rank = wave_code_rank(code, valid, R, C, cnt + wave * R, lane);
+            __syncthreads();
+            if (tid < R) {
+                int run = base[tid];
+                for (int w = 0; w < kWaves; ++w) {
+                    const int x = cnt[w * R + tid];
+                    cnt[w * R + tid] = run;
+                    run += x;
                 }
-                float *dst = rowbuf + k * oc + c0;
-#pragma unroll
-                for (int e = 0; e < V; ++e) dst[e] += sum[e];
+                base[tid] = run;
             }
+            __syncthreads();
+            if (valid) so[cnt[wave * R + code] + rank] = static_cast<uint32_t>(b) * static_cast<uint32_t>(a.out_f) * 4u;
+            __syncthreads();  // the next tile rewrites the counts
         }
-        if (tile0 + nthr < a.items) {
-            const bool nv = tile0 + nthr + tidl < a.items;
-            r_next = nv ? rec_t[tile0 + nthr + tidl] : 0ull;
-            gu_next = thr && !a.full && nv ? gu_t[tile0 + nthr + tidl] : 0.f;
-        }
-        __syncthreads();  // LDS is reused by the next tile
     }
 
-    // 7. gradient rows, scaled, written once
-    if (a.grad_lut != nullptr) {
-        float *dst = a.grad_lut + static_cast<size_t>(t) * R * a.out_f + o0;
-        for (int unit = tid; unit < R * S; unit += nthr) {
-            const int k = unit / S, c0 = (unit % S) * V;
-            if (o0 + c0 < a.out_f) {
-                float y[V];
-#pragma unroll
-                for (int e = 0; e < V; ++e) y[e] = rowbuf[k * oc + c0 + e] * a.scale;
-                store_f32<V>(dst + static_cast<size_t>(k) * a.out_f + c0, y);
-            }
+    // 4. threshold gradient: the waves' sums in wave order
+    if (thr) {
+        __syncthreads();
+        if (tid < C) {
+            float sum = tp[tid];
+            for (int w = 1; w < kWaves; ++w) sum += tp[w * 8 + tid];
+            a.grad_thr[t * C + tid] = sum;
         }
     }
-    // 8. threshold gradient of this table: the waves' sums in wave order
-    if (thr && tid < C) {
-        float sum = tp[tid];
-        for (int w = 1; w < kWaves; ++w) sum += tp[w * TROPNN_MAX_COMPARISONS + tid];
-        a.grad_thr[t * C + tid] = sum;
+}
+
+// Row kernel: LUT gradient of table t over columns [chunk * S * V, + S * V).
+// The sorted slots form batches of kRowsBatch, each inside one row; the
+// batches are dealt to row groups (S lanes x V columns) as contiguous ranges
+// of lo or lo + 1 batches, the longer ones first. Per batch a group loads its
+// slots' grad-row offsets (one broadcast vector load, prefetched a batch
+// ahead with the batch's row), issues the kRowsBatch grad-row loads (padding
+// slots read out of range, zeros) and adds them to the open row's sum in
+// slot order. A row lying wholly in the range is scaled and written there; a
+// row crossing the range's start (end) leaves its sum in the group's slot 0
+// (1), and a combine step adds the pieces in range order and writes the
+// row. Empty rows are written as zeros, so grad_lut is fully overwritten.
+template <int V, int S>
+__global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArgs a) {
+    constexpr int NG = kRowsThreads / S;  // row groups
+    constexpr int K = kRowsBatch;
+    constexpr int P = S * V;  // columns of the chunk
+    extern __shared__ __align__(16) unsigned char lds[];
+    int *rs = reinterpret_cast<int *>(lds);                       // [R + 1] row starts (slots)
+    float *part = reinterpret_cast<float *>(lds + a.part_off);    // [groups][2][P] split rows
+    const int t = blockIdx.x, R = a.rows, O = a.out_f;
+    const int tid = threadIdx.x, g = tid / S, j = tid % S;
+    const int col = blockIdx.y * P + j * V;
+    const bool col_ok = col < O;  // V divides O: a lane's columns are all in or all out
+    const uint32_t gcol = static_cast<uint32_t>(col) * 4u;
+    const uint32_t coldead = col_ok ? 0u : kOutOfRange;
+    const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.grad_out, a.g_bytes);
+    const uint32_t *so = a.slot_off + static_cast<size_t>(t) * a.slots;
+    const int32_t *br = a.batch_row + static_cast<size_t>(t) * (a.slots / K);
+    float *gl = a.grad_lut + static_cast<size_t>(t) * R * O;
+    for (int k = tid; k <= R; k += kRowsThreads) rs[k] = a.row_start[static_cast<size_t>(t) * (R + 1) + k];
+    __syncthreads();
+
+    const int nb_all = rs[R] / K;
+    const int lo = nb_all / NG, extra = nb_all - lo * NG;
+    const int b_begin = g * lo + min(g, extra), b_end = b_begin + lo + (g < extra ? 1 : 0);
+    int cur = -1;  // row being summed
+    float acc[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[e] = 0.f;
+    auto finish = [&](int k) {  // row k's sum over this range
+        const int fb = rs[k] / K, lb = rs[k + 1] / K - 1;
+        if (fb >= b_begin && lb < b_end) {
+            if (col_ok) {
+                float y[V];
+#pragma unroll
+                for (int e = 0; e < V; ++e) y[e] = acc[e] * a.scale;
+                store_f32_nt<V>(gl + static_cast<size_t>(k) * O + col, y);
+            }
+        } else {
+            vec_t<float, V> w;
+#pragma unroll
+            for (int e = 0; e < V; ++e) w[e] = acc[e];
+            *reinterpret_cast<vec_t<float, V> *>(part + (g * 2 + (fb < b_begin ? 0 : 1)) * P + j * V) = w;
+        }
+    };
+    // a batch's slot offsets and row (past the range: out-of-range slots)
+    auto meta = [&](int bt, uint32_t(&off)[K], int &row) {
+        if (bt < b_end) {
+            const vec_t<uint32_t, 4> *src = reinterpret_cast<const vec_t<uint32_t, 4> *>(so + static_cast<size_t>(bt) * K);
+#pragma unroll
+            for (int q = 0; q < K / 4; ++q) {
+                const vec_t<uint32_t, 4> w = src[q];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) off[4 * q + e] = w[e];
+            }
+            row = br[bt];
+        } else {
+#pragma unroll
+            for (int u = 0; u < K; ++u) off[u] = kSlotPad;
+            row = -1;
+        }
+    };
+    uint32_t offn[K];
+    int rown;
+    meta(b_begin, offn, rown);
+    for (int i = 0; __ballot(b_begin + i < b_end) != 0; ++i) {  // wave-uniform trip count
+        const int bt = b_begin + i;
+        uint32_t off[K];
+#pragma unroll
+        for (int u = 0; u < K; ++u) off[u] = offn[u];
+        const int k = rown;
+        meta(bt + 1, offn, rown);
+        float gv[K][V];
+#pragma unroll
+        for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, (off[u] + gcol) | coldead, 0, gv[u]);
+        if (bt < b_end && k != cur) {
+            if (cur >= 0) finish(cur);
+            cur = k;
+#pragma unroll
+            for (int e = 0; e < V; ++e) acc[e] = 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < K; ++u)
+#pragma unroll
+            for (int e = 0; e < V; ++e) acc[e] += gv[u][e];
+    }
+    if (cur >= 0) finish(cur);
+    __syncthreads();
+
+    // combine: group g writes rows g, g + groups, ...: an empty row as zeros,
+    // a row split over ranges as its pieces in range order (slot 1 of its
+    // first range, slot 0 of the others); rows inside one range are written
+    const int bl = lo + 1;
+    auto range_of = [&](int bt) { return bt < extra * bl ? bt / bl : extra + (bt - extra * bl) / max(lo, 1); };
+    for (int k = g; k < R; k += NG) {
+        const int fb = rs[k] / K, nbk = rs[k + 1] / K - fb;
+        vec_t<float, V> w = 0.f;
+        if (nbk > 0) {
+            const int gf = range_of(fb), gla = range_of(fb + nbk - 1);
+            if (gf == gla) continue;
+            w = *reinterpret_cast<const vec_t<float, V> *>(part + (gf * 2 + 1) * P + j * V);
+            for (int gg = gf + 1; gg <= gla; ++gg) w += *reinterpret_cast<const vec_t<float, V> *>(part + gg * 2 * P + j * V);
+        }
+        if (col_ok) {
+            float y[V];
+#pragma unroll
+            for (int e = 0; e < V; ++e) y[e] = w[e] * a.scale;
+            store_f32_nt<V>(gl + static_cast<size_t>(k) * O + col, y);
+        }
     }
 }
 
@@ -705,7 +695,7 @@ struct FusedArgs {
 
 // One workgroup per table; the row group of S lanes x V columns spans the
 // whole output row (S * V >= O). The table's LUT rows sit in LDS as f32.
-// Per tile of 1024 items: counting sort by code (as in the table kernel),
+// Per tile of 1024 items: counting sort by code (as in the sort kernel),
 // then row group g owns rows g, g + groups, ... and walks each row's items
 // in item order, 32 / V at a time: one grad row load per item serves both the
 // LUT-gradient sum and the item's STE dot against L[nb] - L[code] (L[code]
@@ -1130,28 +1120,27 @@ hipError_t allow_lds(K kernel, int bytes) {
 }
 
 template <int V, int S>
-hipError_t launch_table_vs(const LutArgs &args, const BackwardPlan &p, hipStream_t stream) {
-    auto kernel = pairwise_bwd_table_kernel<V, S>;
-    if (hipError_t e = allow_lds(kernel, p.lut_lds_bytes); e != hipSuccess) return e;
-    return launch_kernel(TROPNN_KERNEL_BACKWARD_TABLE, kernel, dim3(args.tables, p.o_chunks), dim3(p.lut_threads),
-                         p.lut_lds_bytes, stream, args);
+hipError_t launch_rows_vs(const RowsArgs &args, const BackwardPlan &p, int tables, hipStream_t stream) {
+    return launch_kernel(TROPNN_KERNEL_BACKWARD_TABLE, pairwise_bwd_rows_kernel<V, S>, dim3(tables, p.rows_chunks),
+                         dim3(kRowsThreads), p.rows_lds_bytes, stream, args);
 }
 
 template <int V>
-hipError_t launch_table_v(const LutArgs &args, const BackwardPlan &p, hipStream_t stream) {
-    switch (p.slices) {
-        case 32: return launch_table_vs<V, 32>(args, p, stream);
-        case 16: return launch_table_vs<V, 16>(args, p, stream);
-        case 8: return launch_table_vs<V, 8>(args, p, stream);
-        default: return launch_table_vs<V, 4>(args, p, stream);
+hipError_t launch_rows_v(const RowsArgs &args, const BackwardPlan &p, int tables, hipStream_t stream) {
+    switch (p.rows_slices) {
+        case 64: return launch_rows_vs<V, 64>(args, p, tables, stream);
+        case 32: return launch_rows_vs<V, 32>(args, p, tables, stream);
+        case 16: return launch_rows_vs<V, 16>(args, p, tables, stream);
+        case 8: return launch_rows_vs<V, 8>(args, p, tables, stream);
+        default: return launch_rows_vs<V, 4>(args, p, tables, stream);
     }
 }
 
-hipError_t launch_table(const LutArgs &args, const BackwardPlan &p, hipStream_t stream) {
-    switch (p.vec) {
-        case 4: return launch_table_v<4>(args, p, stream);
-        case 2: return launch_table_v<2>(args, p, stream);
-        default: return launch_table_v<1>(args, p, stream);
+hipError_t launch_rows(const RowsArgs &args, const BackwardPlan &p, int tables, hipStream_t stream) {
+    switch (p.rows_vec) {
+        case 4: return launch_rows_v<4>(args, p, tables, stream);
+        case 2: return launch_rows_v<2>(args, p, tables, stream);
+        default: return launch_rows_v<1>(args, p, tables, stream);
     }
 }
 
@@ -1185,39 +1174,6 @@ __global__ void fill_zero_kernel(float *p, size_t n) {
         p[k] = 0.f;
 }
 
-// LDS bytes of a table workgroup for a given split (see the kernel's layout)
-int table_lds(const Dims &d, int slices, int vec, BackwardPlan *p) {
-    const int waves = kLutThreads / kWave;
-    const int oc = slices * vec;
-    int off = 0;
-    const int hist_off = off;
-    off += waves * d.rows * 4;
-    const int start_off = off;
-    off += (d.rows + 1) * 4;
-    off = (off + 15) & ~15;
-    const int sorted_off = off;
-    off += kLutThreads * 4;
-    const int rowbuf_off = off;
-    off += d.rows * oc * 4;
-    const int part_off = off;
-    off += (kLutThreads / slices) * 2 * oc * 4;
-    const int thr_off = off;
-    off += waves * TROPNN_MAX_COMPARISONS * 4;
-    const int wtot_off = off;
-    off += waves * 4 + kWave * 4;  // scan carries, prefetch sink
-    if (p != nullptr) {
-        p->hist_off = hist_off;
-        p->start_off = start_off;
-        p->sorted_off = sorted_off;
-        p->rowbuf_off = rowbuf_off;
-        p->part_off = part_off;
-        p->thr_off = thr_off;
-        p->wtot_off = wtot_off;
-        p->lut_lds_bytes = off;
-    }
-    return off;
-}
-
 }  // namespace
 
 hipError_t launch_fill_zero(float *p, size_t n, hipStream_t stream) {
@@ -1239,23 +1195,22 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     BackwardPlan p{};
     p.full = ste_mode == TROPNN_STE_FULL;
     const int esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
-    // table kernel: V columns per lane (a divisor of the row, at most 4), S
-    // lanes per row group: the smallest of 4, 8, 16, 32 whose S * V columns
-    // span the row, else 32; narrower while the LDS exceeds 160 KB
-    p.vec = 4;
-    while (p.vec > 1 && d.out_f % p.vec != 0) p.vec >>= 1;
-    p.slices = 4;
-    while (p.slices < 32 && p.slices * p.vec < d.out_f) p.slices <<= 1;
-    while (table_lds(d, p.slices, p.vec, nullptr) > 160 * 1024 && (p.slices > 4 || p.vec > 1)) {
-        if (p.slices > 4)
-            p.slices >>= 1;
-        else
-            p.vec >>= 1;
-    }
-    table_lds(d, p.slices, p.vec, &p);
-    p.o_chunk = p.slices * p.vec;
-    p.o_chunks = (d.out_f + p.o_chunk - 1) / p.o_chunk;
-    p.lut_threads = kLutThreads;
+    // row kernel: V columns per lane (a divisor of the row, at most 4), S
+    // lanes per row group: the smallest power of two from 4 whose S * V
+    // columns cover min(O, 64); 64-column chunks keep one chunk of the grad
+    // rows within an XCD's L2 while the tables of the chunk are walked
+    p.rows_vec = 4;
+    while (p.rows_vec > 1 && d.out_f % p.rows_vec != 0) p.rows_vec >>= 1;
+    p.rows_slices = 4;
+    while (p.rows_slices < 64 && p.rows_slices * p.rows_vec < (d.out_f < 64 ? d.out_f : 64)) p.rows_slices <<= 1;
+    const int rows_chunk = p.rows_slices * p.rows_vec;
+    p.rows_chunks = (d.out_f + rows_chunk - 1) / rows_chunk;
+    p.rows_part_off = ((d.rows + 1) * 4 + 15) & ~15;
+    p.rows_lds_bytes = p.rows_part_off + (kRowsThreads / p.rows_slices) * 2 * rows_chunk * 4;
+    p.sort_lds_bytes = ((kSortThreads / kWave) * d.rows + d.rows + kSortThreads / kWave) * 4 + (kSortThreads / kWave) * 8 * 4;
+    // the sorted slots of a table: its items plus up to K - 1 padding slots
+    // per row, rounded up to whole batches
+    p.sort_slots = (d.items + d.rows * (kRowsBatch - 1) + kRowsBatch - 1) / kRowsBatch * kRowsBatch;
 
     // item kernel: N elements per lane as in the forward (the smallest power
     // of two whose 64-lane tile spans the row, 16 bytes at most, dividing the
@@ -1315,8 +1270,23 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
         p.f_lds_bytes = off;
         p.fused = d.rows * p.fpitch * 4 <= 64 * 1024 && off <= 160 * 1024;
     }
-    p.workspace_bytes = static_cast<size_t>(d.tables) * d.items *
-                        (p.fused ? sizeof(uint64_t) : (p.full ? d.comps * sizeof(float) : sizeof(float)));
+    // workspace: fused path {gu, r} [T][B] u64; general path gu ([T][B], or
+    // [T][C][B] with the full STE) f32, then the sort kernel's slot offsets
+    // [T][slots] u32, row starts [T][R + 1] i32 and batch rows
+    // [T][slots / K] i32, each region 16-byte aligned
+    auto align16 = [](size_t v) { return (v + 15) & ~static_cast<size_t>(15); };
+    if (p.fused) {
+        p.workspace_bytes = static_cast<size_t>(d.tables) * d.items * sizeof(uint64_t);
+    } else {
+        size_t off = align16(static_cast<size_t>(d.tables) * d.items * (p.full ? d.comps : 1) * sizeof(float));
+        p.ws_slot_off = off;
+        off = align16(off + static_cast<size_t>(d.tables) * p.sort_slots * sizeof(uint32_t));
+        p.ws_row_start = off;
+        off = align16(off + static_cast<size_t>(d.tables) * (d.rows + 1) * sizeof(int32_t));
+        p.ws_batch_row = off;
+        off = align16(off + static_cast<size_t>(d.tables) * (p.sort_slots / kRowsBatch) * sizeof(int32_t));
+        p.workspace_bytes = off;
+    }
     return p;
 }
 
@@ -1416,29 +1386,37 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
         if (e != hipSuccess) return e;
     }
     if (grad_lut == nullptr && grad_thr == nullptr) return hipSuccess;
-    LutArgs b{};
-    b.grad_out = grad_out;
-    b.rec = rec64;
-    b.gu = workspace;
-    b.full = p.full ? 1 : 0;
-    b.scale = scale;
-    b.grad_lut = grad_lut;
-    b.grad_thr = grad_thr;
-    b.g_bytes = g_bytes;
-    b.items = d.items;
-    b.out_f = d.out_f;
-    b.tables = d.tables;
-    b.comps = d.comps;
-    b.rows = d.rows;
-    b.o_chunk = p.o_chunk;
-    b.hist_off = p.hist_off;
-    b.start_off = p.start_off;
-    b.sorted_off = p.sorted_off;
-    b.rowbuf_off = p.rowbuf_off;
-    b.part_off = p.part_off;
-    b.thr_off = p.thr_off;
-    b.wtot_off = p.wtot_off;
-    return launch_table(b, p, stream);
+    unsigned char *ws = reinterpret_cast<unsigned char *>(workspace);
+    SortArgs so{};
+    so.rec = rec64;
+    so.gu = workspace;
+    so.slot_off = grad_lut != nullptr ? reinterpret_cast<uint32_t *>(ws + p.ws_slot_off) : nullptr;
+    so.row_start = reinterpret_cast<int32_t *>(ws + p.ws_row_start);
+    so.batch_row = reinterpret_cast<int32_t *>(ws + p.ws_batch_row);
+    so.grad_thr = grad_thr;
+    so.full = p.full ? 1 : 0;
+    so.items = d.items;
+    so.out_f = d.out_f;
+    so.comps = d.comps;
+    so.rows = d.rows;
+    so.slots = p.sort_slots;
+    if (hipError_t e = launch_kernel(TROPNN_KERNEL_BACKWARD_SORT, pairwise_bwd_sort_kernel, dim3(d.tables),
+                                     dim3(kSortThreads), p.sort_lds_bytes, stream, so);
+        e != hipSuccess || grad_lut == nullptr)
+        return e;
+    RowsArgs r{};
+    r.grad_out = grad_out;
+    r.slot_off = so.slot_off;
+    r.row_start = so.row_start;
+    r.batch_row = so.batch_row;
+    r.grad_lut = grad_lut;
+    r.scale = scale;
+    r.g_bytes = g_bytes;
+    r.out_f = d.out_f;
+    r.rows = d.rows;
+    r.slots = p.sort_slots;
+    r.part_off = p.rows_part_off;
+    return launch_rows(r, p, d.tables, stream);
 }
 
 }  // namespace tropnn

@@ -38,17 +38,20 @@ struct ForwardPlan {
     int lds_bytes;
 };
 
-// Launch shape of the backward: the item kernel (STE dots, gu, input
-// gradient) and the table kernel (LUT gradient, threshold gradient).
+// Launch shape of the backward. General path: the item kernel (STE dots, gu,
+// input gradient), the sort kernel (items of each table in code order,
+// threshold gradient) and the row kernel (LUT gradient).
 struct BackwardPlan {
-    // table kernel
-    int vec;            // V: columns per lane (divides the row, at most 4)
-    int slices;         // S: lanes per row group (4 to 32)
-    int o_chunk;        // S * V output columns per table workgroup
-    int o_chunks;       // grid.y of the table kernel
-    int lut_threads;    // threads of a table workgroup = items per sort tile
-    int hist_off, start_off, sorted_off, rowbuf_off, part_off, thr_off, wtot_off;  // LDS byte offsets
-    int lut_lds_bytes;
+    // row kernel
+    int rows_vec;       // V: columns per lane (divides the row, at most 4)
+    int rows_slices;    // S: lanes per row group (4 to 64)
+    int rows_chunks;    // grid.y: column chunks of S * V
+    int rows_part_off;  // LDS byte offset of the split-row slots
+    int rows_lds_bytes;
+    // sort kernel
+    int sort_lds_bytes;
+    int sort_slots;     // sorted-slot capacity of a table (items + padding to whole batches)
+    size_t ws_slot_off, ws_row_start, ws_batch_row;  // workspace byte offsets (general path)
     // item kernel
     int item_vec;       // N: LUT / grad elements per lane load (16 bytes at most)
     int item_o_tiles;   // 64 * N column tiles per row
@@ -60,7 +63,7 @@ struct BackwardPlan {
     // fused path (O a multiple of 4 up to 64, or of 8 up to 256, a table's LUT
     // rows within 64 KB as f32): one kernel per table does the LUT gradient, the
     // STE dots and the threshold gradient; a scatter kernel per item the input
-    // gradient. Otherwise the item and table kernels above.
+    // gradient. Otherwise the item, sort and row kernels above.
     bool fused;
     int fvec;           // V: columns per lane
     int fslices;        // S: lanes per row group, S * V >= O
@@ -70,7 +73,7 @@ struct BackwardPlan {
     int f_slots;        // sorted-list capacity of a tile (items + padding to whole batches)
     int f_lds_bytes;
     int scatter_lds_bytes;   // gu slots [T * C] f32 + the inverse anchor index
-    size_t workspace_bytes;  // fused: {gu, r} [T][B] u64; full STE: gu [T][C][B] f32; else gu [T][B] f32
+    size_t workspace_bytes;  // fused: {gu, r} [T][B] u64; general: gu, then the sort kernel's output
 };
 
 // Row loads a forward wave keeps in flight (its gather chunk), by LUT element
