@@ -64,15 +64,19 @@ def test_workspace_size(lib):
     assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_MIN_MARGIN) == 136 * 512 * 8
     # general path: gu [T][B] f32 (full STE: [T][C][B]), then the sort
     # kernel's slot offsets [T][slots] (slots = B + R (K - 1), K = 8, rounded
-    # up to whole batches), row starts [T][R + 1] and batch rows [T][slots / K]
-    def general(b, t, r, gu_per_item):
+    # up to whole batches), row starts [T][R + 1], batch rows [T][slots / K]
+    # and the chunk-major copy of G [chunks][B][P] (P = 64 columns, or the
+    # row's width rounded up to the row kernel's lanes)
+    def general(b, o, t, r, gu_per_item, p):
         a16 = lambda v: (v + 15) // 16 * 16
         slots = (b + r * 7 + 7) // 8 * 8
-        return a16(a16(a16(a16(t * b * 4 * gu_per_item) + t * slots * 4) + t * (r + 1) * 4) + t * (slots // 8) * 4)
+        chunks = (o + p - 1) // p
+        head = a16(a16(a16(t * b * 4 * gu_per_item) + t * slots * 4) + t * (r + 1) * 4)
+        return a16(a16(head + t * (slots // 8) * 4) + chunks * b * p * 4)
 
-    assert ws(64, 1024, 4096, 512, 8, ph.LUT_F16, ph.STE_MIN_MARGIN) == general(64, 512, 256, 1)
-    assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_FULL) == general(512, 136, 64, 6)
-    assert ws(33, 20, 10, 7, 3, ph.LUT_F32, ph.STE_MIN_MARGIN) == general(33, 7, 8, 1)
+    assert ws(64, 1024, 4096, 512, 8, ph.LUT_F16, ph.STE_MIN_MARGIN) == general(64, 4096, 512, 256, 1, 64)
+    assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_FULL) == general(512, 128, 136, 64, 6, 64)
+    assert ws(33, 20, 10, 7, 3, ph.LUT_F32, ph.STE_MIN_MARGIN) == general(33, 10, 7, 8, 1, 16)
     assert ws(512, 128, 128, 136, 9, ph.LUT_F32, ph.STE_MIN_MARGIN) == 0
     assert ws(512, 128, 128, 136, 6, ph.LUT_F32, 7) == 0 and "ste_mode" in _err(lib)
 

@@ -49,8 +49,9 @@
 //      give each item its rank among equal codes of its wave; per-wave counts
 //      and a DPP scan give row starts), written once to the workspace as the
 //      items' grad-row offsets with every row padded to whole batches of 8
-//      slots, plus each batch's row; and the table's threshold gradient from
-//      gu.
+//      slots, plus each batch's row; the table's share of a chunk-major copy
+//      of G (64-column chunks, each one contiguous block); and the table's
+//      threshold gradient from gu.
 //  (3) row kernel, one workgroup per (table, 64-column chunk): row groups of
 //      S lanes (V columns each) walk balanced contiguous ranges of the sorted
 //      batches, eight grad-row loads in flight per batch (padding slots read
@@ -69,6 +70,7 @@ namespace {
 constexpr int kSortThreads = 1024;  // items per tile of the sort kernel
 constexpr int kRowsThreads = 1024;  // threads of a row-kernel workgroup
 constexpr int kRowsBatch = 8;       // sorted slots per row-kernel batch; rows are padded to whole batches
+constexpr int kRowsChunk = 64;     // columns of a row-kernel workgroup (at most): 2 MB of G at c4, within an L2
 constexpr uint32_t kSlotPad = 0x80000000u;  // grad-row offset of a padding slot: past any grad buffer (<= 2 GiB)
 constexpr int kItemTables = 16;    // tables per item-kernel wave (one reduce-scatter)
 constexpr int kEntries = 16;       // index entries a walker reads per batch
@@ -97,20 +99,24 @@ struct SortArgs {
     int32_t *row_start;   // [T][R + 1] first slot of each LUT row; [R] = the padded length
     int32_t *batch_row;   // [T][slots / kRowsBatch] the LUT row of each batch of slots
     float *grad_thr;      // or null
+    const float *grad_out;  // G [B][O]
+    float *g_chunked;     // G copied chunk-major: [chunks][B][P] (P = the row kernel's chunk width)
     int full;             // full STE: gu of every comparison
     int items, out_f, comps, rows, slots;
+    int chunk_cols, chunk_vec, chunks;  // P, the row kernel's V, ceil(O / P)
 };
 
 // Row kernel (general path), one workgroup per (table, column chunk).
 struct RowsArgs {
-    const float *grad_out;
+    const float *g_chunked;  // [chunks][B][P]
     const uint32_t *slot_off;
     const int32_t *row_start;
     const int32_t *batch_row;
     float *grad_lut;
     float scale;
-    uint32_t g_bytes;
-    int out_f, rows, slots, part_off;
+    uint32_t gc_bytes;     // bytes of the chunk-major copy
+    uint32_t chunk_bytes;  // B * P * 4: one chunk of the copy
+    int out_f, rows, tables, slots, part_off;
 };
 
 __device__ __forceinline__ int rec_code(uint64_t r) { return static_cast<int>((r >> 32) & 0xffffu); }
@@ -437,14 +443,18 @@ __device__ __forceinline__ int wave_code_rank(int code, bool valid, int R, int C
 }
 
 // Sort kernel: the stable counting sort of table t's items by LUT row code,
-// written once for every column chunk of the row kernel. Pass 1 counts each
+// written once for every column chunk of the row kernel, and table t's share
+// of a chunk-major copy of G for the row kernel (G's rows are O * 4 bytes
+// apart, a power of two at c4, so one column chunk of every row maps onto
+// few L2 sets; the copy makes a chunk one contiguous block). Pass 1 counts each
 // code over tiles of 1024 items (and sums the threshold gradient's partials:
 // -gu at each item's min-margin comparison, or at every comparison with the
 // full STE, a fixed tree per wave, waves in order, tiles in order); the row
 // starts are the counts rounded up to whole batches of kRowsBatch slots,
 // exclusively scanned. Pass 2 places every item at its row's next free slot
 // (tiles, waves and lanes in order, so item order is kept inside a row) as
-// its grad-row byte offset; padding slots get kSlotPad.
+// its byte offset b * P * 4 inside a chunk of the copy; padding slots get
+// kSlotPad.
 __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArgs a) {
     constexpr int kWaves = kSortThreads / kWave;
     constexpr int K = kRowsBatch;
@@ -532,12 +542,35 @@ __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArg
                 base[tid] = run;
             }
             __syncthreads();
-            if (valid) so[cnt[wave * R + code] + rank] = static_cast<uint32_t>(b) * static_cast<uint32_t>(a.out_f) * 4u;
+            if (valid) so[cnt[wave * R + code] + rank] = static_cast<uint32_t>(b) * static_cast<uint32_t>(a.chunk_cols) * 4u;
             __syncthreads();  // the next tile rewrites the counts
+        }
+
+        // 4. this table's share of the chunk-major copy: rows (chunk, item)
+        //    of P columns, a contiguous range of them per table; the row's
+        //    pieces of V columns go to consecutive threads, so both sides are
+        //    contiguous. Pieces past O stay unwritten (the row kernel masks
+        //    those columns).
+        const int pieces = a.chunk_cols / a.chunk_vec;  // S, a power of two <= 64
+        const int rows_total = a.chunks * a.items;
+        const int r0 = static_cast<int>(static_cast<int64_t>(rows_total) * t / gridDim.x);
+        const int r1 = static_cast<int>(static_cast<int64_t>(rows_total) * (t + 1) / gridDim.x);
+        const int piece = tid % pieces;
+        for (int cb = r0 + tid / pieces; cb < r1; cb += kSortThreads / pieces) {
+            const int chunk = cb / a.items, b = cb - chunk * a.items;
+            const int col = chunk * a.chunk_cols + piece * a.chunk_vec;
+            if (col >= a.out_f) continue;
+            const float *src = a.grad_out + static_cast<size_t>(b) * a.out_f + col;
+            float *dst = a.g_chunked + static_cast<size_t>(cb) * a.chunk_cols + piece * a.chunk_vec;
+            if (a.chunk_vec == 4) {
+                *reinterpret_cast<vec_t<float, 4> *>(dst) = *reinterpret_cast<const vec_t<float, 4> *>(src);
+            } else {
+                for (int e = 0; e < a.chunk_vec; ++e) dst[e] = src[e];
+            }
         }
     }
 
-    // 4. threshold gradient: the waves' sums in wave order
+    // 5. threshold gradient: the waves' sums in wave order
     if (thr) {
         __syncthreads();
         if (tid < C) {
@@ -548,7 +581,9 @@ __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArg
     }
 }
 
-// Row kernel: LUT gradient of table t over columns [chunk * S * V, + S * V).
+// Row kernel: LUT gradient of table t over columns [chunk * S * V, + S * V),
+// reading the chunk-major copy of G (an item's piece of the chunk at
+// slot offset + chunk * B * P * 4).
 // The sorted slots form batches of kRowsBatch, each inside one row; the
 // batches are dealt to row groups (S lanes x V columns) as contiguous ranges
 // of lo or lo + 1 batches, the longer ones first. Per batch a group loads its
@@ -567,13 +602,20 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
     extern __shared__ __align__(16) unsigned char lds[];
     int *rs = reinterpret_cast<int *>(lds);                       // [R + 1] row starts (slots)
     float *part = reinterpret_cast<float *>(lds + a.part_off);    // [groups][2][P] split rows
-    const int t = blockIdx.x, R = a.rows, O = a.out_f;
+    // unit = chunk * T + table, each XCD taking one contiguous block of units:
+    // an XCD walks its chunks one at a time over every table, so the chunk's
+    // slice of G is read into its L2 once
+    const int unit = xcd_block_unit(blockIdx.x, gridDim.x);
+    const int chunk = unit / a.tables, t = unit - chunk * a.tables;
+    const int R = a.rows, O = a.out_f;
     const int tid = threadIdx.x, g = tid / S, j = tid % S;
-    const int col = blockIdx.y * P + j * V;
+    const int col = chunk * P + j * V;
     const bool col_ok = col < O;  // V divides O: a lane's columns are all in or all out
-    const uint32_t gcol = static_cast<uint32_t>(col) * 4u;
+    // grad-row piece of slot offset s: s + chunk base + lane offset; padding
+    // (s = kSlotPad) and dead columns fall past the copy and read zeros
+    const uint32_t gcol = static_cast<uint32_t>(chunk) * a.chunk_bytes + static_cast<uint32_t>(j * V) * 4u;
     const uint32_t coldead = col_ok ? 0u : kOutOfRange;
-    const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.grad_out, a.g_bytes);
+    const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.g_chunked, a.gc_bytes);
     const uint32_t *so = a.slot_off + static_cast<size_t>(t) * a.slots;
     const int32_t *br = a.batch_row + static_cast<size_t>(t) * (a.slots / K);
     float *gl = a.grad_lut + static_cast<size_t>(t) * R * O;
@@ -625,14 +667,11 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
     meta(b_begin, offn, rown);
     for (int i = 0; __ballot(b_begin + i < b_end) != 0; ++i) {  // wave-uniform trip count
         const int bt = b_begin + i;
-        uint32_t off[K];
-#pragma unroll
-        for (int u = 0; u < K; ++u) off[u] = offn[u];
         const int k = rown;
-        meta(bt + 1, offn, rown);
         float gv[K][V];
 #pragma unroll
-        for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, (off[u] + gcol) | coldead, 0, gv[u]);
+        for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, (offn[u] + gcol) | coldead, 0, gv[u]);
+        meta(bt + 1, offn, rown);  // the next batch's offsets, while these rows arrive
         if (bt < b_end && k != cur) {
             if (cur >= 0) finish(cur);
             cur = k;
@@ -1121,7 +1160,7 @@ hipError_t allow_lds(K kernel, int bytes) {
 
 template <int V, int S>
 hipError_t launch_rows_vs(const RowsArgs &args, const BackwardPlan &p, int tables, hipStream_t stream) {
-    return launch_kernel(TROPNN_KERNEL_BACKWARD_TABLE, pairwise_bwd_rows_kernel<V, S>, dim3(tables, p.rows_chunks),
+    return launch_kernel(TROPNN_KERNEL_BACKWARD_TABLE, pairwise_bwd_rows_kernel<V, S>, dim3(tables * p.rows_chunks),
                          dim3(kRowsThreads), p.rows_lds_bytes, stream, args);
 }
 
@@ -1202,8 +1241,9 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     p.rows_vec = 4;
     while (p.rows_vec > 1 && d.out_f % p.rows_vec != 0) p.rows_vec >>= 1;
     p.rows_slices = 4;
-    while (p.rows_slices < 64 && p.rows_slices * p.rows_vec < (d.out_f < 64 ? d.out_f : 64)) p.rows_slices <<= 1;
+    while (p.rows_slices < 64 && p.rows_slices * p.rows_vec < (d.out_f < kRowsChunk ? d.out_f : kRowsChunk)) p.rows_slices <<= 1;
     const int rows_chunk = p.rows_slices * p.rows_vec;
+    p.rows_chunk = rows_chunk;
     p.rows_chunks = (d.out_f + rows_chunk - 1) / rows_chunk;
     p.rows_part_off = ((d.rows + 1) * 4 + 15) & ~15;
     p.rows_lds_bytes = p.rows_part_off + (kRowsThreads / p.rows_slices) * 2 * rows_chunk * 4;
@@ -1285,6 +1325,8 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
         off = align16(off + static_cast<size_t>(d.tables) * (d.rows + 1) * sizeof(int32_t));
         p.ws_batch_row = off;
         off = align16(off + static_cast<size_t>(d.tables) * (p.sort_slots / kRowsBatch) * sizeof(int32_t));
+        p.ws_g_chunked = off;
+        off = align16(off + static_cast<size_t>(p.rows_chunks) * d.items * rows_chunk * sizeof(float));
         p.workspace_bytes = off;
     }
     return p;
@@ -1394,6 +1436,11 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
     so.row_start = reinterpret_cast<int32_t *>(ws + p.ws_row_start);
     so.batch_row = reinterpret_cast<int32_t *>(ws + p.ws_batch_row);
     so.grad_thr = grad_thr;
+    so.grad_out = grad_out;
+    so.g_chunked = reinterpret_cast<float *>(ws + p.ws_g_chunked);
+    so.chunk_cols = p.rows_chunk;
+    so.chunk_vec = p.rows_vec;
+    so.chunks = p.rows_chunks;
     so.full = p.full ? 1 : 0;
     so.items = d.items;
     so.out_f = d.out_f;
@@ -1405,15 +1452,17 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
         e != hipSuccess || grad_lut == nullptr)
         return e;
     RowsArgs r{};
-    r.grad_out = grad_out;
+    r.g_chunked = so.g_chunked;
     r.slot_off = so.slot_off;
     r.row_start = so.row_start;
     r.batch_row = so.batch_row;
     r.grad_lut = grad_lut;
     r.scale = scale;
-    r.g_bytes = g_bytes;
+    r.chunk_bytes = static_cast<uint32_t>(static_cast<size_t>(d.items) * p.rows_chunk * 4);
+    r.gc_bytes = static_cast<uint32_t>(static_cast<size_t>(p.rows_chunks) * r.chunk_bytes);
     r.out_f = d.out_f;
     r.rows = d.rows;
+    r.tables = d.tables;
     r.slots = p.sort_slots;
     r.part_off = p.rows_part_off;
     return launch_rows(r, p, d.tables, stream);

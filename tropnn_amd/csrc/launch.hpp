@@ -45,13 +45,14 @@ struct BackwardPlan {
     // row kernel
     int rows_vec;       // V: columns per lane (divides the row, at most 4)
     int rows_slices;    // S: lanes per row group (4 to 64)
-    int rows_chunks;    // grid.y: column chunks of S * V
+    int rows_chunk;     // P = S * V columns per workgroup
+    int rows_chunks;    // column chunks of P
     int rows_part_off;  // LDS byte offset of the split-row slots
     int rows_lds_bytes;
     // sort kernel
     int sort_lds_bytes;
     int sort_slots;     // sorted-slot capacity of a table (items + padding to whole batches)
-    size_t ws_slot_off, ws_row_start, ws_batch_row;  // workspace byte offsets (general path)
+    size_t ws_slot_off, ws_row_start, ws_batch_row, ws_g_chunked;  // workspace byte offsets (general path)
     // item kernel
     int item_vec;       // N: LUT / grad elements per lane load (16 bytes at most)
     int item_o_tiles;   // 64 * N column tiles per row
