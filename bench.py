@@ -97,7 +97,6 @@ def log(msg: str) -> None:
 KERNEL_SOURCES = (
     "tropnn_amd/csrc/forward.hip",
     "tropnn_amd/csrc/backward.hip",
-    "tropnn_amd/csrc/abi.hip",
     "tropnn_amd/csrc/device.hpp",
     "tropnn_amd/csrc/launch.hpp",
     "include/tropnn_hip.h",
@@ -105,8 +104,10 @@ KERNEL_SOURCES = (
 
 
 def source_digest() -> str:
-    """sha256 of the kernel sources with comments and whitespace removed, so
-    that a comment edit does not invalidate a profile of the same code."""
+    """sha256 of the kernel sources (kernels, launch planning, the shared
+    header; not the C ABI's argument validation) with comments and
+    whitespace removed, so that a comment edit does not invalidate a profile
+    of the same code."""
     import hashlib
     import re
 

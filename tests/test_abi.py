@@ -144,6 +144,10 @@ def test_backward_rejects_bad_arguments(lib):
     small_ws = list(args)
     small_ws[19] = 4
     assert bwd(*small_ws) == 1 and "workspace" in _err(lib)
+    # the LUT gradient alone needs the workspace too (the general path sorts into it)
+    lut_only = list(args)
+    lut_only[15], lut_only[16], lut_only[18] = None, None, None
+    assert bwd(*lut_only) == 1 and "workspace" in _err(lib)
 
 
 def test_event_hook_rejects_bad_kernel(lib):

@@ -264,6 +264,12 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
     if (lut_bytes > (int64_t{1} << 31) || g_bytes > (int64_t{1} << 31))
         return fail(TROPNN_ERR_UNSUPPORTED, "LUT (%lld bytes) or grad_output (%lld bytes) exceeds the 2 GiB limit",
                     (long long)lut_bytes, (long long)g_bytes);
+    // the general path's chunk-major copy of grad_output (rows rounded up to
+    // whole column chunks) is addressed the same way
+    const int64_t gc_bytes = int64_t{p.rows_chunks} * p.rows_chunk * d.items * 4;
+    if (!p.fused && grad_lut && gc_bytes > (int64_t{1} << 31))
+        return fail(TROPNN_ERR_UNSUPPORTED, "grad_output in column chunks (%lld bytes) exceeds the 2 GiB limit",
+                    (long long)gc_bytes);
     hipError_t e = tropnn::launch_backward(d, p, grad_output, lut, route_record, margins, index_offsets,
                                            index_entries, output_scale, surrogate, grad_latent, grad_thresholds,
                                            grad_lut, static_cast<float *>(workspace), static_cast<hipStream_t>(stream));
