@@ -381,6 +381,41 @@ def test_route_debug_cache_off():
     assert hip._last_indices is None and hip._last_margins is None
 
 
+# ---------------------------------------------------------------- large batches
+@pytest.mark.parametrize("lut_dtype", ["f32", "f16"])
+def test_large_batch_forward_multi_item(lut_dtype):
+    """From 2048 items a forward workgroup takes 8 items. At 2053 items (a
+    partial last workgroup): codes and margins bit-exact against the oracle,
+    the output within tolerance, and bit-identical to the one-item kernel's
+    (the same items run as two calls below the threshold)."""
+    i, o, t, c, b = 128, 128, 136, 6, 2053
+    ref, hip = make_pair(i, o, t, c, seed=4, thr_std=0.3, lut_dtype=lut_dtype)
+    x = seeded((b, i), seed=21)
+    xd = x.to(DEV)
+    hip.eval()
+    with torch.no_grad():
+        y_full = hip(xd)
+        idx, mar = hip._last_indices.clone(), hip._last_margins.clone()
+        y_parts = torch.cat([hip(xd[:1024]), hip(xd[1024:])])
+    torch.cuda.synchronize()
+    assert torch.equal(y_full, y_parts)
+    codes = routing_np.route_codes(x.numpy(), ref.anchors.numpy(), ref.thresholds.detach().numpy())
+    margins = routing_np.margins_f32(x.numpy(), ref.anchors.numpy(), ref.thresholds.detach().numpy())
+    np.testing.assert_array_equal(idx.cpu().reshape(b, t).numpy(), codes)
+    np.testing.assert_array_equal(mar.cpu().reshape(b, t, c).numpy().view(np.uint32), margins.view(np.uint32))
+    with torch.no_grad():
+        y_ref = ref.eval()(x)
+    assert rel_err(y_full, y_ref) <= (F16_TOL if lut_dtype == "f16" else F32_TOL)
+
+
+def test_large_batch_training_multi_item():
+    ref, hip = make_pair(64, 32, 20, 5, seed=6, thr_std=0.4)
+    x = seeded((2053, 64), seed=22)
+    g = seeded((2053, 1, 32), seed=23)
+    yx_ref, yx_hip = train_step(ref, hip, x, g)
+    assert_train_parity(ref, hip, yx_ref, yx_hip)
+
+
 # ---------------------------------------------------------------- route-debug codes format
 @pytest.mark.parametrize(
     "i,o,t,c,b",

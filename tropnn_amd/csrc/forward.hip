@@ -252,6 +252,146 @@ __global__ __launch_bounds__(1024) void pairwise_forward_kernel(FwdArgs a) {
     }
 }
 
+// Large batches: one workgroup takes kMultiItems consecutive items (and one
+// output tile of 64 * N columns). Its waves load their comparators once for
+// all the items, the items' input rows are staged as one contiguous block,
+// every item is routed from LDS (its codes to the wave's per-item list), and
+// the gathers go two items at a time (2 x 16 row loads in flight per wave,
+// rows summed in table order as the one-item kernel sums them). The waves'
+// partial rows of all the items meet in LDS once and are summed in wave
+// order, so this kernel's outputs equal the one-item kernel's bit for bit.
+// Planner conditions: at most 16 tables per wave in at most kBallots
+// ballots, and at most 8 bytes of a row per lane.
+constexpr int kMultiItems = 8;
+constexpr int kMultiMinItems = 2048;  // batches from which a workgroup takes kMultiItems items
+
+template <typename T, int N, bool TRAIN, bool DEBUG>
+__global__ __launch_bounds__(1024) void pairwise_forward_multi_kernel(FwdArgs a) {
+    constexpr int M = kMultiItems;
+    constexpr int kG = 16;
+    static_assert(N * sizeof(T) <= 8, "two items' row chunks must fit the registers");
+    extern __shared__ __align__(16) unsigned char lds[];
+    float *xs = reinterpret_cast<float *>(lds);                // [M][in_f]
+    float *red = reinterpret_cast<float *>(lds + a.red_off);   // [waves][M][64 N]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nwaves = blockDim.x >> 6;
+    const int b0 = xcd_block_unit(blockIdx.x, gridDim.x) * M;
+    const int nitems = min(M, a.items - b0);
+    uint8_t *codes_w = lds + a.codes_off + wave * M * a.codes_pitch;  // [M][pitch]
+
+    const int tpb = kWave >> a.lpt_log2;
+    const int slot = lane >> a.lpt_log2;
+    const int c = lane & ((1 << a.lpt_log2) - 1);
+    const int t_begin = wave * a.per_wave;
+    const int t_end = min(a.tables, t_begin + a.per_wave);
+    const int n_t = max(0, t_end - t_begin);
+    const int nballot = (n_t + tpb - 1) / tpb;
+
+    // 1. comparators, once for all the items; the items' input rows
+    Comparator pre[kBallots];
+#pragma unroll
+    for (int j = 0; j < kBallots; ++j) pre[j] = load_comparator(a, t_begin + j * tpb + slot, t_end, c);
+    {
+        const float *src = a.x + static_cast<size_t>(b0) * a.in_f;
+        const int n = nitems * a.in_f;
+        if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+            for (int k = tid; k < (n >> 2); k += blockDim.x)
+                reinterpret_cast<vec_t<float, 4> *>(xs)[k] = reinterpret_cast<const vec_t<float, 4> *>(src)[k];
+        } else {
+            for (int k = tid; k < n; k += blockDim.x) xs[k] = src[k];
+        }
+    }
+    __syncthreads();
+
+    // 2. route every item (LDS and ballots only); route records after each
+    for (int m = 0; m < M; ++m) {
+        if (m >= nitems) break;
+        const float *xm = xs + m * a.in_f;
+        uint8_t *cm = codes_w + m * a.codes_pitch;
+        RouteOut ro[kBallots];
+#pragma unroll
+        for (int j = 0; j < kBallots; ++j) {
+            ro[j] = RouteOut{0ull, false};
+            if (j < nballot)
+                ro[j] = route_ballot<TRAIN, DEBUG>(a, xm, cm, pre[j], t_begin + j * tpb + slot, j * tpb + slot, c, slot,
+                                                   b0 + m);
+        }
+        if constexpr (TRAIN) {
+#pragma unroll
+            for (int j = 0; j < kBallots; ++j)
+                if (ro[j].win) a.rec[static_cast<size_t>(t_begin + j * tpb + slot) * a.items + b0 + m] = ro[j].rec;
+        }
+        if constexpr (DEBUG) {
+            if (a.codes != nullptr && blockIdx.y == 0)
+                for (int k = lane; k < n_t; k += kWave) a.codes[static_cast<size_t>(b0 + m) * a.tables + t_begin + k] = cm[k];
+        }
+    }
+    // LDS operations of one wave complete in order: the code lists are ready
+
+    // 3. gather two items at a time
+    const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(a.lut, a.lut_bytes);
+    const int col = blockIdx.y * (kWave * N) + lane * N;
+    const uint32_t voff = col < a.out_f ? static_cast<uint32_t>(col) * static_cast<uint32_t>(sizeof(T)) : kOutOfRange;
+    const int tbase = t_begin * a.table_bytes;
+#pragma unroll
+    for (int m0 = 0; m0 < M; m0 += 2) {
+        if (m0 >= nitems) break;
+        uint32_t words[2][kG / 4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const vec_t<uint32_t, 4> w = *reinterpret_cast<const vec_t<uint32_t, 4> *>(codes_w + (m0 + h) * a.codes_pitch);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) words[h][e] = __builtin_amdgcn_readfirstlane(w[e]);
+        }
+        float v[2][kG][N];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int u = 0; u < kG; ++u) {
+                const bool live = u < n_t && m0 + h < nitems;
+                const int code = static_cast<int>((words[h][u >> 2] >> (8 * (u & 3))) & 0xffu);
+                const int soff = live ? tbase + u * a.table_bytes + code * a.row_bytes : 0;
+                buffer_row<T, N>(rsrc, live ? voff : kOutOfRange, soff, v[h][u]);
+            }
+        // the pair's partial rows (tables in order) go to LDS at once
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float acc[N];
+#pragma unroll
+            for (int e = 0; e < N; ++e) acc[e] = 0.f;
+#pragma unroll
+            for (int u = 0; u < kG; ++u)
+#pragma unroll
+                for (int e = 0; e < N; ++e) acc[e] += v[h][u][e];
+            if (m0 + h < nitems) {
+#pragma unroll
+                for (int e = 0; e < N; ++e) red[((wave * M + m0 + h) * kWave + lane) * N + e] = acc[e];
+            }
+        }
+    }
+
+    // 4. every item's partial rows, summed in wave order, scaled, stored
+    __syncthreads();
+    for (int u = tid; u < nitems * kWave; u += blockDim.x) {
+        const int m = u / kWave, l = u % kWave;
+        const int cl = blockIdx.y * (kWave * N) + l * N;
+        if (cl < a.out_f) {
+            float y[N];
+#pragma unroll
+            for (int e = 0; e < N; ++e) y[e] = red[((0 * M + m) * kWave + l) * N + e];
+            for (int w = 1; w < nwaves; ++w)
+#pragma unroll
+                for (int e = 0; e < N; ++e) y[e] += red[((w * M + m) * kWave + l) * N + e];
+#pragma unroll
+            for (int e = 0; e < N; ++e) y[e] *= a.scale;
+            store_f32_nt<N>(a.out + static_cast<size_t>(b0 + m) * a.out_f + cl, y);
+        }
+    }
+}
+
 // Route only (no gather): one thread per (item, table) evaluates the table's
 // comparisons in order and writes any of uint8 codes, int64 codes and f32
 // margins, laid out [items][tables] and [items][tables][comparisons]. The
@@ -290,6 +430,15 @@ __global__ __launch_bounds__(kRouteThreads) void pairwise_route_kernel(RouteArgs
 template <typename T, int N>
 hipError_t launch_typed(const FwdArgs &args, const ForwardPlan &p, bool train, bool debug, hipStream_t stream) {
     const dim3 grid(p.blocks, p.o_tiles), block(p.threads);
+    if constexpr (N * sizeof(T) <= 8) {
+        if (p.multi) {
+            auto kernel = train ? (debug ? pairwise_forward_multi_kernel<T, N, true, true>
+                                         : pairwise_forward_multi_kernel<T, N, true, false>)
+                                : (debug ? pairwise_forward_multi_kernel<T, N, false, true>
+                                         : pairwise_forward_multi_kernel<T, N, false, false>);
+            return launch_kernel(TROPNN_KERNEL_FORWARD, kernel, grid, block, p.lds_bytes, stream, args);
+        }
+    }
     auto kernel = train ? (debug ? pairwise_forward_kernel<T, N, true, true> : pairwise_forward_kernel<T, N, true, false>)
                         : (debug ? pairwise_forward_kernel<T, N, false, true> : pairwise_forward_kernel<T, N, false, false>);
     return launch_kernel(TROPNN_KERNEL_FORWARD, kernel, grid, block, p.lds_bytes, stream, args);
@@ -338,6 +487,35 @@ ForwardPlan plan_forward(const Dims &d) {
     p.red_off = off;
     off += (p.waves_per_item - 1) * kWave * p.vec * 4;
     p.lds_bytes = off;
+
+    // large batches: kMultiItems items per workgroup when every wave's
+    // tables fit one gather chunk of 16 in at most kBallots ballots and a
+    // lane's row chunk is at most 8 bytes
+    p.multi = false;
+    if (d.items >= kMultiMinItems && p.vec * esize <= 8) {
+        const int w16 = (d.tables + 15) / 16;
+        const int per16 = (d.tables + w16 - 1) / w16;
+        const int tpb = kWave >> p.lpt_log2;
+        if (w16 <= 16 && (per16 + tpb - 1) / tpb <= kBallots) {
+            int moff = ((kMultiItems * d.in_f * 4) + 15) & ~15;
+            const int mcodes = moff;
+            moff += w16 * kMultiItems * 16;
+            moff = (moff + 15) & ~15;
+            const int mred = moff;
+            moff += w16 * kMultiItems * kWave * p.vec * 4;
+            if (moff <= 64 * 1024) {
+                p.multi = true;
+                p.per_wave = per16;
+                p.waves_per_item = (d.tables + per16 - 1) / per16;
+                p.threads = p.waves_per_item * kWave;
+                p.blocks = (d.items + kMultiItems - 1) / kMultiItems;
+                p.codes_pitch = 16;
+                p.codes_off = mcodes;
+                p.red_off = mred;
+                p.lds_bytes = moff;
+            }
+        }
+    }
     return p;
 }
 

@@ -36,6 +36,7 @@ struct ForwardPlan {
     int codes_off;       // LDS byte offsets
     int red_off;
     int lds_bytes;
+    bool multi;          // large batch: several items per workgroup (blocks = ceil(items / kMultiItems))
 };
 
 // Launch shape of the backward. General path: the item kernel (STE dots, gu,
