@@ -202,6 +202,51 @@ __device__ __forceinline__ int xcd_block_unit(int i, int n) {
     return x * per + min(x, extra) + k;
 }
 
+// acc + the binary16 value in the low (HI = false) or high half of w, widened
+// to f32: one v_fma_mix_f32 computing half * 1.0 + acc with a single
+// rounding, the same value as a conversion (exact) followed by an add, which
+// take two instructions. hipcc turns fmaf(float(half), 1.0f, acc) back into
+// the two, hence the inline assembly.
+template <bool HI>
+__device__ __forceinline__ float add_f16_mix(float acc, uint32_t w) {
+    if constexpr (HI)
+        asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(w));
+    else
+        asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(w));
+    return acc;
+}
+
+// N elements of T per lane at byte offset voff + soff as raw 32-bit words
+// (W = N * sizeof(T) / 4, at least one; a 2-byte load fills the low half).
+template <typename T, int N>
+__device__ __forceinline__ void buffer_words(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, int soff,
+                                             uint32_t (&w)[(N * sizeof(T) + 3) / 4]) {
+    constexpr int kBytes = N * static_cast<int>(sizeof(T));
+    if constexpr (kBytes == 2) {
+        w[0] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, voff, soff, 0);
+    } else if constexpr (kBytes == 4) {
+        w[0] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff, soff, 0);
+    } else {
+        static_assert(kBytes == 8, "2, 4 or 8 bytes per lane");
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rsrc, voff, soff, 0);
+        const vec_t<uint32_t, 2> u = __builtin_bit_cast(vec_t<uint32_t, 2>, v);
+        w[0] = u[0];
+        w[1] = u[1];
+    }
+}
+
+// acc[e] += element e of a row chunk held as raw words (T = f32 or f16).
+template <typename T, int N>
+__device__ __forceinline__ void add_words(float (&acc)[N], const uint32_t (&w)[(N * sizeof(T) + 3) / 4]) {
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int e = 0; e < N; ++e) acc[e] += __builtin_bit_cast(float, w[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < N; ++e) acc[e] = (e & 1) ? add_f16_mix<true>(acc[e], w[e >> 1]) : add_f16_mix<false>(acc[e], w[e >> 1]);
+    }
+}
+
 // Clamp an anchor into [0, n) so a corrupt anchor can never address memory
 // outside the staged input row; the host validates anchors before launch.
 __device__ __forceinline__ int clamp_index(int64_t a, int n) {

@@ -346,16 +346,27 @@ __global__ __launch_bounds__(1024) void pairwise_forward_multi_kernel(FwdArgs a)
 #pragma unroll
             for (int e = 0; e < 4; ++e) words[h][e] = __builtin_amdgcn_readfirstlane(w[e]);
         }
-        float v[2][kG][N];
+        constexpr int W = (N * sizeof(T) + 3) / 4;
+        uint32_t v[2][kG][W];
+        if (n_t == kG && m0 + 1 < nitems) {  // every row live (wave-uniform): no selects
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int u = 0; u < kG; ++u) {
-                const bool live = u < n_t && m0 + h < nitems;
-                const int code = static_cast<int>((words[h][u >> 2] >> (8 * (u & 3))) & 0xffu);
-                const int soff = live ? tbase + u * a.table_bytes + code * a.row_bytes : 0;
-                buffer_row<T, N>(rsrc, live ? voff : kOutOfRange, soff, v[h][u]);
-            }
+                for (int u = 0; u < kG; ++u) {
+                    const int code = static_cast<int>((words[h][u >> 2] >> (8 * (u & 3))) & 0xffu);
+                    buffer_words<T, N>(rsrc, voff, tbase + u * a.table_bytes + code * a.row_bytes, v[h][u]);
+                }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int u = 0; u < kG; ++u) {
+                    const bool live = u < n_t && m0 + h < nitems;
+                    const int code = static_cast<int>((words[h][u >> 2] >> (8 * (u & 3))) & 0xffu);
+                    const int soff = live ? tbase + u * a.table_bytes + code * a.row_bytes : 0;
+                    buffer_words<T, N>(rsrc, live ? voff : kOutOfRange, soff, v[h][u]);
+                }
+        }
         // the pair's partial rows (tables in order) go to LDS at once
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -363,9 +374,7 @@ __global__ __launch_bounds__(1024) void pairwise_forward_multi_kernel(FwdArgs a)
 #pragma unroll
             for (int e = 0; e < N; ++e) acc[e] = 0.f;
 #pragma unroll
-            for (int u = 0; u < kG; ++u)
-#pragma unroll
-                for (int e = 0; e < N; ++e) acc[e] += v[h][u][e];
+            for (int u = 0; u < kG; ++u) add_words<T, N>(acc, v[h][u]);
             if (m0 + h < nitems) {
 #pragma unroll
                 for (int e = 0; e < N; ++e) red[((wave * M + m0 + h) * kWave + lane) * N + e] = acc[e];
