@@ -584,3 +584,19 @@ def test_anchor_index_matches_numpy():
         want_offsets.append(len(want_entries))
     np.testing.assert_array_equal(offsets, np.array(want_offsets))
     np.testing.assert_array_equal(entries[: len(want_entries)], np.array(want_entries))
+
+
+def test_no_grad_inference_writes_no_route_record():
+    """Under torch.no_grad() the forward runs without the autograd Function
+    and without a route record; outputs and debug tensors equal a forward
+    with grad enabled."""
+    _, hip = make_pair(16, 8, 5, 3, seed=1, thr_std=0.3)
+    x = seeded((9, 16), 3).to(DEV)
+    hip.eval()
+    y_grad = hip(x)
+    idx_grad, mar_grad = hip._last_indices.clone(), hip._last_margins.clone()
+    with torch.no_grad():
+        y_nog = hip(x)
+    assert not y_nog.requires_grad and y_grad.requires_grad
+    assert torch.equal(y_nog, y_grad.detach())
+    assert torch.equal(hip._last_indices, idx_grad) and torch.equal(hip._last_margins, mar_grad)

@@ -441,6 +441,19 @@ def pairwise_hip(
     _require_gpu(latent, anchors, thresholds, lut)
     if lut_read is None:
         lut_read = lut
+    if not torch.is_grad_enabled():
+        # no graph will be recorded (inference under torch.no_grad): the
+        # kernels write no route record; outputs as the Function returns them
+        out, _, indices, margins, _ = _route_forward(
+            latent.detach(),
+            anchors,
+            thresholds.detach(),
+            lut_read.detach(),
+            output_scale=float(output_scale),
+            want_record=False,
+            return_route=return_route if return_route == "codes" else bool(return_route),
+        )
+        return out, indices, margins
     return _PairwiseHipFunction.apply(
         latent,
         anchors,
