@@ -408,10 +408,20 @@ def test_large_batch_forward_multi_item(lut_dtype):
     assert rel_err(y_full, y_ref) <= (F16_TOL if lut_dtype == "f16" else F32_TOL)
 
 
-def test_large_batch_training_multi_item():
-    ref, hip = make_pair(64, 32, 20, 5, seed=6, thr_std=0.4)
-    x = seeded((2053, 64), seed=22)
-    g = seeded((2053, 1, 32), seed=23)
+@pytest.mark.parametrize(
+    "i,o,t,c,min_margin,surrogate",
+    [
+        (64, 32, 20, 5, True, "fast_sigmoid_odd"),
+        (64, 10, 20, 5, True, "fast_sigmoid_odd"),  # general backward path (O % 4 != 0)
+        (48, 24, 17, 6, False, "izhikevich"),  # full STE
+    ],
+)
+def test_large_batch_training_multi_item(i, o, t, c, min_margin, surrogate):
+    """Training at 2053 items: the multi-item forward, and the backward's
+    sort over several 1024-item tiles."""
+    ref, hip = make_pair(i, o, t, c, seed=6, thr_std=0.4, use_min_margin_ste=min_margin, surrogate=surrogate)
+    x = seeded((2053, i), seed=22)
+    g = seeded((2053, 1, o), seed=23)
     yx_ref, yx_hip = train_step(ref, hip, x, g)
     assert_train_parity(ref, hip, yx_ref, yx_hip)
 
