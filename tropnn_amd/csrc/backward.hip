@@ -23,8 +23,10 @@
 //      load per item serves the row's LUT-gradient sum (registers; rows that
 //      cross a range boundary are combined in range order afterwards) and the
 //      item's STE dot against L[nb] - L[code], completed by one
-//      reduce-scatter per batch: gu is stored as a {gu, r} record per
-//      (table, item) and summed per comparison into the threshold gradient.
+//      reduce-scatter per batch and left in the slot's LDS word; after the
+//      walk one thread per slot forms gu = dot * surrogate'(u), stores it as
+//      a {gu, r} record per (table, item) and sums it per comparison into the
+//      threshold gradient.
 //  (S) scatter kernel, one workgroup per item: expands the item's records into
 //      (table, comparison) slots and walks the inverse anchor index into
 //      grad_latent, as the item kernel's last phase does.
@@ -729,7 +731,7 @@ struct FusedArgs {
     uint64_t quad_magic;  // ceil(2^32 / (out_f / 4)): chunk index -> LUT row
     int items, out_f, tables, comps, rows;
     int slots;  // sorted-list capacity: a tile's items plus K - 1 padding slots per row
-    int lut_off, cnt_off, off_off, sorted_off, u_off, rowbuf_off, thr_off, wtot_off, part_off, brow_off;  // LDS bytes
+    int lut_off, cnt_off, off_off, sorted_off, u_off, dt_off, rowbuf_off, thr_off, wtot_off, part_off, brow_off;  // LDS bytes
 };
 
 // One workgroup per table; the row group of S lanes x V columns spans the
@@ -739,9 +741,11 @@ struct FusedArgs {
 // in item order, 32 / V at a time: one grad row load per item serves both the
 // LUT-gradient sum and the item's STE dot against L[nb] - L[code] (L[code]
 // in registers for the whole row, L[nb] from LDS). One reduce-scatter per
-// batch completes its dots; lanes holding a dot form gu, store {gu, r} for
-// the scatter kernel and leave gu in the sorted position's LDS slot, from
-// which a pass per tile reduces the threshold gradient.
+// batch completes its dots, which the lanes holding them leave in the sorted
+// positions' LDS slots; a pass per tile with one thread per slot then forms
+// gu (the surrogate's division once per item, not once per lane of a row
+// group), stores {gu, r} for the scatter kernel and reduces the threshold
+// gradient.
 template <typename T, int V, int S>
 __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(FusedArgs a) {
     constexpr int kWaves = kFusedThreads / kWave;
@@ -756,6 +760,7 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
     int *off = reinterpret_cast<int *>(lds + a.off_off);                   // [R + 1] row starts
     uint2 *ent = reinterpret_cast<uint2 *>(lds + a.sorted_off);           // [slots] sorted entries (see below)
     float *us = reinterpret_cast<float *>(lds + a.u_off);                  // [slots] margin u, by position
+    float *dt = reinterpret_cast<float *>(lds + a.dt_off);                 // [slots] scaled STE dot, by position
     float *rowbuf = reinterpret_cast<float *>(lds + a.rowbuf_off);         // [R][pitch] (several tiles)
     float *tp = reinterpret_cast<float *>(lds + a.thr_off);                // [waves][8]
     int *wtot = reinterpret_cast<int *>(lds + a.wtot_off);                 // [waves] scan carries, [1] sink
@@ -977,18 +982,10 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
                 }
                 d[q] = sd;
             }
-            if (need_gu) {
+            if (need_gu) {  // the slot's dot; gu is formed per slot after the walk
                 const float dot = reduce_scatter<S, K>(d, j) * a.scale;
                 const int q = (j / (S / K)) & (K - 1);  // the item whose dot this lane holds
-                const uint32_t y = ent[base + q].y;
-                if (j % (S / K) == 0 && (y & kPadSlot) == 0) {
-                    const int r = static_cast<int>((y >> 18) & 7u);
-                    const float gu = dot * surrogate_grad(us[base + q], a.surrogate);
-                    if (a.gurec != nullptr)
-                        a.gurec[static_cast<size_t>(t) * a.items + tile0 + ((y >> 21) & 1023u)] =
-                            static_cast<uint64_t>(__builtin_bit_cast(uint32_t, gu)) | (static_cast<uint64_t>(r) << 32);
-                    us[base + q] = gu;  // the position's margin is spent: it now holds gu
-                }
+                if (j % (S / K) == 0) dt[base + q] = dot;
             }
         }
         if (cur >= 0) finish(cur);
@@ -1023,24 +1020,34 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
                 }
             }
         }
-        // 6. threshold gradient of the tile: -gu at each sorted position's
-        //    min-margin comparison, a fixed tree per wave (lane 8c ends with
-        //    the wave's sum for comparison c) added to the wave's slots. The
-        //    next placement rewrites the sorted list only after two barriers.
-        if (a.grad_thr != nullptr) {  // padding slots hold gu = 0
+        // 6. one thread per sorted slot: gu = dot * surrogate'(u), the
+        //    {gu, r} record for the scatter kernel, and the threshold
+        //    gradient of the tile: -gu at the slot's min-margin comparison,
+        //    a fixed tree per wave (lane 8c ends with the wave's sum for
+        //    comparison c) added to the wave's slots. Padding slots carry no
+        //    gu. The next placement rewrites the sorted list only after two
+        //    barriers.
+        if (need_gu) {
             const int slots = off[R];
             if (wave * kWave < slots) {
                 float tv[8];
 #pragma unroll
                 for (int c = 0; c < 8; ++c) tv[c] = 0.f;
                 for (int q = tidl; q < slots; q += kFusedThreads) {
-                    const int r = static_cast<int>((ent[q].y >> 18) & 7u);
-                    const float gu = us[q];
+                    const uint32_t y = ent[q].y;
+                    const int r = static_cast<int>((y >> 18) & 7u);
+                    const bool pad = (y & kPadSlot) != 0;
+                    const float gu = pad ? 0.f : dt[q] * surrogate_grad(us[q], a.surrogate);
+                    if (!pad && a.gurec != nullptr)
+                        a.gurec[static_cast<size_t>(t) * a.items + tile0 + ((y >> 21) & 1023u)] =
+                            static_cast<uint64_t>(__builtin_bit_cast(uint32_t, gu)) | (static_cast<uint64_t>(r) << 32);
 #pragma unroll
                     for (int c = 0; c < 8; ++c) tv[c] += r == c ? -gu : 0.f;
                 }
-                const float tot = reduce_scatter<kWave, 8>(tv, lane);
-                if ((lane & 7) == 0) tp[wave * 8 + (lane >> 3)] += tot;
+                if (a.grad_thr != nullptr) {
+                    const float tot = reduce_scatter<kWave, 8>(tv, lane);
+                    if ((lane & 7) == 0) tp[wave * 8 + (lane >> 3)] += tot;
+                }
             }
         }
         if (next >= a.items) break;
@@ -1298,6 +1305,8 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
         off += (p.f_slots + batch) * 8;  // entries, then the sentinel slots
         p.f_u_off = off;
         off += (p.f_slots + batch) * 4;
+        p.f_dt_off = off;
+        off += (p.f_slots + batch) * 4;
         p.f_thr_off = off;
         off += waves * 8 * 4;
         p.f_wtot_off = off;
@@ -1368,6 +1377,7 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
         f.off_off = p.f_off_off;
         f.sorted_off = p.f_sorted_off;
         f.u_off = p.f_u_off;
+        f.dt_off = p.f_dt_off;
         f.rowbuf_off = p.f_rowbuf_off;
         f.thr_off = p.f_thr_off;
         f.wtot_off = p.f_wtot_off;

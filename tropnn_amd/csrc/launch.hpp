@@ -70,7 +70,7 @@ struct BackwardPlan {
     int fvec;           // V: columns per lane
     int fslices;        // S: lanes per row group, S * V >= O
     int fpitch;         // S * V: LDS row pitch in floats
-    int f_lut_off, f_cnt_off, f_off_off, f_sorted_off, f_u_off, f_rowbuf_off, f_thr_off, f_wtot_off;  // LDS bytes
+    int f_lut_off, f_cnt_off, f_off_off, f_sorted_off, f_u_off, f_dt_off, f_rowbuf_off, f_thr_off, f_wtot_off;  // LDS bytes
     int f_part_off, f_brow_off;
     int f_slots;        // sorted-list capacity of a tile (items + padding to whole batches)
     int f_lds_bytes;
