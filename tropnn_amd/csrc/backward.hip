@@ -692,7 +692,8 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
     // a row split over ranges as its pieces in range order (slot 1 of its
     // first range, slot 0 of the others); rows inside one range are written
     const int bl = lo + 1;
-    auto range_of = [&](int bt) { return bt < extra * bl ? bt / bl : extra + (bt - extra * bl) / max(lo, 1); };
+    const float inv_bl = 1.0f / static_cast<float>(bl), inv_lo = 1.0f / static_cast<float>(max(lo, 1));
+    auto range_of = [&](int bt) { return bt < extra * bl ? small_div(bt, inv_bl) : extra + small_div(bt - extra * bl, inv_lo); };
     for (int k = g; k < R; k += NG) {
         const int fb = rs[k] / K, nbk = rs[k + 1] / K - fb;
         vec_t<float, V> w = 0.f;
@@ -997,7 +998,10 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
         //    (slot 1 of its first range, slot 0 of the others)
         if (a.grad_lut != nullptr) {
             const int bl = lo + 1;  // ranges of the first `extra` groups
-            auto range_of = [&](int bt) { return bt < extra * bl ? bt / bl : extra + (bt - extra * bl) / max(lo, 1); };
+            const float inv_bl = 1.0f / static_cast<float>(bl), inv_lo = 1.0f / static_cast<float>(max(lo, 1));
+            auto range_of = [&](int bt) {
+                return bt < extra * bl ? small_div(bt, inv_bl) : extra + small_div(bt - extra * bl, inv_lo);
+            };
             for (int k = g; k < R; k += NG) {
                 const int fb = off[k] / K, nbk = off[k + 1] / K - fb;
                 const int gf = nbk > 0 ? range_of(fb) : 0, gl = nbk > 0 ? range_of(fb + nbk - 1) : 0;
