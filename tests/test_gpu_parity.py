@@ -610,3 +610,22 @@ def test_no_grad_inference_writes_no_route_record():
     assert not y_nog.requires_grad and y_grad.requires_grad
     assert torch.equal(y_nog, y_grad.detach())
     assert torch.equal(hip._last_indices, idx_grad) and torch.equal(hip._last_margins, mar_grad)
+
+
+def test_retain_graph_backward_twice():
+    """Two backward passes over one forward (retain_graph=True) through the
+    module: the second accumulates the same gradients again."""
+    ref, hip = make_pair(64, 32, 20, 5, seed=2, thr_std=0.2)
+    x = seeded((77, 64), 4)
+    g = seeded((77, 1, 32), 5)
+    x_hip = x.to(DEV).requires_grad_(True)
+    y = hip.train()(x_hip)
+    y.backward(g.to(DEV), retain_graph=True)
+    first = (x_hip.grad.clone(), hip.thresholds.grad.clone(), hip.lut.grad.clone())
+    y.backward(g.to(DEV))
+    torch.cuda.synchronize()
+    for a, total in zip(first, (x_hip.grad, hip.thresholds.grad, hip.lut.grad)):
+        assert torch.equal(total, a + a)
+    x_ref = x.clone().requires_grad_(True)
+    ref.train()(x_ref).backward(g)
+    assert rel_err(first[0], x_ref.grad) <= F32_TOL
