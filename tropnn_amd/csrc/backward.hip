@@ -187,9 +187,20 @@ __device__ __forceinline__ float reduce_scatter(const float (&d)[N], int j) {
     return v[0];
 }
 
+// Word k of the inverse anchor index as the feature walk stages it in LDS:
+// offsets [in_f + 1], entries [n_ent = 2 T C], then kEntries zeros, so that
+// the walk may read a whole batch of entries past a feature's last one.
+__device__ __forceinline__ int index_word(const int32_t *offs, const int32_t *ents, int in_f, int n_ent, int k) {
+    return k <= in_f ? offs[k] : (k - in_f - 1 < n_ent ? ents[k - in_f - 1] : 0);
+}
+
 // grad_x row of one item: thread f sums the item's signed gu slots gud[(t * C
 // + c)] named by feature f's entries of the inverse anchor index (staged in
-// LDS as offsets [in_f + 1] then entries), in entry order; side 1 subtracts.
+// LDS as index_word lays it out), in entry order; side 1 subtracts. A batch
+// reads its kEntries entries and slots unconditionally (entries past the
+// feature's last belong to later features or are the zero padding, so every
+// slot index is in range) and drops the extra ones with a select: straight-
+// line code instead of a branch around every load.
 __device__ __forceinline__ void feature_walk(const float *gud, const int *idx_s, int in_f, float *grad_x_row, int tid,
                                              int nthr) {
     const int *off_s = idx_s, *ent_s = idx_s + in_f + 1;
@@ -199,13 +210,15 @@ __device__ __forceinline__ void feature_walk(const float *gud, const int *idx_s,
         for (int eb = f0; eb < f1; eb += kEntries) {
             int en[kEntries];
 #pragma unroll
-            for (int q = 0; q < kEntries; ++q) en[q] = eb + q < f1 ? ent_s[eb + q] : 0;
+            for (int q = 0; q < kEntries; ++q) en[q] = ent_s[eb + q];
             float v[kEntries];
 #pragma unroll
-            for (int q = 0; q < kEntries; ++q) v[q] = eb + q < f1 ? gud[en[q] >> 1] : 0.f;
+            for (int q = 0; q < kEntries; ++q) v[q] = gud[en[q] >> 1];
 #pragma unroll
-            for (int q = 0; q < kEntries; ++q)
-                if (eb + q < f1) gx = (en[q] & 1) ? gx - v[q] : gx + v[q];
+            for (int q = 0; q < kEntries; ++q) {
+                const float sv = (en[q] & 1) ? -v[q] : v[q];  // gx + (-v) rounds as gx - v
+                gx = eb + q < f1 ? gx + sv : gx;
+            }
         }
         __builtin_nontemporal_store(gx, grad_x_row + f);
     }
@@ -230,8 +243,9 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void 
 
     // 0. the inverse anchor index (offsets, then entries) is staged in LDS
     //    for the feature walk; its first loads go out with the first block's
-    const int nidx = a.grad_x != nullptr ? a.in_f + 1 + 2 * a.tables * C : 0;
-    int *idx_s = reinterpret_cast<int *>(gud + a.tables * C);  // [in_f + 1 + 2 T C]
+    const int n_ent = 2 * a.tables * C;
+    const int nidx = a.grad_x != nullptr ? a.in_f + 1 + n_ent + kEntries : 0;
+    int *idx_s = reinterpret_cast<int *>(gud + a.tables * C);  // [in_f + 1 + 2 T C + kEntries]
     constexpr int kLoaded = item_wave_tables(static_cast<int>(sizeof(T)), N);  // tables with rows in flight
     const int ti = lane >> 2;  // lane l serves table l / 4 of a block
     // the first block's record of this lane, then this thread's index words,
@@ -243,7 +257,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void 
 #pragma unroll
         for (int q = 0; q < kIndexRegs; ++q) {
             const int k = tid + q * nthr;
-            iv[q] = k < nidx ? (k <= a.in_f ? a.index_offsets[k] : a.index_entries[k - a.in_f - 1]) : 0;
+            iv[q] = k < nidx ? index_word(a.index_offsets, a.index_entries, a.in_f, n_ent, k) : 0;
         }
 #pragma unroll
         for (int q = 0; q < kIndexRegs; ++q)
@@ -305,7 +319,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void 
     }
     if (a.grad_x == nullptr) return;
     for (int k = tid + kIndexRegs * nthr; k < nidx; k += nthr)
-        idx_s[k] = k <= a.in_f ? a.index_offsets[k] : a.index_entries[k - a.in_f - 1];
+        idx_s[k] = index_word(a.index_offsets, a.index_entries, a.in_f, n_ent, k);
     __syncthreads();
 
     // 4. one thread per input feature: its signed slots in entry order
@@ -335,10 +349,10 @@ __global__ __launch_bounds__(1024) void pairwise_bwd_full_kernel(ItemArgs a) {
     const int C = a.comps, R = a.rows;
     const int t0 = wave * a.per_wave;
     const int nt = max(0, min(a.tables, t0 + a.per_wave) - t0);
-    const int nidx = a.grad_x != nullptr ? a.in_f + 1 + 2 * a.tables * C : 0;
-    int *idx_s = reinterpret_cast<int *>(gud + a.tables * C);  // [in_f + 1 + 2 T C]
-    for (int k = tid; k < nidx; k += nthr)
-        idx_s[k] = k <= a.in_f ? a.index_offsets[k] : a.index_entries[k - a.in_f - 1];
+    const int n_ent = 2 * a.tables * C;
+    const int nidx = a.grad_x != nullptr ? a.in_f + 1 + n_ent + kEntries : 0;
+    int *idx_s = reinterpret_cast<int *>(gud + a.tables * C);  // [in_f + 1 + 2 T C + kEntries]
+    for (int k = tid; k < nidx; k += nthr) idx_s[k] = index_word(a.index_offsets, a.index_entries, a.in_f, n_ent, k);
 
     const __amdgpu_buffer_rsrc_t lut_rsrc = buffer_rsrc(a.lut, a.lut_bytes);
     const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.grad_out, a.g_bytes);
@@ -1104,9 +1118,10 @@ __global__ __launch_bounds__(kScatterThreads) void pairwise_bwd_scatter_kernel(S
     extern __shared__ __align__(16) unsigned char lds[];
     const int C = a.comps;
     float *gud = reinterpret_cast<float *>(lds);                     // [T * C]
-    int *idx_s = reinterpret_cast<int *>(gud + a.tables * C);         // [in_f + 1 + 2 T C]
+    int *idx_s = reinterpret_cast<int *>(gud + a.tables * C);         // [in_f + 1 + 2 T C + kEntries]
     const int b = xcd_block_unit(blockIdx.x, gridDim.x), tid = threadIdx.x;  // records of adjacent items share lines
-    const int nidx = a.in_f + 1 + 2 * a.tables * C;
+    const int n_ent = 2 * a.tables * C;
+    const int nidx = a.in_f + 1 + n_ent + kEntries;
     for (int t0 = 0; t0 < a.tables; t0 += kScatterThreads) {
         const int tt = t0 + tid;
         const uint64_t rr = tt < a.tables ? a.gurec[static_cast<size_t>(tt) * a.items + b] : 0ull;
@@ -1115,7 +1130,7 @@ __global__ __launch_bounds__(kScatterThreads) void pairwise_bwd_scatter_kernel(S
 #pragma unroll
         for (int q = 0; q < kScatterIndex; ++q) {
             const int k = kb + tid + q * kScatterThreads;
-            iv[q] = k < nidx ? (k <= a.in_f ? a.index_offsets[k] : a.index_entries[k - a.in_f - 1]) : 0;
+            iv[q] = k < nidx ? index_word(a.index_offsets, a.index_entries, a.in_f, n_ent, k) : 0;
         }
 #pragma unroll
         for (int q = 0; q < kScatterIndex; ++q)
@@ -1127,7 +1142,7 @@ __global__ __launch_bounds__(kScatterThreads) void pairwise_bwd_scatter_kernel(S
         }
     }
     for (int k = tid + kScatterIndex * kScatterThreads; k < nidx; k += kScatterThreads)
-        idx_s[k] = k <= a.in_f ? a.index_offsets[k] : a.index_entries[k - a.in_f - 1];
+        idx_s[k] = index_word(a.index_offsets, a.index_entries, a.in_f, n_ent, k);
     __syncthreads();
     feature_walk(gud, idx_s, a.in_f, a.grad_x + static_cast<size_t>(b) * a.in_f, tid, kScatterThreads);
 }
@@ -1280,7 +1295,7 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     p.item_per_wave = (d.tables + w - 1) / w;
     p.item_waves = (d.tables + p.item_per_wave - 1) / p.item_per_wave;
     p.item_threads = p.item_waves * kWave;
-    p.item_lds_bytes = (d.tables * d.comps + d.in_f + 1 + 2 * d.tables * d.comps) * 4;
+    p.item_lds_bytes = (d.tables * d.comps + d.in_f + 1 + 2 * d.tables * d.comps + kEntries) * 4;
     p.scatter_lds_bytes = p.item_lds_bytes;
 
     // fused path: the row group spans the row, lanes own whole V-column
