@@ -64,13 +64,15 @@ def algorithmic_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = 
         one f32 grad-row contribution per (item, table), grad_lut once,
         grad_thr;
       backward_scatter: x re-read (margins), grad_x, anchors + thresholds;
-    general backward:
-      backward_item: G, x re-read, codes, current + neighbour rows per
-        (item, table), grad_x, anchors + thresholds;
-      backward_sort: grad_thr (the code sort it also does moves no
-        algorithmic bytes);
-      backward_table: one f32 grad-row contribution per (item, table),
-        grad_lut once."""
+    general backward (min-margin STE):
+      backward_sort: nothing algorithmic (the code sort and G's chunk-major
+        copy are implementation choices);
+      backward_table: G, codes, current + neighbour rows per (item, table)
+        (served from the table's LUT chunk in LDS), one f32 grad-row
+        contribution per (item, table), grad_lut once;
+      backward_reduce: grad_thr (the partial dots it sums are an
+        implementation choice);
+      backward_scatter: x re-read (margins), grad_x, anchors + thresholds."""
     r = 1 << c
     fwd = 4 * b * i + 20 * t * c + e * b * t * o + 4 * b * o + b * t
     g_codes_rows = 4 * b * o + b * t + 2 * e * b * t * o
@@ -78,7 +80,8 @@ def algorithmic_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = 
     lut_rows = 4 * b * t * o + 4 * t * r * o
     if fused:
         return {"forward": fwd, "backward_fused": g_codes_rows + lut_rows + 4 * t * c, "backward_scatter": x_side}
-    return {"forward": fwd, "backward_item": g_codes_rows + x_side, "backward_sort": 4 * t * c, "backward_table": lut_rows}
+    return {"forward": fwd, "backward_sort": 0, "backward_table": g_codes_rows + lut_rows,
+            "backward_reduce": 4 * t * c, "backward_scatter": x_side}
 
 
 def fused_backward() -> bool:
@@ -434,7 +437,8 @@ def bench_c4(args, dev) -> dict:
     f32 LUT (2 GiB) gradients. A step takes tens of milliseconds, so plain
     eager module steps are timed (K steps after the warmup); each kernel's
     duration comes from events its own dispatch stamps, over the same steps.
-    The backward takes the general path (item, sort and row kernels)."""
+    The backward takes the general path (sort, row, reduce and scatter
+    kernels)."""
     import torch
 
     from tropnn_amd import PairwiseLinear
@@ -525,7 +529,7 @@ def bench_c4(args, dev) -> dict:
         "step_roofline_frac": round(total_algo / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "kernels": {
             n: {"avg_us": round(kern_us[n], 1), "algorithmic_bytes": algo[n],
-                "achieved_GBs": round(algo[n] / (kern_us[n] * 1e-6) / 1e9, 1)}
+                "achieved_GBs": round(algo[n] / (kern_us[n] * 1e-6) / 1e9, 1) if kern_us[n] > 0 else None}
             for n in names
         },
     }

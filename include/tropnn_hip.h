@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TROPNN_HIP_ABI_VERSION 6
+#define TROPNN_HIP_ABI_VERSION 7
 
 /* status codes */
 #define TROPNN_OK 0
@@ -182,14 +182,19 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
  * hipEvent_t handles to be recorded on the launch stream immediately before
  * and after the NEXT launch of one kernel:
  *   TROPNN_KERNEL_FORWARD           the fused route + gather + scale kernel
- *   TROPNN_KERNEL_BACKWARD_TABLE    the per-(table, column chunk) LUT-gradient kernel
- *   TROPNN_KERNEL_BACKWARD_ITEM     the per-item STE-dot / input-gradient kernel
- *   TROPNN_KERNEL_BACKWARD_SORT     the per-table code sort / threshold-gradient kernel between them
+ *   TROPNN_KERNEL_BACKWARD_TABLE    the per-(table, column chunk) LUT-gradient kernel (with the
+ *                                   min-margin STE: also each chunk's partial STE dots)
+ *   TROPNN_KERNEL_BACKWARD_ITEM     the per-item STE-dot / input-gradient kernel of the full STE
+ *   TROPNN_KERNEL_BACKWARD_SORT     the per-table code sort kernel before the row kernel
+ *                                   (full STE: also the threshold gradient)
+ *   TROPNN_KERNEL_BACKWARD_REDUCE   the per-table kernel after it (min-margin): partial dots ->
+ *                                   gu, threshold gradient, {gu, r} records
  *   TROPNN_KERNEL_BACKWARD_FUSED    the per-table LUT-gradient / STE-dot / threshold-gradient
  *                                   kernel of narrow rows (out_features a multiple of 4 up to 64
  *                                   or of 8 up to 256, one table's rows within 64 KB as f32)
- *   TROPNN_KERNEL_BACKWARD_SCATTER  the per-item input-gradient kernel that follows it
- * A backward launches either FUSED then SCATTER, or ITEM, SORT and TABLE.
+ *   TROPNN_KERNEL_BACKWARD_SCATTER  the per-item input-gradient kernel after FUSED or REDUCE
+ * A backward launches FUSED then SCATTER (narrow rows), or SORT, TABLE, REDUCE and
+ * SCATTER (other rows, min-margin STE), or ITEM, SORT and TABLE (other rows, full STE).
  * One-shot and process-global (not for concurrent use from several threads).
  * Passing NULL events disarms. Lets a benchmark time one kernel per step with
  * events on the exact stream the kernel runs on.
@@ -200,6 +205,7 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
 #define TROPNN_KERNEL_BACKWARD_FUSED 3
 #define TROPNN_KERNEL_BACKWARD_SCATTER 4
 #define TROPNN_KERNEL_BACKWARD_SORT 5
+#define TROPNN_KERNEL_BACKWARD_REDUCE 6
 int tropnn_hip_arm_kernel_events(int kernel, void *start_event, void *stop_event);
 
 #ifdef __cplusplus

@@ -269,6 +269,9 @@ def test_train_parity(i, o, t, c, b, thr_std):
         (128, 256, 40, 5, 64, False, "fast_sigmoid_odd", "f32"),  # 4 columns per lane
         (128, 128, 136, 6, 256, False, "izhikevich", "f16"),
         (100, 1000, 12, 7, 40, False, "fast_sigmoid_odd", "f16"),  # 8 f16 columns per lane
+        (100, 1000, 12, 7, 300, True, "fast_sigmoid_odd", "f16"),  # general path, 16 column chunks
+        (64, 300, 20, 8, 2100, True, "izhikevich", "f32"),  # general path, 5 chunks, 3 sort tiles
+        (40, 6, 50, 3, 500, True, "izhikevich", "f32"),  # general path, 4-lane row groups
     ],
 )
 def test_train_parity_ste_variants(i, o, t, c, b, min_margin, surrogate, lut_dtype):

@@ -26,7 +26,7 @@ from typing import Any
 import torch
 from torch import Tensor
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 LUT_F32, LUT_F16 = 0, 1
 SURROGATE_IDS = {"fast_sigmoid_odd": 0, "izhikevich": 1}
 STE_MIN_MARGIN, STE_FULL = 0, 1
@@ -63,6 +63,7 @@ KERNEL_IDS = {
     "backward_fused": 3,
     "backward_scatter": 4,
     "backward_sort": 5,
+    "backward_reduce": 6,
 }
 
 

@@ -82,7 +82,7 @@ int check_forward_ptrs(const tropnn::Dims &d, const tropnn::ForwardPlan &p, cons
 }
 
 std::mutex g_events_mu;
-tropnn::ArmedEvents g_armed[TROPNN_KERNEL_BACKWARD_SORT + 1];
+tropnn::ArmedEvents g_armed[TROPNN_KERNEL_BACKWARD_REDUCE + 1];
 
 }  // namespace
 
@@ -106,7 +106,7 @@ void arm_events(int kernel, hipEvent_t start, hipEvent_t stop) {
 extern "C" {
 
 int tropnn_hip_arm_kernel_events(int kernel, void *start_event, void *stop_event) {
-    if (kernel < TROPNN_KERNEL_FORWARD || kernel > TROPNN_KERNEL_BACKWARD_SORT)
+    if (kernel < TROPNN_KERNEL_FORWARD || kernel > TROPNN_KERNEL_BACKWARD_REDUCE)
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "unknown kernel id %d", kernel);
     if ((start_event == nullptr) != (stop_event == nullptr))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "arm both events or neither");
@@ -243,8 +243,9 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
     if (margins && misaligned(margins, 4))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "margins must be 4-byte aligned");
     const size_t esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
-    // fused path: LUT chunks of 4 elements, 16-byte grad rows and LUT-grad rows
-    const size_t lut_align = p.fused ? 4 * esize : p.item_vec * esize;
+    // fused path: LUT chunks of 4 elements, 16-byte grad rows and LUT-grad rows;
+    // general path: the item kernel's and the row kernel's pieces
+    const size_t lut_align = p.fused ? 4 * esize : static_cast<size_t>(p.rows_vec > p.item_vec ? p.rows_vec : p.item_vec) * esize;
     const size_t gvec = p.fused ? 4 : static_cast<size_t>(p.rows_vec > p.item_vec ? p.rows_vec : p.item_vec);
     const size_t lut_grad_vec = p.fused ? 4 : static_cast<size_t>(p.rows_vec);
     if (misaligned(lut, lut_align) || misaligned(grad_output, gvec * 4) ||

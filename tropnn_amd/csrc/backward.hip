@@ -12,7 +12,8 @@
 // fixed summation orders make every gradient deterministic).
 //
 // Narrow rows (O a multiple of 4 up to 64, or of 8 up to 256, one table's LUT
-// rows within 64 KB as f32; c2 is one) take the fused path, two launches:
+// rows within 64 KB as f32; c2 is one) with the min-margin STE take the fused
+// path, two launches:
 //  (F) fused kernel, one workgroup per table. The table's LUT rows are staged
 //      in LDS as f32; each tile of 1024 items is counting-sorted by code (one
 //      ballot per code bit, per-wave counts written by each code's first item,
@@ -31,36 +32,36 @@
 //      (table, comparison) slots and walks the inverse anchor index into
 //      grad_latent, as the item kernel's last phase does.
 //
-// Other shapes take the general path, three launches:
-//  (1) item kernel, one workgroup per item, shaped like the forward: each wave
-//      takes up to 16 consecutive tables. A lane holds the record of table
-//      lane / 4; the wave moves each table's code and min-margin comparison to
-//      scalar registers and loads the two LUT rows L[code], L[nb] (nb = code
-//      with the min-margin bit flipped) with scalar row offsets, 64 lanes
-//      spanning the row. Each lane forms its part of the 16 STE dots
-//      sum_o G[b,o] (L[nb,o] - L[code,o]); one reduce-scatter over the wave
-//      (DPP inside rows, shuffles across them) completes all 16 at once, lane
-//      4i holding table i's dot. That lane applies scale and surrogate
-//      derivative, stores gu[t][b] and expands it into the item's LDS slots
-//      (one per (table, comparison), zero except at the min-margin one). Then
-//      one thread per input feature sums the signed slots named by the
-//      feature's entries of the inverse anchor index, in entry order, and
-//      writes grad_latent.
-//  (2) sort kernel, one workgroup per table: the stable counting sort of the
+// Other shapes take the general path. With the min-margin STE, four launches:
+//  (1) sort kernel, one workgroup per table: the stable counting sort of the
 //      table's items by LUT row code (C wave ballots per tile of 1024 items
 //      give each item its rank among equal codes of its wave; per-wave counts
 //      and a DPP scan give row starts), written once to the workspace as the
-//      items' grad-row offsets with every row padded to whole batches of 8
-//      slots, plus each batch's row; the table's share of a chunk-major copy
-//      of G (64-column chunks, each one contiguous block); and the table's
-//      threshold gradient from gu.
-//  (3) row kernel, one workgroup per (table, 64-column chunk): row groups of
+//      items' grad-row offsets (with the item's min-margin comparison in the
+//      low bits) with every row padded to whole batches of 8 slots, plus each
+//      batch's row; and the table's share of a chunk-major copy of G
+//      (64-column chunks, each one contiguous block).
+//  (2) row kernel, one workgroup per (table, 64-column chunk): row groups of
 //      S lanes (V columns each) walk balanced contiguous ranges of the sorted
 //      batches, eight grad-row loads in flight per batch (padding slots read
 //      out of range: zeros), summing each row in registers; a row inside one
 //      range is scaled and written there, a row crossing ranges is combined
 //      from the ranges' LDS slots in range order, and empty rows are written
-//      as zeros. The sort is done once per table instead of once per chunk.
+//      as zeros. The same grad-row pieces give each item's partial STE dot
+//      over the chunk against L[nb] - L[code] from the table's LUT chunk in
+//      LDS; one reduce-scatter per batch completes the batch's partial dots,
+//      stored per (table, chunk, item). So the STE reads every LUT row once
+//      per (table, chunk), not twice per (item, table).
+//  (3) reduce kernel, one workgroup per table: each item's partial dots summed
+//      in chunk order, gu = dot * scale * surrogate'(u), the {gu, r} record
+//      and the threshold gradient.
+//  (4) the scatter kernel above: the input gradient.
+// With the full STE (every comparison carries a dot), three launches: the
+// full-STE item kernel (one workgroup per item, shaped like the forward: each
+// wave takes a block of tables, their current and C neighbour rows in flight,
+// one reduce-scatter completing the block's dots; gu per comparison, then the
+// feature walk into grad_latent), the sort kernel (which then also sums the
+// threshold gradient from gu) and the row kernel without dots.
 //  A third, tiny kernel builds the inverse anchor index; callers rebuild it
 //  only when the anchors change.
 #include "device.hpp"
@@ -74,9 +75,7 @@ constexpr int kRowsThreads = 1024;  // threads of a row-kernel workgroup
 constexpr int kRowsBatch = 8;       // sorted slots per row-kernel batch; rows are padded to whole batches
 constexpr int kRowsChunk = 64;     // columns of a row-kernel workgroup (at most): 2 MB of G at c4, within an L2
 constexpr uint32_t kSlotPad = 0x80000000u;  // grad-row offset of a padding slot: past any grad buffer (<= 2 GiB)
-constexpr int kItemTables = 16;    // tables per item-kernel wave (one reduce-scatter)
 constexpr int kEntries = 16;       // index entries a walker reads per batch
-constexpr int kIndexRegs = 4;      // index words per thread loaded with the first record
 
 struct ItemArgs {
     const float *grad_out;
@@ -114,11 +113,30 @@ struct RowsArgs {
     const uint32_t *slot_off;
     const int32_t *row_start;
     const int32_t *batch_row;
-    float *grad_lut;
+    float *grad_lut;         // or null (dots only)
     float scale;
     uint32_t gc_bytes;     // bytes of the chunk-major copy
     uint32_t chunk_bytes;  // B * P * 4: one chunk of the copy
     int out_f, rows, tables, slots, part_off;
+    // partial STE dots (min-margin): the table's LUT chunk staged in LDS
+    const void *lut;       // [T][R][O] f32 or f16
+    uint32_t lut_bytes;
+    float *pdot;           // [T][chunks][slots] per sorted slot: sum over the chunk's columns of G (L[nb] - L[code]), unscaled
+    int items, chunks, lut_off;
+};
+
+// Reduce kernel (general path, min-margin), one workgroup per table.
+struct ReduceArgs {
+    const float *pdot;     // [T][chunks][slots]
+    const uint32_t *slot_off;  // [T][slots] the sort kernel's slots: item offset | r, or kSlotPad
+    const int32_t *row_start;  // [T][R + 1]: [R] is the table's slot count
+    const uint64_t *rec;   // [T][B] route records
+    uint64_t *gurec;       // [T][B] {gu bits, r} for the scatter kernel, or null
+    float *grad_thr;       // or null
+    float scale;
+    int surrogate;
+    int items, chunks, comps, rows, slots;
+    int item_shift;        // slot offset >> item_shift = item (offsets are item * P * 4)
 };
 
 __device__ __forceinline__ int rec_code(uint64_t r) { return static_cast<int>((r >> 32) & 0xffffu); }
@@ -222,108 +240,6 @@ __device__ __forceinline__ void feature_walk(const float *gud, const int *idx_s,
         }
         __builtin_nontemporal_store(gx, grad_x_row + f);
     }
-}
-
-// ------------------------------------------------------------------ item kernel
-
-// At most 80 VGPRs (6 waves per SIMD): two workgroups of up to 9 waves then
-// share a CU.
-template <typename T, int N>
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void pairwise_bwd_item_kernel(ItemArgs a) {
-    extern __shared__ __align__(16) unsigned char lds[];
-    float *gud = reinterpret_cast<float *>(lds);  // [T * C] this item's gu slots
-
-    const int tid = threadIdx.x, nthr = blockDim.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int b = xcd_block_unit(blockIdx.x, gridDim.x);  // [T][B] records of adjacent items share lines
-    const int C = a.comps, R = a.rows;
-    const int t0 = wave * a.per_wave;
-    const int nt = max(0, min(a.tables, t0 + a.per_wave) - t0);
-
-    // 0. the inverse anchor index (offsets, then entries) is staged in LDS
-    //    for the feature walk; its first loads go out with the first block's
-    const int n_ent = 2 * a.tables * C;
-    const int nidx = a.grad_x != nullptr ? a.in_f + 1 + n_ent + kEntries : 0;
-    int *idx_s = reinterpret_cast<int *>(gud + a.tables * C);  // [in_f + 1 + 2 T C + kEntries]
-    constexpr int kLoaded = item_wave_tables(static_cast<int>(sizeof(T)), N);  // tables with rows in flight
-    const int ti = lane >> 2;  // lane l serves table l / 4 of a block
-    // the first block's record of this lane, then this thread's index words,
-    // which go to LDS as soon as they arrive (the dots need the record first
-    // anyway)
-    uint64_t rr_next = ti < min(kLoaded, nt) ? a.rec[static_cast<size_t>(t0 + ti) * a.items + b] : 0ull;
-    {
-        int iv[kIndexRegs];
-#pragma unroll
-        for (int q = 0; q < kIndexRegs; ++q) {
-            const int k = tid + q * nthr;
-            iv[q] = k < nidx ? index_word(a.index_offsets, a.index_entries, a.in_f, n_ent, k) : 0;
-        }
-#pragma unroll
-        for (int q = 0; q < kIndexRegs; ++q)
-            if (tid + q * nthr < nidx) idx_s[tid + q * nthr] = iv[q];
-    }
-
-    const __amdgpu_buffer_rsrc_t lut_rsrc = buffer_rsrc(a.lut, a.lut_bytes);
-    const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.grad_out, a.g_bytes);
-    for (int tb = t0; tb < t0 + nt; tb += kLoaded) {  // blocks of kLoaded tables
-        const int ntb = min(kLoaded, t0 + nt - tb);
-        // 1. this lane's table record
-        const bool has = ti < ntb;
-        const uint64_t rr = rr_next;
-        const int code_v = rec_code(rr) & (R - 1);
-        const int r_v = rec_r(rr) & 7;
-
-        // 2. per table: both LUT rows at scalar row offsets (all in flight),
-        //    then this lane's part of each dot against the item's grad row
-        float d[kItemTables];
-#pragma unroll
-        for (int i = 0; i < kItemTables; ++i) d[i] = 0.f;
-        for (int ct = 0; ct < a.o_tiles; ++ct) {
-            const int col = ct * (kWave * N) + lane * N;
-            const bool col_ok = col < a.out_f;
-            float g[N];
-            buffer_row<float, N>(g_rsrc, col_ok ? static_cast<uint32_t>(b * a.out_f + col) * 4u : kOutOfRange, 0, g);
-            const uint32_t voff = col_ok ? static_cast<uint32_t>(col) * static_cast<uint32_t>(sizeof(T)) : kOutOfRange;
-            // all kLoaded tables' rows in flight at once (sized to 80 VGPRs)
-            {
-                constexpr int kBatch = kLoaded;
-                constexpr int i0 = 0;
-                float lk[kBatch][N], ln[kBatch][N];
-#pragma unroll
-                for (int i = 0; i < kBatch; ++i) {
-                    const bool live = i0 + i < ntb;
-                    const int code = __builtin_amdgcn_readlane(code_v, 4 * (i0 + i));
-                    const int nb = (code ^ (1 << __builtin_amdgcn_readlane(r_v, 4 * (i0 + i)))) & (R - 1);
-                    const int trow = (tb + i0 + i) * a.table_bytes;
-                    buffer_row<T, N>(lut_rsrc, live ? voff : kOutOfRange, live ? trow + code * a.row_bytes : 0, lk[i]);
-                    buffer_row<T, N>(lut_rsrc, live ? voff : kOutOfRange, live ? trow + nb * a.row_bytes : 0, ln[i]);
-                }
-#pragma unroll
-                for (int i = 0; i < kBatch; ++i)
-#pragma unroll
-                    for (int e = 0; e < N; ++e) d[i0 + i] += g[e] * (ln[i][e] - lk[i][e]);
-            }
-        }
-
-        // 3. lane 4i completes table i's dot: gu, stored and expanded into slots
-        const float dot = reduce_scatter<kWave, kItemTables>(d, lane) * a.scale;
-        if (has && (lane & 3) == 0) {
-            const float gu = dot * surrogate_grad(rec_u(rr), a.surrogate);
-            if (a.gu != nullptr) a.gu[static_cast<size_t>(tb + ti) * a.items + b] = gu;
-            float *slot = gud + (tb + ti) * C;
-            for (int c = 0; c < C; ++c) slot[c] = c == r_v ? gu : 0.f;
-        }
-        const int tn = tb + kLoaded;  // next block's record
-        if (tn < t0 + nt) rr_next = ti < min(kLoaded, t0 + nt - tn) ? a.rec[static_cast<size_t>(tn + ti) * a.items + b] : 0ull;
-    }
-    if (a.grad_x == nullptr) return;
-    for (int k = tid + kIndexRegs * nthr; k < nidx; k += nthr)
-        idx_s[k] = index_word(a.index_offsets, a.index_entries, a.in_f, n_ent, k);
-    __syncthreads();
-
-    // 4. one thread per input feature: its signed slots in entry order
-    feature_walk(gud, idx_s, a.in_f, a.grad_x + static_cast<size_t>(b) * a.in_f, tid, nthr);
 }
 
 // ------------------------------------------------------------------ full-STE item kernel
@@ -469,8 +385,9 @@ __device__ __forceinline__ int wave_code_rank(int code, bool valid, int R, int C
 // starts are the counts rounded up to whole batches of kRowsBatch slots,
 // exclusively scanned. Pass 2 places every item at its row's next free slot
 // (tiles, waves and lanes in order, so item order is kept inside a row) as
-// its byte offset b * P * 4 inside a chunk of the copy; padding slots get
-// kSlotPad.
+// its byte offset b * P * 4 inside a chunk of the copy, with the item's
+// min-margin comparison r in the offset's low 3 bits (P * 4 >= 16); padding
+// slots get kSlotPad.
 __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArgs a) {
     constexpr int kWaves = kSortThreads / kWave;
     constexpr int K = kRowsBatch;
@@ -545,7 +462,8 @@ __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArg
         for (int tile0 = 0; tile0 < a.items; tile0 += kSortThreads) {
             const int b = tile0 + tid;
             const bool valid = b < a.items;
-            const int code = rec_code(valid ? rec_t[b] : 0ull) & (R - 1);
+            const uint64_t rr = valid ? rec_t[b] : 0ull;
+            const int code = rec_code(rr) & (R - 1);
             const int rank = wave_code_rank(code, valid, R, C, cnt + wave * R, lane);
             __syncthreads();
             if (tid < R) {
@@ -558,7 +476,9 @@ __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArg
                 base[tid] = run;
             }
             __syncthreads();
-            if (valid) so[cnt[wave * R + code] + rank] = static_cast<uint32_t>(b) * static_cast<uint32_t>(a.chunk_cols) * 4u;
+            if (valid)
+                so[cnt[wave * R + code] + rank] =
+                    (static_cast<uint32_t>(b) * static_cast<uint32_t>(a.chunk_cols) * 4u) | static_cast<uint32_t>(rec_r(rr) & 7);
             __syncthreads();  // the next tile rewrites the counts
         }
 
@@ -599,7 +519,16 @@ __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArg
 
 // Row kernel: LUT gradient of table t over columns [chunk * S * V, + S * V),
 // reading the chunk-major copy of G (an item's piece of the chunk at
-// slot offset + chunk * B * P * 4).
+// slot offset + chunk * B * P * 4; the offset's low 3 bits carry the item's
+// min-margin comparison r). With DOTS the workgroup also stages the table's
+// LUT chunk in LDS as f32 and, from the same grad-row pieces, forms each
+// item's partial STE dot over the chunk, sum G (L[code ^ 2^r] - L[code]):
+// the current row L[code] stays in registers for the row, the neighbour rows
+// come from LDS, one reduce-scatter per batch completes the batch's dots, and
+// the lanes holding them store them at their sorted slots,
+// pdot[t][chunk][slot] (a batch's dots are contiguous). So the LUT rows of
+// the STE dots are read once per (table, chunk) instead of once per (item,
+// table).
 // The sorted slots form batches of kRowsBatch, each inside one row; the
 // batches are dealt to row groups (S lanes x V columns) as contiguous ranges
 // of lo or lo + 1 batches, the longer ones first. Per batch a group loads its
@@ -610,14 +539,16 @@ __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArg
 // row crossing the range's start (end) leaves its sum in the group's slot 0
 // (1), and a combine step adds the pieces in range order and writes the
 // row. Empty rows are written as zeros, so grad_lut is fully overwritten.
-template <int V, int S>
+template <typename T, int V, int S, bool DOTS>
 __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArgs a) {
     constexpr int NG = kRowsThreads / S;  // row groups
     constexpr int K = kRowsBatch;
     constexpr int P = S * V;  // columns of the chunk
+    constexpr int KR = K <= S ? K : S;  // dots per reduce-scatter
     extern __shared__ __align__(16) unsigned char lds[];
     int *rs = reinterpret_cast<int *>(lds);                       // [R + 1] row starts (slots)
     float *part = reinterpret_cast<float *>(lds + a.part_off);    // [groups][2][P] split rows
+    float *lut_s = reinterpret_cast<float *>(lds + a.lut_off);    // DOTS: [R][P] the table's LUT chunk
     // unit = chunk * T + table, each XCD taking one contiguous block of units:
     // an XCD walks its chunks one at a time over every table, so the chunk's
     // slice of G is read into its L2 once
@@ -634,8 +565,22 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
     const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.g_chunked, a.gc_bytes);
     const uint32_t *so = a.slot_off + static_cast<size_t>(t) * a.slots;
     const int32_t *br = a.batch_row + static_cast<size_t>(t) * (a.slots / K);
-    float *gl = a.grad_lut + static_cast<size_t>(t) * R * O;
+    float *gl = a.grad_lut != nullptr ? a.grad_lut + static_cast<size_t>(t) * R * O : nullptr;
     for (int k = tid; k <= R; k += kRowsThreads) rs[k] = a.row_start[static_cast<size_t>(t) * (R + 1) + k];
+    if constexpr (DOTS) {
+        // the LUT chunk: R rows of P columns (pieces of V, columns past O zero)
+        const __amdgpu_buffer_rsrc_t lut_rsrc = buffer_rsrc(a.lut, a.lut_bytes);
+        for (int q = tid; q < R * S; q += kRowsThreads) {
+            const int row = q / S, pc = q - row * S, c0 = chunk * P + pc * V;
+            float w[V];
+            buffer_row<T, V>(lut_rsrc,
+                             c0 < O ? static_cast<uint32_t>((static_cast<size_t>(t) * R + row) * O + c0) * sizeof(T)
+                                    : kOutOfRange,
+                             0, w);
+#pragma unroll
+            for (int e = 0; e < V; ++e) lut_s[row * P + pc * V + e] = w[e];
+        }
+    }
     __syncthreads();
 
     const int nb_all = rs[R] / K;
@@ -643,9 +588,12 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
     const int b_begin = g * lo + min(g, extra), b_end = b_begin + lo + (g < extra ? 1 : 0);
     int cur = -1;  // row being summed
     float acc[V];
+    float lkv[V];  // DOTS: L[cur] over this lane's columns
 #pragma unroll
-    for (int e = 0; e < V; ++e) acc[e] = 0.f;
+    for (int e = 0; e < V; ++e) acc[e] = lkv[e] = 0.f;
+    float *pd = DOTS ? a.pdot + (static_cast<size_t>(t) * a.chunks + chunk) * a.slots : nullptr;
     auto finish = [&](int k) {  // row k's sum over this range
+        if (gl == nullptr) return;
         const int fb = rs[k] / K, lb = rs[k + 1] / K - 1;
         if (fb >= b_begin && lb < b_end) {
             if (col_ok) {
@@ -684,20 +632,49 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
     for (int i = 0; __ballot(b_begin + i < b_end) != 0; ++i) {  // wave-uniform trip count
         const int bt = b_begin + i;
         const int k = rown;
+        uint32_t off[K];
+#pragma unroll
+        for (int u = 0; u < K; ++u) off[u] = offn[u];
         float gv[K][V];
 #pragma unroll
-        for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, (offn[u] + gcol) | coldead, 0, gv[u]);
+        for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, ((off[u] & ~7u) + gcol) | coldead, 0, gv[u]);
         meta(bt + 1, offn, rown);  // the next batch's offsets, while these rows arrive
         if (bt < b_end && k != cur) {
             if (cur >= 0) finish(cur);
             cur = k;
 #pragma unroll
             for (int e = 0; e < V; ++e) acc[e] = 0.f;
+            if constexpr (DOTS) {
+#pragma unroll
+                for (int e = 0; e < V; ++e) lkv[e] = lut_s[k * P + j * V + e];
+            }
         }
 #pragma unroll
         for (int u = 0; u < K; ++u)
 #pragma unroll
             for (int e = 0; e < V; ++e) acc[e] += gv[u][e];
+        if constexpr (DOTS) {
+            // a group past its range has cur's row (or row 0) and reads zeros
+            const int kk = bt < b_end ? k : max(cur, 0);
+            float d[K];
+#pragma unroll
+            for (int u = 0; u < K; ++u) {
+                const int nb = (kk ^ (1 << (off[u] & 7u))) & (R - 1);  // the mask keeps a corrupt record in range
+                float sd = 0.f;
+#pragma unroll
+                for (int e = 0; e < V; ++e) sd += gv[u][e] * (lut_s[nb * P + j * V + e] - lkv[e]);
+                d[u] = sd;
+            }
+#pragma unroll
+            for (int h = 0; h < K / KR; ++h) {
+                float dh[KR];
+#pragma unroll
+                for (int q = 0; q < KR; ++q) dh[q] = d[h * KR + q];
+                const float dot = reduce_scatter<S, KR>(dh, j);
+                const int q = (j / (S / KR)) & (KR - 1);  // the slot whose dot this lane holds
+                if (j % (S / KR) == 0 && bt < b_end) pd[bt * K + h * KR + q] = dot;
+            }
+        }
     }
     if (cur >= 0) finish(cur);
     __syncthreads();
@@ -708,6 +685,7 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
     const int bl = lo + 1;
     const float inv_bl = 1.0f / static_cast<float>(bl), inv_lo = 1.0f / static_cast<float>(max(lo, 1));
     auto range_of = [&](int bt) { return bt < extra * bl ? small_div(bt, inv_bl) : extra + small_div(bt - extra * bl, inv_lo); };
+    if (gl == nullptr) return;
     for (int k = g; k < R; k += NG) {
         const int fb = rs[k] / K, nbk = rs[k + 1] / K - fb;
         vec_t<float, V> w = 0.f;
@@ -722,6 +700,68 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
 #pragma unroll
             for (int e = 0; e < V; ++e) y[e] = w[e] * a.scale;
             store_f32_nt<V>(gl + static_cast<size_t>(k) * O + col, y);
+        }
+    }
+}
+
+// Reduce kernel (general path, min-margin): one workgroup per table, one
+// thread per sorted slot of a tile of 1024 slots. A slot's STE dot is the
+// sum of its chunks' partial dots in chunk order (contiguous reads across the
+// threads); gu = dot * scale * surrogate'(u) with u from the slot item's
+// route record. It stores the {gu, r} record for the scatter kernel and sums
+// the threshold gradient, -gu at the item's min-margin comparison (a fixed
+// tree per wave, waves in order, tiles in order: slots in sorted order).
+// Padding slots carry no gu.
+constexpr int kReduceThreads = 1024;
+
+__global__ __launch_bounds__(kReduceThreads) void pairwise_bwd_reduce_kernel(ReduceArgs a) {
+    constexpr int kWaves = kReduceThreads / kWave;
+    __shared__ float tp[kWaves * 8];
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint64_t *rec_t = a.rec + static_cast<size_t>(t) * a.items;
+    const uint32_t *so = a.slot_off + static_cast<size_t>(t) * a.slots;
+    const float *pd = a.pdot + static_cast<size_t>(t) * a.chunks * a.slots;
+    const int n_slots = a.row_start[static_cast<size_t>(t) * (a.rows + 1) + a.rows];
+    if (lane < 8) tp[wave * 8 + lane] = 0.f;  // each wave its own slots
+    for (int q0 = 0; q0 < n_slots; q0 += kReduceThreads) {
+        const int q = q0 + tid;
+        const uint32_t off = q < n_slots ? so[q] : kSlotPad;
+        const bool live = off != kSlotPad;
+        const int b = static_cast<int>(off >> a.item_shift);
+        const uint64_t rr = live ? rec_t[b] : 0ull;
+        float dot = 0.f;
+        if (live) {
+            constexpr int kU = 8;  // partial dots in flight
+            int c = 0;
+            for (; c + kU <= a.chunks; c += kU) {
+                float v[kU];
+#pragma unroll
+                for (int u = 0; u < kU; ++u) v[u] = pd[static_cast<size_t>(c + u) * a.slots + q];
+#pragma unroll
+                for (int u = 0; u < kU; ++u) dot += v[u];
+            }
+            for (; c < a.chunks; ++c) dot += pd[static_cast<size_t>(c) * a.slots + q];
+        }
+        const int r = static_cast<int>(off & 7u);
+        const float gu = live ? dot * a.scale * surrogate_grad(rec_u(rr), a.surrogate) : 0.f;
+        if (live && a.gurec != nullptr)
+            a.gurec[static_cast<size_t>(t) * a.items + b] =
+                static_cast<uint64_t>(__builtin_bit_cast(uint32_t, gu)) | (static_cast<uint64_t>(r) << 32);
+        if (a.grad_thr != nullptr) {
+            float tv[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) tv[c] = live && r == c ? -gu : 0.f;
+            const float sum = reduce_scatter<kWave, 8>(tv, lane);  // lane 8c: the wave's sum for comparison c
+            if ((lane & 7) == 0) tp[wave * 8 + (lane >> 3)] += sum;
+        }
+    }
+    if (a.grad_thr != nullptr) {
+        __syncthreads();
+        if (tid < a.comps) {
+            float sum = tp[tid];
+            for (int w = 1; w < kWaves; ++w) sum += tp[w * 8 + tid];
+            a.grad_thr[t * a.comps + tid] = sum;
         }
     }
 }
@@ -1184,37 +1224,47 @@ hipError_t allow_lds(K kernel, int bytes) {
     return e;
 }
 
-template <int V, int S>
+template <typename T, int V, int S, bool DOTS>
 hipError_t launch_rows_vs(const RowsArgs &args, const BackwardPlan &p, int tables, hipStream_t stream) {
-    return launch_kernel(TROPNN_KERNEL_BACKWARD_TABLE, pairwise_bwd_rows_kernel<V, S>, dim3(tables * p.rows_chunks),
-                         dim3(kRowsThreads), p.rows_lds_bytes, stream, args);
+    auto kernel = pairwise_bwd_rows_kernel<T, V, S, DOTS>;
+    const int lds = DOTS ? p.rows_lds_dots_bytes : p.rows_lds_bytes;
+    if (hipError_t e = allow_lds(kernel, lds); e != hipSuccess) return e;
+    return launch_kernel(TROPNN_KERNEL_BACKWARD_TABLE, kernel, dim3(tables * p.rows_chunks), dim3(kRowsThreads), lds,
+                         stream, args);
 }
 
-template <int V>
+template <typename T, int V, bool DOTS>
 hipError_t launch_rows_v(const RowsArgs &args, const BackwardPlan &p, int tables, hipStream_t stream) {
     switch (p.rows_slices) {
-        case 64: return launch_rows_vs<V, 64>(args, p, tables, stream);
-        case 32: return launch_rows_vs<V, 32>(args, p, tables, stream);
-        case 16: return launch_rows_vs<V, 16>(args, p, tables, stream);
-        case 8: return launch_rows_vs<V, 8>(args, p, tables, stream);
-        default: return launch_rows_vs<V, 4>(args, p, tables, stream);
+        case 64: return launch_rows_vs<T, V, 64, DOTS>(args, p, tables, stream);
+        case 32: return launch_rows_vs<T, V, 32, DOTS>(args, p, tables, stream);
+        case 16: return launch_rows_vs<T, V, 16, DOTS>(args, p, tables, stream);
+        case 8: return launch_rows_vs<T, V, 8, DOTS>(args, p, tables, stream);
+        default: return launch_rows_vs<T, V, 4, DOTS>(args, p, tables, stream);
     }
 }
 
-hipError_t launch_rows(const RowsArgs &args, const BackwardPlan &p, int tables, hipStream_t stream) {
+template <typename T, bool DOTS>
+hipError_t launch_rows_t(const RowsArgs &args, const BackwardPlan &p, int tables, hipStream_t stream) {
     switch (p.rows_vec) {
-        case 4: return launch_rows_v<4>(args, p, tables, stream);
-        case 2: return launch_rows_v<2>(args, p, tables, stream);
-        default: return launch_rows_v<1>(args, p, tables, stream);
+        case 4: return launch_rows_v<T, 4, DOTS>(args, p, tables, stream);
+        case 2: return launch_rows_v<T, 2, DOTS>(args, p, tables, stream);
+        default: return launch_rows_v<T, 1, DOTS>(args, p, tables, stream);
     }
+}
+
+// dots: partial STE dots as well (min-margin); the LUT's element type only
+// matters then
+hipError_t launch_rows(const RowsArgs &args, const BackwardPlan &p, int tables, int lut_dtype, bool dots,
+                       hipStream_t stream) {
+    if (!dots) return launch_rows_t<float, false>(args, p, tables, stream);
+    return lut_dtype == TROPNN_LUT_F16 ? launch_rows_t<_Float16, true>(args, p, tables, stream)
+                                       : launch_rows_t<float, true>(args, p, tables, stream);
 }
 
 template <typename T, int N>
 hipError_t launch_item_typed(const ItemArgs &args, const BackwardPlan &p, hipStream_t stream) {
-    if (p.full)
-        return launch_kernel(TROPNN_KERNEL_BACKWARD_ITEM, pairwise_bwd_full_kernel<T, N>, dim3(args.items),
-                             dim3(p.item_threads), p.item_lds_bytes, stream, args);
-    return launch_kernel(TROPNN_KERNEL_BACKWARD_ITEM, pairwise_bwd_item_kernel<T, N>, dim3(args.items),
+    return launch_kernel(TROPNN_KERNEL_BACKWARD_ITEM, pairwise_bwd_full_kernel<T, N>, dim3(args.items),
                          dim3(p.item_threads), p.item_lds_bytes, stream, args);
 }
 
@@ -1256,6 +1306,21 @@ hipError_t launch_anchor_index(const int64_t *anchors, int in_f, int tables, int
     return hipGetLastError();
 }
 
+hipError_t launch_scatter(const uint64_t *gurec, const int32_t *index_offsets, const int32_t *index_entries,
+                          float *grad_x, const Dims &d, const BackwardPlan &p, hipStream_t stream) {
+    ScatterArgs s{};
+    s.gurec = gurec;
+    s.index_offsets = index_offsets;
+    s.index_entries = index_entries;
+    s.grad_x = grad_x;
+    s.items = d.items;
+    s.in_f = d.in_f;
+    s.tables = d.tables;
+    s.comps = d.comps;
+    return launch_kernel(TROPNN_KERNEL_BACKWARD_SCATTER, pairwise_bwd_scatter_kernel, dim3(d.items),
+                         dim3(kScatterThreads), p.scatter_lds_bytes, stream, s);
+}
+
 BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     BackwardPlan p{};
     p.full = ste_mode == TROPNN_STE_FULL;
@@ -1273,6 +1338,8 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     p.rows_chunks = (d.out_f + rows_chunk - 1) / rows_chunk;
     p.rows_part_off = ((d.rows + 1) * 4 + 15) & ~15;
     p.rows_lds_bytes = p.rows_part_off + (kRowsThreads / p.rows_slices) * 2 * rows_chunk * 4;
+    p.rows_lut_off = (p.rows_lds_bytes + 15) & ~15;  // with dots: the LUT chunk [R][P] f32
+    p.rows_lds_dots_bytes = p.rows_lut_off + d.rows * rows_chunk * 4;
     p.sort_lds_bytes = ((kSortThreads / kWave) * d.rows + d.rows + kSortThreads / kWave) * 4 + (kSortThreads / kWave) * 8 * 4;
     // the sorted slots of a table: its items plus up to K - 1 padding slots
     // per row, rounded up to whole batches
@@ -1338,15 +1405,17 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
         p.f_lds_bytes = off;
         p.fused = d.rows * p.fpitch * 4 <= 64 * 1024 && off <= 160 * 1024;
     }
-    // workspace: fused path {gu, r} [T][B] u64; general path gu ([T][B], or
-    // [T][C][B] with the full STE) f32, then the sort kernel's slot offsets
-    // [T][slots] u32, row starts [T][R + 1] i32 and batch rows
-    // [T][slots / K] i32, each region 16-byte aligned
+    // workspace: fused path {gu, r} [T][B] u64; general path {gu, r} [T][B]
+    // u64 (min-margin) or gu [T][C][B] f32 (full STE), then the sort
+    // kernel's slot offsets [T][slots] u32, row starts [T][R + 1] i32, batch
+    // rows [T][slots / K] i32, the chunk-major copy of G [chunks][B][P] f32
+    // and (min-margin) the row kernel's partial dots [T][chunks][slots] f32,
+    // each region 16-byte aligned
     auto align16 = [](size_t v) { return (v + 15) & ~static_cast<size_t>(15); };
     if (p.fused) {
         p.workspace_bytes = static_cast<size_t>(d.tables) * d.items * sizeof(uint64_t);
     } else {
-        size_t off = align16(static_cast<size_t>(d.tables) * d.items * (p.full ? d.comps : 1) * sizeof(float));
+        size_t off = align16(static_cast<size_t>(d.tables) * d.items * (p.full ? d.comps * sizeof(float) : sizeof(uint64_t)));
         p.ws_slot_off = off;
         off = align16(off + static_cast<size_t>(d.tables) * p.sort_slots * sizeof(uint32_t));
         p.ws_row_start = off;
@@ -1355,6 +1424,8 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
         off = align16(off + static_cast<size_t>(d.tables) * (p.sort_slots / kRowsBatch) * sizeof(int32_t));
         p.ws_g_chunked = off;
         off = align16(off + static_cast<size_t>(p.rows_chunks) * d.items * rows_chunk * sizeof(float));
+        p.ws_pdot = off;
+        if (!p.full) off = align16(off + static_cast<size_t>(d.tables) * p.rows_chunks * p.sort_slots * sizeof(float));
         p.workspace_bytes = off;
     }
     return p;
@@ -1403,19 +1474,10 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
         hipError_t e = d.lut_dtype == TROPNN_LUT_F16 ? launch_fused_typed<_Float16>(f, p, stream)
                                                       : launch_fused_typed<float>(f, p, stream);
         if (e != hipSuccess || grad_x == nullptr) return e;
-        ScatterArgs s{};
-        s.gurec = gurec;
-        s.index_offsets = index_offsets;
-        s.index_entries = index_entries;
-        s.grad_x = grad_x;
-        s.items = d.items;
-        s.in_f = d.in_f;
-        s.tables = d.tables;
-        s.comps = d.comps;
-        return launch_kernel(TROPNN_KERNEL_BACKWARD_SCATTER, pairwise_bwd_scatter_kernel, dim3(d.items),
-                             dim3(kScatterThreads), p.scatter_lds_bytes, stream, s);
+        return launch_scatter(gurec, index_offsets, index_entries, grad_x, d, p, stream);
     }
-    if (grad_x != nullptr || grad_thr != nullptr) {
+    const bool need_gu = grad_x != nullptr || grad_thr != nullptr;
+    if (p.full && need_gu) {  // full STE: per-item dots of every comparison, grad_latent
         ItemArgs a{};
         a.grad_out = grad_out;
         a.lut = lut;
@@ -1456,15 +1518,18 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
         }
         if (e != hipSuccess) return e;
     }
-    if (grad_lut == nullptr && grad_thr == nullptr) return hipSuccess;
+    // min-margin: the row kernel forms the STE dots, so it runs whenever any
+    // gradient is asked for; the full STE needs it for the LUT gradient only
+    const bool dots = !p.full && need_gu;
+    if (grad_lut == nullptr && !dots && !(p.full && grad_thr != nullptr)) return hipSuccess;
     unsigned char *ws = reinterpret_cast<unsigned char *>(workspace);
     SortArgs so{};
     so.rec = rec64;
-    so.gu = workspace;
-    so.slot_off = grad_lut != nullptr ? reinterpret_cast<uint32_t *>(ws + p.ws_slot_off) : nullptr;
+    so.gu = p.full ? workspace : nullptr;
+    so.slot_off = grad_lut != nullptr || dots ? reinterpret_cast<uint32_t *>(ws + p.ws_slot_off) : nullptr;
     so.row_start = reinterpret_cast<int32_t *>(ws + p.ws_row_start);
     so.batch_row = reinterpret_cast<int32_t *>(ws + p.ws_batch_row);
-    so.grad_thr = grad_thr;
+    so.grad_thr = p.full ? grad_thr : nullptr;
     so.grad_out = grad_out;
     so.g_chunked = reinterpret_cast<float *>(ws + p.ws_g_chunked);
     so.chunk_cols = p.rows_chunk;
@@ -1478,7 +1543,7 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
     so.slots = p.sort_slots;
     if (hipError_t e = launch_kernel(TROPNN_KERNEL_BACKWARD_SORT, pairwise_bwd_sort_kernel, dim3(d.tables),
                                      dim3(kSortThreads), p.sort_lds_bytes, stream, so);
-        e != hipSuccess || grad_lut == nullptr)
+        e != hipSuccess || so.slot_off == nullptr)
         return e;
     RowsArgs r{};
     r.g_chunked = so.g_chunked;
@@ -1494,7 +1559,33 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
     r.tables = d.tables;
     r.slots = p.sort_slots;
     r.part_off = p.rows_part_off;
-    return launch_rows(r, p, d.tables, stream);
+    r.lut = lut;
+    r.lut_bytes = static_cast<uint32_t>(static_cast<size_t>(d.tables) * d.rows * d.out_f * esize);
+    r.pdot = dots ? reinterpret_cast<float *>(ws + p.ws_pdot) : nullptr;
+    r.items = d.items;
+    r.chunks = p.rows_chunks;
+    r.lut_off = p.rows_lut_off;
+    if (hipError_t e = launch_rows(r, p, d.tables, d.lut_dtype, dots, stream); e != hipSuccess || !dots) return e;
+    ReduceArgs ra{};
+    ra.pdot = r.pdot;
+    ra.slot_off = so.slot_off;
+    ra.row_start = so.row_start;
+    ra.rows = d.rows;
+    ra.slots = p.sort_slots;
+    ra.item_shift = __builtin_ctz(static_cast<unsigned>(p.rows_chunk) * 4u);
+    ra.rec = rec64;
+    ra.gurec = grad_x != nullptr ? reinterpret_cast<uint64_t *>(workspace) : nullptr;
+    ra.grad_thr = grad_thr;
+    ra.scale = scale;
+    ra.surrogate = surrogate;
+    ra.items = d.items;
+    ra.chunks = p.rows_chunks;
+    ra.comps = d.comps;
+    if (hipError_t e = launch_kernel(TROPNN_KERNEL_BACKWARD_REDUCE, pairwise_bwd_reduce_kernel, dim3(d.tables),
+                                     dim3(kReduceThreads), 0, stream, ra);
+        e != hipSuccess || grad_x == nullptr)
+        return e;
+    return launch_scatter(ra.gurec, index_offsets, index_entries, grad_x, d, p, stream);
 }
 
 }  // namespace tropnn

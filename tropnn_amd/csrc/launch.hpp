@@ -39,9 +39,12 @@ struct ForwardPlan {
     bool multi;          // large batch: several items per workgroup (blocks = ceil(items / kMultiItems))
 };
 
-// Launch shape of the backward. General path: the item kernel (STE dots, gu,
-// input gradient), the sort kernel (items of each table in code order,
-// threshold gradient) and the row kernel (LUT gradient).
+// Launch shape of the backward. General path, min-margin STE: the sort kernel
+// (items of each table in code order), the row kernel (LUT gradient and
+// partial STE dots per column chunk), the reduce kernel (gu, threshold
+// gradient) and the scatter kernel (input gradient). Full STE: the item
+// kernel (every comparison's dot, gu, input gradient), the sort kernel
+// (threshold gradient too) and the row kernel (LUT gradient).
 struct BackwardPlan {
     // row kernel
     int rows_vec;       // V: columns per lane (divides the row, at most 4)
@@ -50,10 +53,12 @@ struct BackwardPlan {
     int rows_chunks;    // column chunks of P
     int rows_part_off;  // LDS byte offset of the split-row slots
     int rows_lds_bytes;
+    int rows_lut_off;   // with partial STE dots: LDS byte offset of the LUT chunk
+    int rows_lds_dots_bytes;
     // sort kernel
     int sort_lds_bytes;
     int sort_slots;     // sorted-slot capacity of a table (items + padding to whole batches)
-    size_t ws_slot_off, ws_row_start, ws_batch_row, ws_g_chunked;  // workspace byte offsets (general path)
+    size_t ws_slot_off, ws_row_start, ws_batch_row, ws_g_chunked, ws_pdot;  // workspace byte offsets (general path)
     // item kernel
     int item_vec;       // N: LUT / grad elements per lane load (16 bytes at most)
     int item_o_tiles;   // 64 * N column tiles per row
