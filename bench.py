@@ -52,13 +52,16 @@ R = 1 << C
 E = 4  # f32 LUT element bytes
 
 
-def algorithmic_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = T, c: int = C, e: int = E) -> dict[str, int]:
+def algorithmic_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = T, c: int = C, e: int = E,
+                      streamed: bool = False) -> dict[str, int]:
     """Per-launch algorithmic bytes (gather / embedding-bag convention: every
     (item, table) pair moves its LUT row(s) once, streamed tensors and params
     once), split by the kernel that moves them; e = LUT element bytes. Sums to
     the FwdBwd figure of the plan: 148,548,672 B at c2 (the defaults),
     174,323,843,072 B at c4.
       forward: x, anchors + thresholds, one row per (item, table), y, codes;
+        streamed (large training shapes, c4): forward_route takes x,
+        anchors + thresholds and the codes, forward the rows and y;
     fused backward (narrow rows, c2's path):
       backward_fused: G, codes, current + neighbour rows per (item, table),
         one f32 grad-row contribution per (item, table), grad_lut once,
@@ -80,7 +83,11 @@ def algorithmic_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = 
     lut_rows = 4 * b * t * o + 4 * t * r * o
     if fused:
         return {"forward": fwd, "backward_fused": g_codes_rows + lut_rows + 4 * t * c, "backward_scatter": x_side}
-    return {"forward": fwd, "backward_sort": 0, "backward_table": g_codes_rows + lut_rows,
+    head = {"forward": fwd}
+    if streamed:
+        route = 4 * b * i + 20 * t * c + b * t
+        head = {"forward_route": route, "forward": fwd - route}
+    return {**head, "backward_sort": 0, "backward_table": g_codes_rows + lut_rows,
             "backward_reduce": 4 * t * c, "backward_scatter": x_side}
 
 
@@ -437,8 +444,9 @@ def bench_c4(args, dev) -> dict:
     f32 LUT (2 GiB) gradients. A step takes tens of milliseconds, so plain
     eager module steps are timed (K steps after the warmup); each kernel's
     duration comes from events its own dispatch stamps, over the same steps.
-    The backward takes the general path (sort, row, reduce and scatter
-    kernels)."""
+    The forward takes the streamed path (route-record kernel, then the
+    streamed gather) and the backward the general path (sort, row, reduce and
+    scatter kernels)."""
     import torch
 
     from tropnn_amd import PairwiseLinear
@@ -461,7 +469,7 @@ def bench_c4(args, dev) -> dict:
     for w in range(args.warmup):
         step(w % nb)
     torch.cuda.synchronize()
-    algo = algorithmic_bytes(False, e=2, **C4)
+    algo = algorithmic_bytes(False, e=2, streamed=True, **C4)
     names = tuple(algo)
     stream = torch.cuda.current_stream(dev)
     evs = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)] for n in names}

@@ -181,7 +181,11 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
  * calls, tools/benchmarking/benchmark.py:91-118). Arms two caller-created
  * hipEvent_t handles to be recorded on the launch stream immediately before
  * and after the NEXT launch of one kernel:
- *   TROPNN_KERNEL_FORWARD           the fused route + gather + scale kernel
+ *   TROPNN_KERNEL_FORWARD           the fused route + gather + scale kernel (large training
+ *                                   shapes: the streamed gather + scale kernel)
+ *   TROPNN_KERNEL_FORWARD_ROUTE     the route-record kernel before the streamed gather (training
+ *                                   forward with at least 4096 items, out_features a multiple of
+ *                                   64, comparisons <= 8 and a LUT of at least 32 MiB)
  *   TROPNN_KERNEL_BACKWARD_TABLE    the per-(table, column chunk) LUT-gradient kernel (with the
  *                                   min-margin STE: also each chunk's partial STE dots)
  *   TROPNN_KERNEL_BACKWARD_ITEM     the per-item STE-dot / input-gradient kernel of the full STE
@@ -206,6 +210,7 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
 #define TROPNN_KERNEL_BACKWARD_SCATTER 4
 #define TROPNN_KERNEL_BACKWARD_SORT 5
 #define TROPNN_KERNEL_BACKWARD_REDUCE 6
+#define TROPNN_KERNEL_FORWARD_ROUTE 7
 int tropnn_hip_arm_kernel_events(int kernel, void *start_event, void *stop_event);
 
 #ifdef __cplusplus

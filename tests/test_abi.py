@@ -153,6 +153,6 @@ def test_backward_rejects_bad_arguments(lib):
 
 
 def test_event_hook_rejects_bad_kernel(lib):
-    assert lib.tropnn_hip_arm_kernel_events(7, None, None) == 1
+    assert lib.tropnn_hip_arm_kernel_events(8, None, None) == 1
     assert lib.tropnn_hip_arm_kernel_events(0, ctypes.c_void_p(8), None) == 1
     assert lib.tropnn_hip_arm_kernel_events(0, None, None) == 0

@@ -64,6 +64,7 @@ KERNEL_IDS = {
     "backward_scatter": 4,
     "backward_sort": 5,
     "backward_reduce": 6,
+    "forward_route": 7,
 }
 
 

@@ -82,7 +82,7 @@ int check_forward_ptrs(const tropnn::Dims &d, const tropnn::ForwardPlan &p, cons
 }
 
 std::mutex g_events_mu;
-tropnn::ArmedEvents g_armed[TROPNN_KERNEL_BACKWARD_REDUCE + 1];
+tropnn::ArmedEvents g_armed[TROPNN_KERNEL_FORWARD_ROUTE + 1];
 
 }  // namespace
 
@@ -106,7 +106,7 @@ void arm_events(int kernel, hipEvent_t start, hipEvent_t stop) {
 extern "C" {
 
 int tropnn_hip_arm_kernel_events(int kernel, void *start_event, void *stop_event) {
-    if (kernel < TROPNN_KERNEL_FORWARD || kernel > TROPNN_KERNEL_BACKWARD_REDUCE)
+    if (kernel < TROPNN_KERNEL_FORWARD || kernel > TROPNN_KERNEL_FORWARD_ROUTE)
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "unknown kernel id %d", kernel);
     if ((start_event == nullptr) != (stop_event == nullptr))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "arm both events or neither");
@@ -132,6 +132,9 @@ int tropnn_hip_pairwise_forward(int64_t items, int64_t in_features, int64_t out_
     if ((route_record && misaligned(route_record, 8)) || (indices && misaligned(indices, 8)) ||
         (margins && misaligned(margins, 4)))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "route_record, indices and margins must be aligned to their element size");
+    if (route_record && p.stream_ok && (misaligned(lut, 16) || misaligned(output, 16)))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "the streamed training forward reads the LUT and writes the output "
+                                                 "in 16-byte pieces: both must be 16-byte aligned");
     if (p.lds_bytes > 64 * 1024)
         return fail(TROPNN_ERR_UNSUPPORTED, "forward needs %d bytes of LDS (tables too large)", p.lds_bytes);
     // the gather addresses the LUT through one buffer resource with 32-bit offsets

@@ -577,8 +577,12 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
                              c0 < O ? static_cast<uint32_t>((static_cast<size_t>(t) * R + row) * O + c0) * sizeof(T)
                                     : kOutOfRange,
                              0, w);
+            vec_t<float, V> wv;
 #pragma unroll
-            for (int e = 0; e < V; ++e) lut_s[row * P + pc * V + e] = w[e];
+            for (int e = 0; e < V; ++e) wv[e] = w[e];
+            // whole-vector LDS accesses: element by element the lanes' 4-byte
+            // accesses stride by V * 4 bytes and collide in the banks
+            *reinterpret_cast<vec_t<float, V> *>(lut_s + row * P + pc * V) = wv;
         }
     }
     __syncthreads();
@@ -645,8 +649,9 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
 #pragma unroll
             for (int e = 0; e < V; ++e) acc[e] = 0.f;
             if constexpr (DOTS) {
+                const vec_t<float, V> lv = *reinterpret_cast<const vec_t<float, V> *>(lut_s + k * P + j * V);
 #pragma unroll
-                for (int e = 0; e < V; ++e) lkv[e] = lut_s[k * P + j * V + e];
+                for (int e = 0; e < V; ++e) lkv[e] = lv[e];
             }
         }
 #pragma unroll
@@ -660,9 +665,10 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
 #pragma unroll
             for (int u = 0; u < K; ++u) {
                 const int nb = (kk ^ (1 << (off[u] & 7u))) & (R - 1);  // the mask keeps a corrupt record in range
+                const vec_t<float, V> nv = *reinterpret_cast<const vec_t<float, V> *>(lut_s + nb * P + j * V);
                 float sd = 0.f;
 #pragma unroll
-                for (int e = 0; e < V; ++e) sd += gv[u][e] * (lut_s[nb * P + j * V + e] - lkv[e]);
+                for (int e = 0; e < V; ++e) sd += gv[u][e] * (nv[e] - lkv[e]);
                 d[u] = sd;
             }
 #pragma unroll

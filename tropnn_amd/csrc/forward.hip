@@ -416,6 +416,226 @@ struct RouteArgs {
     int items, in_f, tables, comps;
 };
 
+// ------------------------------------------------------------------ streamed forward (large training shapes)
+
+// Route of a block of items for every table: one thread per table, the
+// block's input rows staged in LDS. Writes the route records [T][B] (the
+// streamed gather reads the codes from them) and any debug output, with the
+// fused forward's arithmetic and its argmin rules (NaN first, then the
+// smaller |m|, then the lower comparison index), so records, codes and
+// margins are bit-identical to the fused forward's.
+struct RouteRecArgs {
+    const float *x;
+    const int64_t *anchors;
+    const float *thr;
+    uint64_t *rec;
+    int64_t *indices;
+    float *margins;
+    uint8_t *codes;
+    int items, in_f, tables, comps, block_items;
+};
+
+constexpr int kRouteRecThreads = 512;
+
+__global__ __launch_bounds__(kRouteRecThreads) void pairwise_route_records_kernel(RouteRecArgs a) {
+    extern __shared__ __align__(16) float xs[];  // [block_items][in_f]
+    const int b0 = blockIdx.x * a.block_items, n = min(a.block_items, a.items - b0);
+    const float *src = a.x + static_cast<size_t>(b0) * a.in_f;
+    for (int k = threadIdx.x; k < n * a.in_f; k += kRouteRecThreads) xs[k] = src[k];
+    __syncthreads();
+    for (int t = threadIdx.x; t < a.tables; t += kRouteRecThreads) {
+        int ia[TROPNN_MAX_COMPARISONS], ib[TROPNN_MAX_COMPARISONS];
+        float th[TROPNN_MAX_COMPARISONS];
+        for (int c = 0; c < a.comps; ++c) {
+            const size_t q = static_cast<size_t>(t) * a.comps + c;
+            ia[c] = clamp_index(a.anchors[2 * q], a.in_f);
+            ib[c] = clamp_index(a.anchors[2 * q + 1], a.in_f);
+            th[c] = a.thr[q];
+        }
+        for (int m = 0; m < n; ++m) {
+            const float *xr = xs + m * a.in_f;
+            const size_t bt = static_cast<size_t>(b0 + m) * a.tables + t;
+            int code = 0, best = 0;
+            uint32_t best_key = 0xFFFFFFFFu;
+            float best_m = 0.f;
+            for (int c = 0; c < a.comps; ++c) {
+                const float mg = (xr[ia[c]] - xr[ib[c]]) - th[c];
+                code |= (mg > 0.f ? 1 : 0) << c;
+                const float mag = fabsf(mg);
+                const uint32_t key = mag != mag ? 0u : __builtin_bit_cast(uint32_t, mag) + 1u;
+                if (key < best_key) {  // strict: the first index wins a tie
+                    best_key = key;
+                    best = c;
+                    best_m = mg;
+                }
+                if (a.margins != nullptr) a.margins[bt * a.comps + c] = mg;
+            }
+            a.rec[static_cast<size_t>(t) * a.items + b0 + m] = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, best_m)) |
+                                                             (static_cast<uint64_t>(code) << 32) |
+                                                             (static_cast<uint64_t>(best) << 48);
+            if (a.indices != nullptr) a.indices[bt] = code;
+            if (a.codes != nullptr) a.codes[bt] = static_cast<uint8_t>(code);
+        }
+    }
+}
+
+// Streamed gather: one workgroup per (block of M items, 64-column chunk), the
+// workgroups of a chunk adjacent on one XCD. The workgroup walks the tables
+// in order with table t's LUT chunk (R rows x 64 columns) in LDS, double
+// buffered: while it sums table t, the chunk of table t + 1 goes to the other
+// buffer and the chunks of t + 2 and t + 3 are on their way to registers,
+// and likewise the items' codes (from the route records). Thread (slot,
+// piece) owns items 4 slot .. 4 slot + 3 and one 16-byte piece of the chunk:
+// per table four LDS row reads and the adds. The workgroups of one chunk
+// stream the same LUT chunks at about the same time, so the LUT crosses HBM
+// about once instead of once per (item, table) row gather. Tables are summed
+// in blocks of the one-item kernel's tables per wave, and the blocks in
+// order, as that kernel sums its waves: the outputs are bit-identical to it.
+struct StreamArgs {
+    const void *lut;
+    const uint64_t *rec;
+    float *out;
+    float scale;
+    int items, out_f, tables, rows, nblk, block_tables, pitch;  // pitch: LDS bytes per staged row
+};
+
+constexpr int kStreamThreads = 1024;
+constexpr int kStreamCols = 64;  // columns of a chunk
+constexpr int kStreamIpt = 4;    // items per thread
+constexpr int kStreamMinItems = 4096;
+constexpr long long kStreamMinLutBytes = 32ll << 20;
+
+template <typename T>
+__global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel(StreamArgs a) {
+    constexpr int PE = 16 / static_cast<int>(sizeof(T));   // elements per 16-byte piece
+    constexpr int PIECES = kStreamCols / PE;                // pieces per row chunk
+    constexpr int SLOTS = kStreamThreads / PIECES;
+    constexpr int M = SLOTS * kStreamIpt;                   // items per workgroup
+    constexpr int STAGE = 256 * PIECES / kStreamThreads;    // pieces a thread stages per table (R <= 256)
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int R = a.rows;
+    unsigned char *buf0 = lds;                                   // [R][pitch]
+    unsigned char *buf1 = lds + R * a.pitch;
+    uint16_t *codes0 = reinterpret_cast<uint16_t *>(lds + 2 * R * a.pitch);  // [M]
+    uint16_t *codes1 = codes0 + M;
+
+    const int unit = xcd_block_unit(blockIdx.x, gridDim.x);
+    const int chunk = unit / a.nblk, blk = unit - chunk * a.nblk;
+    const int b0 = blk * M;
+    const int tid = threadIdx.x, slot = tid / PIECES, piece = tid % PIECES;
+    const size_t row_bytes = static_cast<size_t>(a.out_f) * sizeof(T);
+    const unsigned char *lut = static_cast<const unsigned char *>(a.lut) + static_cast<size_t>(chunk) * kStreamCols * sizeof(T);
+
+    // staging of table t: thread pieces q = tid + i * 1024 (row q / PIECES);
+    // two register stages, so a table's loads have two iterations to arrive
+    vec_t<uint32_t, 4> stage_a[STAGE], stage_b[STAGE];
+    uint16_t code_a = 0, code_b = 0;
+    auto load_table = [&](int t, vec_t<uint32_t, 4>(&stage)[STAGE], uint16_t &code) {
+        const unsigned char *base = lut + static_cast<size_t>(t) * R * row_bytes;
+#pragma unroll
+        for (int i = 0; i < STAGE; ++i) {
+            const int q = tid + i * kStreamThreads, row = q / PIECES, pc = q % PIECES;
+            if (row < R)
+                stage[i] = *reinterpret_cast<const vec_t<uint32_t, 4> *>(base + row * row_bytes + pc * 16);
+        }
+        if (tid < M) {
+            const int b = b0 + tid;
+            code = b < a.items ? static_cast<uint16_t>((a.rec[static_cast<size_t>(t) * a.items + b] >> 32) & (R - 1)) : 0;
+        }
+    };
+    auto store_table = [&](int t, const vec_t<uint32_t, 4>(&stage)[STAGE], uint16_t code) {
+        unsigned char *buf = (t & 1) ? buf1 : buf0;
+#pragma unroll
+        for (int i = 0; i < STAGE; ++i) {
+            const int q = tid + i * kStreamThreads, row = q / PIECES, pc = q % PIECES;
+            if (row < R) *reinterpret_cast<vec_t<uint32_t, 4> *>(buf + row * a.pitch + pc * 16) = stage[i];
+        }
+        if (tid < M) ((t & 1) ? codes1 : codes0)[tid] = code;
+    };
+
+    float blk_acc[kStreamIpt][PE], tot[kStreamIpt][PE];
+#pragma unroll
+    for (int k = 0; k < kStreamIpt; ++k)
+#pragma unroll
+        for (int e = 0; e < PE; ++e) blk_acc[k][e] = tot[k][e] = 0.f;
+
+    int first_block = 1;
+    // table t from LDS: this thread's four items' codes, their rows' pieces, the adds
+    auto sum_table = [&](int t) {
+        const unsigned char *cur = (t & 1) ? buf1 : buf0;
+        const uint16_t *cc = (t & 1) ? codes1 : codes0;
+        const vec_t<uint16_t, 4> cv = *reinterpret_cast<const vec_t<uint16_t, 4> *>(cc + slot * kStreamIpt);
+        vec_t<uint32_t, 4> w[kStreamIpt];
+#pragma unroll
+        for (int k = 0; k < kStreamIpt; ++k) w[k] = *reinterpret_cast<const vec_t<uint32_t, 4> *>(cur + cv[k] * a.pitch + piece * 16);
+#pragma unroll
+        for (int k = 0; k < kStreamIpt; ++k) {
+            if constexpr (sizeof(T) == 2) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    blk_acc[k][2 * e] = add_f16_mix<false>(blk_acc[k][2 * e], w[k][e]);
+                    blk_acc[k][2 * e + 1] = add_f16_mix<true>(blk_acc[k][2 * e + 1], w[k][e]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    // element to a scalar first: a bit cast of the vector element itself
+                    // reads element 0 for every e
+                    const uint32_t bits = w[k][e];
+                    blk_acc[k][e] += __builtin_bit_cast(float, bits);
+                }
+            }
+        }
+        if ((t + 1) % a.block_tables == 0 || t + 1 == a.tables) {
+#pragma unroll
+            for (int k = 0; k < kStreamIpt; ++k)
+#pragma unroll
+                for (int e = 0; e < PE; ++e) {
+                    tot[k][e] = first_block ? blk_acc[k][e] : tot[k][e] + blk_acc[k][e];
+                    blk_acc[k][e] = 0.f;
+                }
+            first_block = 0;
+        }
+    };
+
+    // prologue: table 0 in LDS, table 1 in stage a, table 2 in stage b.
+    // Iteration t stores table t + 1 (loaded two iterations earlier) into
+    // the other LDS buffer, loads table t + 3 into the stage it freed, sums
+    // table t, and ends on a barrier.
+    load_table(0, stage_a, code_a);
+    store_table(0, stage_a, code_a);
+    if (a.tables > 1) load_table(1, stage_a, code_a);
+    if (a.tables > 2) load_table(2, stage_b, code_b);
+    __syncthreads();
+    for (int t = 0; t < a.tables; t += 2) {
+        if (t + 1 < a.tables) {
+            store_table(t + 1, stage_a, code_a);
+            if (t + 3 < a.tables) load_table(t + 3, stage_a, code_a);
+        }
+        sum_table(t);
+        __syncthreads();
+        if (t + 1 < a.tables) {
+            if (t + 2 < a.tables) {
+                store_table(t + 2, stage_b, code_b);
+                if (t + 4 < a.tables) load_table(t + 4, stage_b, code_b);
+            }
+            sum_table(t + 1);
+            __syncthreads();
+        }
+    }
+    const int col = chunk * kStreamCols + piece * PE;
+#pragma unroll
+    for (int k = 0; k < kStreamIpt; ++k) {
+        const int b = b0 + slot * kStreamIpt + k;
+        if (b < a.items) {
+            float y[PE];
+#pragma unroll
+            for (int e = 0; e < PE; ++e) y[e] = tot[k][e] * a.scale;
+            store_f32_nt<PE>(a.out + static_cast<size_t>(b) * a.out_f + col, y);
+        }
+    }
+}
+
 constexpr int kRouteThreads = 256;
 
 __global__ __launch_bounds__(kRouteThreads) void pairwise_route_kernel(RouteArgs a) {
@@ -451,6 +671,20 @@ hipError_t launch_typed(const FwdArgs &args, const ForwardPlan &p, bool train, b
     auto kernel = train ? (debug ? pairwise_forward_kernel<T, N, true, true> : pairwise_forward_kernel<T, N, true, false>)
                         : (debug ? pairwise_forward_kernel<T, N, false, true> : pairwise_forward_kernel<T, N, false, false>);
     return launch_kernel(TROPNN_KERNEL_FORWARD, kernel, grid, block, p.lds_bytes, stream, args);
+}
+
+template <typename T>
+hipError_t launch_stream(const StreamArgs &args, const ForwardPlan &p, hipStream_t stream) {
+    auto kernel = pairwise_forward_stream_kernel<T>;
+    static int allowed = 0;  // more than the default 64 KB of dynamic LDS: opt in once per instantiation
+    if (p.stream_lds > 64 * 1024 && p.stream_lds > allowed) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, p.stream_lds);
+        if (e != hipSuccess) return e;
+        allowed = p.stream_lds;
+    }
+    return launch_kernel(TROPNN_KERNEL_FORWARD, kernel, dim3(p.stream_blocks), dim3(kStreamThreads), p.stream_lds,
+                         stream, args);
 }
 
 int ilog2(int v) {
@@ -525,6 +759,24 @@ ForwardPlan plan_forward(const Dims &d) {
             }
         }
     }
+
+    // streamed gather (training only: it reads the codes from the route
+    // records): large batches over a LUT far beyond the L2, rows of whole
+    // 64-column chunks, at most 256 rows per table
+    const long long lut_bytes = static_cast<long long>(d.tables) * d.rows * d.out_f * esize;
+    p.stream_ok = d.items >= kStreamMinItems && d.out_f % kStreamCols == 0 && d.rows <= 256 &&
+                  lut_bytes >= kStreamMinLutBytes;
+    if (p.stream_ok) {
+        const int pieces = kStreamCols * esize / 16;
+        const int m = (kStreamThreads / pieces) * kStreamIpt;
+        p.stream_pitch = kStreamCols * esize + 16;  // a 16-byte pad staggers the rows over the LDS banks
+        p.stream_nblk = (d.items + m - 1) / m;
+        p.stream_blocks = p.stream_nblk * (d.out_f / kStreamCols);
+        p.stream_lds = 2 * d.rows * p.stream_pitch + 2 * m * 2;
+        p.route_block_items = 16;
+        while (p.route_block_items > 1 && p.route_block_items * d.in_f * 4 > 64 * 1024) p.route_block_items >>= 1;
+        p.route_lds = p.route_block_items * d.in_f * 4;
+    }
     return p;
 }
 
@@ -558,6 +810,18 @@ hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, c
     a.red_off = p.red_off;
     const bool train = rec != nullptr;
     const bool debug = indices != nullptr || margins != nullptr || codes != nullptr;
+    if (train && p.stream_ok) {
+        RouteRecArgs r{x, anchors, thr, a.rec, indices, margins, codes, d.items, d.in_f, d.tables, d.comps,
+                       p.route_block_items};
+        if (hipError_t e = launch_kernel(TROPNN_KERNEL_FORWARD_ROUTE, pairwise_route_records_kernel,
+                                         dim3((d.items + p.route_block_items - 1) / p.route_block_items),
+                                         dim3(kRouteRecThreads), p.route_lds, stream, r);
+            e != hipSuccess)
+            return e;
+        StreamArgs g{lut, a.rec, out, scale, d.items, d.out_f, d.tables, d.rows, p.stream_nblk, p.per_wave,
+                     p.stream_pitch};
+        return d.lut_dtype == TROPNN_LUT_F16 ? launch_stream<_Float16>(g, p, stream) : launch_stream<float>(g, p, stream);
+    }
     if (d.lut_dtype == TROPNN_LUT_F16) {
         switch (p.vec) {
             case 8: return launch_typed<_Float16, 8>(a, p, train, debug, stream);

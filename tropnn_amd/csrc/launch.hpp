@@ -37,6 +37,16 @@ struct ForwardPlan {
     int red_off;
     int lds_bytes;
     bool multi;          // large batch: several items per workgroup (blocks = ceil(items / kMultiItems))
+    // streamed gather (training, large batch and LUT): a route kernel writes
+    // the records, then one workgroup per (item block, 64-column chunk)
+    // walks the tables with each table's LUT chunk in LDS
+    bool stream_ok;
+    int stream_pitch;       // LDS bytes per staged row
+    int stream_nblk;        // item blocks
+    int stream_blocks;      // workgroups
+    int stream_lds;
+    int route_block_items;  // items per route workgroup (their input rows in LDS)
+    int route_lds;
 };
 
 // Launch shape of the backward. General path, min-margin STE: the sort kernel
