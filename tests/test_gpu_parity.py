@@ -655,3 +655,20 @@ def test_streamed_training_forward(lut_dtype, t, o):
     assert torch.equal(hip._last_indices, idx_eval)
     assert torch.equal(hip._last_margins.view(torch.int32), mar_eval.view(torch.int32))
     assert_train_parity(ref, hip, yx_ref, yx_hip, tol=F16_TOL if lut_dtype == "f16" else F32_TOL)
+
+
+@pytest.mark.parametrize(
+    "i,o,t,c,b,min_margin",
+    [
+        (64, 16, 1100, 8, 37, True),  # general path: the scatter kernel stages 106 KB
+        (64, 16, 1100, 8, 37, False),  # full STE: the per-item kernel stages 106 KB
+        (64, 32, 3000, 4, 40, True),  # fused path: the scatter kernel stages 144 KB
+    ],
+)
+def test_large_tables_times_comparisons(i, o, t, c, b, min_margin):
+    """Shapes whose per-item gu slots [T * C] and inverse anchor index need
+    more than the default 64 KB of LDS (up to the workgroup's 160 KB)."""
+    ref, hip = make_pair(i, o, t, c, seed=7, thr_std=0.3, use_min_margin_ste=min_margin)
+    x = seeded((b, i), seed=8)
+    g = seeded((b, 1, o), seed=9)
+    assert_train_parity(ref, hip, *train_step(ref, hip, x, g))

@@ -260,8 +260,13 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
                         workspace_bytes);
         if (misaligned(workspace, 16)) return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
     }
-    if (p.item_lds_bytes > 64 * 1024)
-        return fail(TROPNN_ERR_UNSUPPORTED, "backward LDS plan exceeds the workgroup limit (in_features or tables too large)");
+    // an item's gu slots [T * C] and the inverse anchor index sit in one
+    // workgroup's LDS (160 KB on gfx950): 3 T C + in_f words, about 13,000
+    // (table, comparison) pairs at in_f = 128
+    if (p.item_lds_bytes > 160 * 1024)
+        return fail(TROPNN_ERR_UNSUPPORTED,
+                    "backward needs %d bytes of LDS per item, over the 160 KB of a workgroup (tables * comparisons "
+                    "or in_features too large)", p.item_lds_bytes);
     // grad rows and the LUT are addressed through buffer resources with 32-bit offsets
     const int64_t lut_bytes = int64_t{d.tables} * d.rows * d.out_f * esize;
     const int64_t g_bytes = int64_t{d.items} * d.out_f * 4;

@@ -64,6 +64,9 @@
 // threshold gradient from gu) and the row kernel without dots.
 //  A third, tiny kernel builds the inverse anchor index; callers rebuild it
 //  only when the anchors change.
+#include <mutex>
+#include <unordered_map>
+
 #include "device.hpp"
 #include "launch.hpp"
 
@@ -1218,16 +1221,9 @@ __global__ __launch_bounds__(256) void anchor_index_kernel(const int64_t *anchor
     }
 }
 
-// Kernels that may need more than the default 64 KB of dynamic LDS opt in
-// once per process.
 template <typename K>
 hipError_t allow_lds(K kernel, int bytes) {
-    static int allowed = 0;  // one flag per kernel instantiation
-    if (bytes <= 64 * 1024 || bytes <= allowed) return hipSuccess;
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    if (e == hipSuccess) allowed = bytes;
-    return e;
+    return allow_dynamic_lds(reinterpret_cast<const void *>(kernel), bytes);
 }
 
 template <typename T, int V, int S, bool DOTS>
@@ -1270,8 +1266,10 @@ hipError_t launch_rows(const RowsArgs &args, const BackwardPlan &p, int tables, 
 
 template <typename T, int N>
 hipError_t launch_item_typed(const ItemArgs &args, const BackwardPlan &p, hipStream_t stream) {
-    return launch_kernel(TROPNN_KERNEL_BACKWARD_ITEM, pairwise_bwd_full_kernel<T, N>, dim3(args.items),
-                         dim3(p.item_threads), p.item_lds_bytes, stream, args);
+    auto kernel = pairwise_bwd_full_kernel<T, N>;
+    if (hipError_t e = allow_lds(kernel, p.item_lds_bytes); e != hipSuccess) return e;
+    return launch_kernel(TROPNN_KERNEL_BACKWARD_ITEM, kernel, dim3(args.items), dim3(p.item_threads), p.item_lds_bytes,
+                         stream, args);
 }
 
 template <typename T, int V, int S>
@@ -1296,6 +1294,18 @@ __global__ void fill_zero_kernel(float *p, size_t n) {
 }
 
 }  // namespace
+
+hipError_t allow_dynamic_lds(const void *kernel, int bytes) {
+    static std::mutex mu;
+    static std::unordered_map<const void *, int> allowed;  // the largest size each kernel opted in for
+    if (bytes <= 64 * 1024) return hipSuccess;
+    std::lock_guard<std::mutex> lock(mu);
+    int &done = allowed[kernel];
+    if (bytes <= done) return hipSuccess;
+    const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess) done = bytes;
+    return e;
+}
 
 hipError_t launch_fill_zero(float *p, size_t n, hipStream_t stream) {
     if (n == 0) return hipSuccess;
@@ -1323,6 +1333,7 @@ hipError_t launch_scatter(const uint64_t *gurec, const int32_t *index_offsets, c
     s.in_f = d.in_f;
     s.tables = d.tables;
     s.comps = d.comps;
+    if (hipError_t e = allow_lds(pairwise_bwd_scatter_kernel, p.scatter_lds_bytes); e != hipSuccess) return e;
     return launch_kernel(TROPNN_KERNEL_BACKWARD_SCATTER, pairwise_bwd_scatter_kernel, dim3(d.items),
                          dim3(kScatterThreads), p.scatter_lds_bytes, stream, s);
 }

@@ -676,13 +676,8 @@ hipError_t launch_typed(const FwdArgs &args, const ForwardPlan &p, bool train, b
 template <typename T>
 hipError_t launch_stream(const StreamArgs &args, const ForwardPlan &p, hipStream_t stream) {
     auto kernel = pairwise_forward_stream_kernel<T>;
-    static int allowed = 0;  // more than the default 64 KB of dynamic LDS: opt in once per instantiation
-    if (p.stream_lds > 64 * 1024 && p.stream_lds > allowed) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, p.stream_lds);
-        if (e != hipSuccess) return e;
-        allowed = p.stream_lds;
-    }
+    if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void *>(kernel), p.stream_lds); e != hipSuccess)
+        return e;
     return launch_kernel(TROPNN_KERNEL_FORWARD, kernel, dim3(p.stream_blocks), dim3(kStreamThreads), p.stream_lds,
                          stream, args);
 }

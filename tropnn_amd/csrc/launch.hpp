@@ -151,4 +151,8 @@ hipError_t launch_kernel(int kernel_id, F kernel, dim3 grid, dim3 block, uint32_
 // Writes n zeros with a kernel (no hipMemsetAsync node in captured graphs).
 hipError_t launch_fill_zero(float *p, size_t n, hipStream_t stream);
 
+// Opts `kernel` into `bytes` of dynamic LDS when that is above the default
+// 64 KB, once per kernel and size (thread-safe; keyed by the kernel's address).
+hipError_t allow_dynamic_lds(const void *kernel, int bytes);
+
 }  // namespace tropnn
