@@ -184,8 +184,8 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
  *   TROPNN_KERNEL_FORWARD           the fused route + gather + scale kernel (large training
  *                                   shapes: the streamed gather + scale kernel)
  *   TROPNN_KERNEL_FORWARD_ROUTE     the route-record kernel before the streamed gather (training
- *                                   forward with at least 4096 items, out_features a multiple of
- *                                   64, comparisons <= 8 and a LUT of at least 32 MiB)
+ *                                   forward with at least 4096 items, LUT rows of whole 128-byte
+ *                                   chunks, comparisons <= 8 and a LUT of at least 32 MiB)
  *   TROPNN_KERNEL_BACKWARD_TABLE    the per-(table, column chunk) LUT-gradient kernel (with the
  *                                   min-margin STE: also each chunk's partial STE dots)
  *   TROPNN_KERNEL_BACKWARD_ITEM     the per-item STE-dot / input-gradient kernel of the full STE

@@ -479,78 +479,94 @@ __global__ __launch_bounds__(kRouteRecThreads) void pairwise_route_records_kerne
     }
 }
 
-// Streamed gather: one workgroup per (block of M items, 64-column chunk), the
-// workgroups of a chunk adjacent on one XCD. The workgroup walks the tables
-// in order with table t's LUT chunk (R rows x 64 columns) in LDS, double
-// buffered: while it sums table t, the chunk of table t + 1 goes to the other
-// buffer and the chunks of t + 2 and t + 3 are on their way to registers,
-// and likewise the items' codes (from the route records). Thread (slot,
-// piece) owns items 4 slot .. 4 slot + 3 and one 16-byte piece of the chunk:
-// per table four LDS row reads and the adds. The workgroups of one chunk
-// stream the same LUT chunks at about the same time, so the LUT crosses HBM
-// about once instead of once per (item, table) row gather. Tables are summed
-// in blocks of the one-item kernel's tables per wave, and the blocks in
-// order, as that kernel sums its waves: the outputs are bit-identical to it.
+// Streamed gather: one workgroup per (block of 512 items, chunk of 128 bytes
+// of every LUT row: 64 f16 or 32 f32 columns), the workgroups of a chunk
+// adjacent on one XCD. The workgroup walks the tables in order with the
+// tables' LUT chunks (R rows x 128 bytes) in three LDS buffers, filled by
+// LDS-direct loads (global_load_lds_dwordx4: no registers, no LDS write
+// instructions) two tables ahead; the items' codes (from the route records)
+// follow the same pipeline through a register. Thread (slot, piece) owns
+// items 4 slot .. 4 slot + 3 and one 16-byte piece of the chunk: per table
+// four LDS row reads and the adds. The workgroups of one chunk stream the
+// same LUT chunks at about the same time, so the LUT crosses HBM about once
+// instead of once per (item, table) row gather. Tables are summed in blocks
+// of the one-item kernel's tables per wave, and the blocks in order, as that
+// kernel sums its waves: the outputs are bit-identical to it.
 struct StreamArgs {
     const void *lut;
     const uint64_t *rec;
     float *out;
     float scale;
-    int items, out_f, tables, rows, nblk, block_tables, pitch;  // pitch: LDS bytes per staged row
+    int items, out_f, tables, rows, nblk, block_tables;
 };
 
 constexpr int kStreamThreads = 1024;
-constexpr int kStreamCols = 64;  // columns of a chunk
-constexpr int kStreamIpt = 4;    // items per thread
+constexpr int kStreamChunkBytes = 128;                       // bytes of a LUT row in a chunk
+constexpr int kStreamPieces = kStreamChunkBytes / 16;        // 16-byte pieces of a row chunk
+constexpr int kStreamIpt = 4;                                // items per thread
+constexpr int kStreamItems = kStreamThreads / kStreamPieces * kStreamIpt;  // items per workgroup
+constexpr int kStreamBufs = 3;                               // LUT chunks in LDS
+constexpr int kStreamBufBytes = 256 * kStreamChunkBytes;     // one chunk, room for R = 256 rows
+constexpr int kStreamLds = kStreamBufs * (kStreamBufBytes + kStreamItems * 2);
 constexpr int kStreamMinItems = 4096;
 constexpr long long kStreamMinLutBytes = 32ll << 20;
 
 template <typename T>
 __global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel(StreamArgs a) {
-    constexpr int PE = 16 / static_cast<int>(sizeof(T));   // elements per 16-byte piece
-    constexpr int PIECES = kStreamCols / PE;                // pieces per row chunk
-    constexpr int SLOTS = kStreamThreads / PIECES;
-    constexpr int M = SLOTS * kStreamIpt;                   // items per workgroup
-    constexpr int STAGE = 256 * PIECES / kStreamThreads;    // pieces a thread stages per table (R <= 256)
+    constexpr int PE = 16 / static_cast<int>(sizeof(T));  // elements per 16-byte piece
+    constexpr int COLS = kStreamChunkBytes / static_cast<int>(sizeof(T));
+    constexpr int M = kStreamItems;
+    constexpr int STAGE = kStreamBufBytes / 16 / kStreamThreads;  // LDS-direct loads per thread per table
     extern __shared__ __align__(16) unsigned char lds[];
     const int R = a.rows;
-    unsigned char *buf0 = lds;                                   // [R][pitch]
-    unsigned char *buf1 = lds + R * a.pitch;
-    uint16_t *codes0 = reinterpret_cast<uint16_t *>(lds + 2 * R * a.pitch);  // [M]
-    uint16_t *codes1 = codes0 + M;
+    uint16_t *codes = reinterpret_cast<uint16_t *>(lds + kStreamBufs * kStreamBufBytes);  // [bufs][M]
 
     const int unit = xcd_block_unit(blockIdx.x, gridDim.x);
     const int chunk = unit / a.nblk, blk = unit - chunk * a.nblk;
     const int b0 = blk * M;
-    const int tid = threadIdx.x, slot = tid / PIECES, piece = tid % PIECES;
+    const int tid = threadIdx.x, slot = tid / kStreamPieces, piece = tid % kStreamPieces;
+    const int wave = tid >> 6;
     const size_t row_bytes = static_cast<size_t>(a.out_f) * sizeof(T);
-    const unsigned char *lut = static_cast<const unsigned char *>(a.lut) + static_cast<size_t>(chunk) * kStreamCols * sizeof(T);
+    const unsigned char *lut = static_cast<const unsigned char *>(a.lut) + static_cast<size_t>(chunk) * kStreamChunkBytes;
 
-    // staging of table t: thread pieces q = tid + i * 1024 (row q / PIECES);
-    // two register stages, so a table's loads have two iterations to arrive
-    vec_t<uint32_t, 4> stage_a[STAGE], stage_b[STAGE];
-    uint16_t code_a = 0, code_b = 0;
-    auto load_table = [&](int t, vec_t<uint32_t, 4>(&stage)[STAGE], uint16_t &code) {
+    // table t's chunk into buffer t % 3: piece q = tid + i * 1024 (row q / 8,
+    // piece q % 8) lands at byte 16 q, i.e. row-major with a 128-byte pitch,
+    // as lane l of a wave writes 16 bytes at the wave's base + 16 l. Rows past
+    // R load row R - 1 (in bounds) into buffer rows no code reads.
+    auto issue_table = [&](int t) {
         const unsigned char *base = lut + static_cast<size_t>(t) * R * row_bytes;
+        unsigned char *buf = lds + (t % kStreamBufs) * kStreamBufBytes;
 #pragma unroll
         for (int i = 0; i < STAGE; ++i) {
-            const int q = tid + i * kStreamThreads, row = q / PIECES, pc = q % PIECES;
-            if (row < R)
-                stage[i] = *reinterpret_cast<const vec_t<uint32_t, 4> *>(base + row * row_bytes + pc * 16);
-        }
-        if (tid < M) {
-            const int b = b0 + tid;
-            code = b < a.items ? static_cast<uint16_t>((a.rec[static_cast<size_t>(t) * a.items + b] >> 32) & (R - 1)) : 0;
+            const int q = tid + i * kStreamThreads, row = min(q / kStreamPieces, R - 1), pc = q % kStreamPieces;
+            __builtin_amdgcn_global_load_lds(base + row * row_bytes + pc * 16,
+                                             (__attribute__((address_space(3))) void *)(buf + (i * kStreamThreads + wave * kWave) * 16),
+                                             16, 0, 0);
         }
     };
-    auto store_table = [&](int t, const vec_t<uint32_t, 4>(&stage)[STAGE], uint16_t code) {
-        unsigned char *buf = (t & 1) ? buf1 : buf0;
-#pragma unroll
-        for (int i = 0; i < STAGE; ++i) {
-            const int q = tid + i * kStreamThreads, row = q / PIECES, pc = q % PIECES;
-            if (row < R) *reinterpret_cast<vec_t<uint32_t, 4> *>(buf + row * a.pitch + pc * 16) = stage[i];
+    // the items' codes: the raw record of table t + 2 waits in a register
+    // (decoded when stored, an iteration later, so that no wait for it
+    // drains the LDS-direct loads issued after it)
+    uint64_t rec_next = 0;
+    auto load_code = [&](int t) {
+        if (tid < M) {
+            const int b = min(b0 + tid, a.items - 1);  // past the batch: any record, never read
+            rec_next = a.rec[static_cast<size_t>(t) * a.items + b];
         }
-        if (tid < M) ((t & 1) ? codes1 : codes0)[tid] = code;
+    };
+    auto store_code = [&](int t) {
+        if (tid < M) codes[(t % kStreamBufs) * M + tid] = static_cast<uint16_t>((rec_next >> 32) & (R - 1));
+    };
+    // all of this wave's loads but the newest `pending` have landed (LDS-direct
+    // ones included), its LDS writes are done, then the workgroup meets: a
+    // plain s_barrier, since __syncthreads()'s fence would wait for every
+    // load, the LDS-direct loads of the next table too
+    auto meet = [&](bool pending) {
+        if (pending)
+            asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)" ::: "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
     };
 
     float blk_acc[kStreamIpt][PE], tot[kStreamIpt][PE];
@@ -558,16 +574,43 @@ __global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel
     for (int k = 0; k < kStreamIpt; ++k)
 #pragma unroll
         for (int e = 0; e < PE; ++e) blk_acc[k][e] = tot[k][e] = 0.f;
-
     int first_block = 1;
-    // table t from LDS: this thread's four items' codes, their rows' pieces, the adds
-    auto sum_table = [&](int t) {
-        const unsigned char *cur = (t & 1) ? buf1 : buf0;
-        const uint16_t *cc = (t & 1) ? codes1 : codes0;
+
+    // prologue: table 0 in LDS with its codes; table 1's chunk and record on their way
+    issue_table(0);
+    load_code(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    store_code(0);
+    if (a.tables > 1) {
+        issue_table(1);
+        load_code(1);
+    }
+    meet(a.tables > 1);  // table 1's three loads may stay in flight
+    for (int t = 0; t < a.tables; ++t) {
+        // iteration t: table t + 1's code stored (its loads, issued an
+        // iteration ago, waited for), table t read, table t + 2's loads
+        // issued, table t summed, and the workgroup meets with table t + 2's
+        // loads in flight
+        if (t + 1 < a.tables) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            store_code(t + 1);
+        }
+        // table t's codes and row pieces are read before table t + 2's loads
+        // are issued: an LDS read after an LDS-direct load waits for it (the
+        // compiler cannot tell the buffers apart), so the loads overlap the
+        // adds and the barrier instead
+        const unsigned char *cur = lds + (t % kStreamBufs) * kStreamBufBytes;
+        const uint16_t *cc = codes + (t % kStreamBufs) * M;
         const vec_t<uint16_t, 4> cv = *reinterpret_cast<const vec_t<uint16_t, 4> *>(cc + slot * kStreamIpt);
         vec_t<uint32_t, 4> w[kStreamIpt];
 #pragma unroll
-        for (int k = 0; k < kStreamIpt; ++k) w[k] = *reinterpret_cast<const vec_t<uint32_t, 4> *>(cur + cv[k] * a.pitch + piece * 16);
+        for (int k = 0; k < kStreamIpt; ++k)
+            w[k] = *reinterpret_cast<const vec_t<uint32_t, 4> *>(cur + cv[k] * kStreamChunkBytes + piece * 16);
+        const bool more = t + 2 < a.tables;
+        if (more) {
+            issue_table(t + 2);
+            load_code(t + 2);
+        }
 #pragma unroll
         for (int k = 0; k < kStreamIpt; ++k) {
             if constexpr (sizeof(T) == 2) {
@@ -596,34 +639,9 @@ __global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel
                 }
             first_block = 0;
         }
-    };
-
-    // prologue: table 0 in LDS, table 1 in stage a, table 2 in stage b.
-    // Iteration t stores table t + 1 (loaded two iterations earlier) into
-    // the other LDS buffer, loads table t + 3 into the stage it freed, sums
-    // table t, and ends on a barrier.
-    load_table(0, stage_a, code_a);
-    store_table(0, stage_a, code_a);
-    if (a.tables > 1) load_table(1, stage_a, code_a);
-    if (a.tables > 2) load_table(2, stage_b, code_b);
-    __syncthreads();
-    for (int t = 0; t < a.tables; t += 2) {
-        if (t + 1 < a.tables) {
-            store_table(t + 1, stage_a, code_a);
-            if (t + 3 < a.tables) load_table(t + 3, stage_a, code_a);
-        }
-        sum_table(t);
-        __syncthreads();
-        if (t + 1 < a.tables) {
-            if (t + 2 < a.tables) {
-                store_table(t + 2, stage_b, code_b);
-                if (t + 4 < a.tables) load_table(t + 4, stage_b, code_b);
-            }
-            sum_table(t + 1);
-            __syncthreads();
-        }
+        meet(more);
     }
-    const int col = chunk * kStreamCols + piece * PE;
+    const int col = chunk * COLS + piece * PE;
 #pragma unroll
     for (int k = 0; k < kStreamIpt; ++k) {
         const int b = b0 + slot * kStreamIpt + k;
@@ -759,15 +777,12 @@ ForwardPlan plan_forward(const Dims &d) {
     // records): large batches over a LUT far beyond the L2, rows of whole
     // 64-column chunks, at most 256 rows per table
     const long long lut_bytes = static_cast<long long>(d.tables) * d.rows * d.out_f * esize;
-    p.stream_ok = d.items >= kStreamMinItems && d.out_f % kStreamCols == 0 && d.rows <= 256 &&
+    p.stream_ok = d.items >= kStreamMinItems && (d.out_f * esize) % kStreamChunkBytes == 0 && d.rows <= 256 &&
                   lut_bytes >= kStreamMinLutBytes;
     if (p.stream_ok) {
-        const int pieces = kStreamCols * esize / 16;
-        const int m = (kStreamThreads / pieces) * kStreamIpt;
-        p.stream_pitch = kStreamCols * esize + 16;  // a 16-byte pad staggers the rows over the LDS banks
-        p.stream_nblk = (d.items + m - 1) / m;
-        p.stream_blocks = p.stream_nblk * (d.out_f / kStreamCols);
-        p.stream_lds = 2 * d.rows * p.stream_pitch + 2 * m * 2;
+        p.stream_nblk = (d.items + kStreamItems - 1) / kStreamItems;
+        p.stream_blocks = p.stream_nblk * (d.out_f * esize / kStreamChunkBytes);
+        p.stream_lds = kStreamLds;
         p.route_block_items = 16;
         while (p.route_block_items > 1 && p.route_block_items * d.in_f * 4 > 64 * 1024) p.route_block_items >>= 1;
         p.route_lds = p.route_block_items * d.in_f * 4;
@@ -813,8 +828,7 @@ hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, c
                                          dim3(kRouteRecThreads), p.route_lds, stream, r);
             e != hipSuccess)
             return e;
-        StreamArgs g{lut, a.rec, out, scale, d.items, d.out_f, d.tables, d.rows, p.stream_nblk, p.per_wave,
-                     p.stream_pitch};
+        StreamArgs g{lut, a.rec, out, scale, d.items, d.out_f, d.tables, d.rows, p.stream_nblk, p.per_wave};
         return d.lut_dtype == TROPNN_LUT_F16 ? launch_stream<_Float16>(g, p, stream) : launch_stream<float>(g, p, stream);
     }
     if (d.lut_dtype == TROPNN_LUT_F16) {

@@ -41,7 +41,6 @@ struct ForwardPlan {
     // the records, then one workgroup per (item block, 64-column chunk)
     // walks the tables with each table's LUT chunk in LDS
     bool stream_ok;
-    int stream_pitch;       // LDS bytes per staged row
     int stream_nblk;        // item blocks
     int stream_blocks;      // workgroups
     int stream_lds;
