@@ -579,11 +579,14 @@ def test_backward_is_deterministic():
         assert torch.equal(a, b)
 
 
-def test_anchor_index_matches_numpy():
+@pytest.mark.parametrize("i,t,c", [(37, 29, 5), (2000, 300, 8), (8192, 600, 8)])
+def test_anchor_index_matches_numpy(i, t, c):
+    """The inverse anchor index against numpy: one LDS chunk of anchors,
+    several chunks with two features per thread, and in_features = 8192
+    (eight features per thread)."""
     from tropnn_amd.backends.pairwise_hip import anchor_index
 
     gen = torch.Generator().manual_seed(3)
-    i, t, c = 37, 29, 5
     anchors = torch.randint(0, i, (t, c, 2), generator=gen)
     offsets, entries = anchor_index(anchors.to(DEV), i)
     offsets, entries = offsets.cpu().numpy(), entries.cpu().numpy()

@@ -1198,29 +1198,62 @@ __global__ __launch_bounds__(kScatterThreads) void pairwise_bwd_scatter_kernel(S
 
 // Inverse anchor index: for every input feature f, the entries
 // ((t * C + c) << 1) | side of the anchors[t][c][side] equal to f, in
-// increasing order. One thread per feature scans the anchors, so the order is
-// fixed.
-__global__ __launch_bounds__(256) void anchor_index_kernel(const int64_t *anchors, int in_f, int tables, int comps,
-                                                          int32_t *offsets, int32_t *entries) {
+// increasing order. Thread tid owns features tid, tid + 1024, ... (at most
+// 8: in_features <= 8192) and scans the anchors in order, so the order is
+// fixed; the anchors pass through LDS in chunks as int32 (-1 outside
+// [0, in_f)), so every scan step is one broadcast LDS read for the wave.
+constexpr int kIdxThreads = 1024;
+constexpr int kIdxChunk = 4096;    // anchors per LDS chunk
+constexpr int kIdxMaxFeat = 8;     // features per thread
+
+__global__ __launch_bounds__(kIdxThreads) void anchor_index_kernel(const int64_t *anchors, int in_f, int tables,
+                                                                  int comps, int32_t *offsets, int32_t *entries) {
     extern __shared__ __align__(16) unsigned char lds[];
-    int *count = reinterpret_cast<int *>(lds);  // [in_f + 1]
-    const int n = tables * comps * 2;
-    for (int f = threadIdx.x; f < in_f; f += blockDim.x) {
-        int cnt = 0;
-        for (int k = 0; k < n; ++k) cnt += anchors[k] == f;
-        count[f] = cnt;
-    }
-    __syncthreads();
-    if (threadIdx.x < kWave) wave_exclusive_scan(count, in_f, threadIdx.x);
-    __syncthreads();
-    for (int f = threadIdx.x; f <= in_f; f += blockDim.x) offsets[f] = count[f];
-    for (int f = threadIdx.x; f < in_f; f += blockDim.x) {
-        int pos = count[f];
-        for (int k = 0; k < n; ++k)
-            if (anchors[k] == f) entries[pos++] = k;  // k = ((t * C + c) << 1) | side
+    int *count = reinterpret_cast<int *>(lds);              // [in_f + 1]
+    int *chunk = count + ((in_f + 1 + 3) & ~3);             // [kIdxChunk]
+    const int n = tables * comps * 2, tid = threadIdx.x;
+    int cnt[kIdxMaxFeat], pos[kIdxMaxFeat];
+#pragma unroll
+    for (int j = 0; j < kIdxMaxFeat; ++j) cnt[j] = 0;
+    // pass 0 counts each owned feature's entries, pass 1 writes them
+    for (int pass = 0; pass < 2; ++pass) {
+        for (int k0 = 0; k0 < n; k0 += kIdxChunk) {
+            const int m = min(kIdxChunk, n - k0);
+            __syncthreads();  // the previous chunk is read
+            for (int k = tid; k < m; k += kIdxThreads) {
+                const int64_t v = anchors[k0 + k];
+                chunk[k] = (v >= 0 && v < in_f) ? static_cast<int>(v) : -1;
+            }
+            __syncthreads();
+            for (int k = 0; k < m; ++k) {
+                const int v = chunk[k];
+#pragma unroll
+                for (int j = 0; j < kIdxMaxFeat; ++j) {
+                    if (v == tid + j * kIdxThreads) {
+                        if (pass == 0)
+                            ++cnt[j];
+                        else
+                            entries[pos[j]++] = k0 + k;  // k = ((t * C + c) << 1) | side
+                    }
+                }
+            }
+        }
+        if (pass == 0) {
+#pragma unroll
+            for (int j = 0; j < kIdxMaxFeat; ++j)
+                if (tid + j * kIdxThreads < in_f) count[tid + j * kIdxThreads] = cnt[j];
+            __syncthreads();
+            if (tid < kWave) wave_exclusive_scan(count, in_f, tid);
+            __syncthreads();
+            for (int f = tid; f <= in_f; f += kIdxThreads) offsets[f] = count[f];
+#pragma unroll
+            for (int j = 0; j < kIdxMaxFeat; ++j) pos[j] = tid + j * kIdxThreads < in_f ? count[tid + j * kIdxThreads] : 0;
+        }
     }
 }
 
+// Kernels that may need more than the default 64 KB of dynamic LDS opt in
+// once per size.
 template <typename K>
 hipError_t allow_lds(K kernel, int bytes) {
     return allow_dynamic_lds(reinterpret_cast<const void *>(kernel), bytes);
@@ -1317,8 +1350,8 @@ hipError_t launch_fill_zero(float *p, size_t n, hipStream_t stream) {
 
 hipError_t launch_anchor_index(const int64_t *anchors, int in_f, int tables, int comps, int32_t *offsets,
                                int32_t *entries, hipStream_t stream) {
-    hipLaunchKernelGGL(anchor_index_kernel, dim3(1), dim3(256), (in_f + 1) * 4 + 64, stream, anchors, in_f, tables,
-                       comps, offsets, entries);
+    hipLaunchKernelGGL(anchor_index_kernel, dim3(1), dim3(kIdxThreads), (((in_f + 1 + 3) & ~3) + kIdxChunk) * 4,
+                       stream, anchors, in_f, tables, comps, offsets, entries);
     return hipGetLastError();
 }
 
