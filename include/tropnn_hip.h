@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TROPNN_HIP_ABI_VERSION 7
+#define TROPNN_HIP_ABI_VERSION 8
 
 /* status codes */
 #define TROPNN_OK 0
@@ -175,6 +175,30 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
                                  const int32_t *index_offsets, const int32_t *index_entries, float output_scale,
                                  int ste_mode, int surrogate, float *grad_latent, float *grad_thresholds,
                                  float *grad_lut, void *workspace, size_t workspace_bytes, tropnn_stream_t stream);
+
+/*
+ * Adam / AdamW step over n_tensors f32 tensors: the optimizer of the
+ * classifier's training step. The reference trains it with
+ * torch.optim.AdamW(weight_decay=0) (examples/emnist.py:310), i.e. torch's
+ * Adam update; this is that update (non-amsgrad, op order of torch's
+ * single-tensor Adam) in one launch over all the tensors' elements:
+ *   weight_decay != 0: decoupled ? p *= 1 - lr * wd : g += wd * p
+ *   m = lerp(m, g, 1 - beta1);  v = v beta2 + (1 - beta2) g^2
+ *   p -= (lr / (1 - beta1^t)) * (m / (sqrt(v) / sqrt(1 - beta2^t) + eps))
+ * with t = *steps[k] + 1 read from device memory, after which *steps[k] = t
+ * (a second launch): a step captured in a HIP graph replays with the current
+ * counts. lr and the other scalars are taken by value; as in torch, the bias
+ * corrections are formed in f64 and each per-element op is one f32 op (no
+ * fused multiply-adds).
+ * params, grads, exp_avgs, exp_avg_sqs, steps: HOST arrays of n_tensors
+ * DEVICE pointers (f32, 4-byte aligned; numels[k] elements each, one float
+ * for steps[k]); the steps pointers must be distinct. exp_avgs and
+ * exp_avg_sqs start at zero and the step counters at 0.
+ */
+int tropnn_hip_adam_step(int n_tensors, float *const *params, const float *const *grads, float *const *exp_avgs,
+                         float *const *exp_avg_sqs, const int64_t *numels, float *const *steps, double lr,
+                         double beta1, double beta2, double eps, double weight_decay, int decoupled_weight_decay,
+                         tropnn_stream_t stream);
 
 /*
  * Profiling hook (no counterpart in the reference, whose harness times whole

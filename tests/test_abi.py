@@ -156,3 +156,33 @@ def test_event_hook_rejects_bad_kernel(lib):
     assert lib.tropnn_hip_arm_kernel_events(8, None, None) == 1
     assert lib.tropnn_hip_arm_kernel_events(0, ctypes.c_void_p(8), None) == 1
     assert lib.tropnn_hip_arm_kernel_events(0, None, None) == 0
+
+
+def test_adam_rejects_bad_arguments(lib):
+    fn = lib.tropnn_hip_adam_step
+    one = ctypes.c_void_p * 1
+    good = one(256)
+    numel = (ctypes.c_int64 * 1)(4)
+    base = [1, good, good, good, good, numel, good, 1e-3, 0.9, 0.999, 1e-8, 0.0, 0, None]
+    assert fn(-1, *base[1:]) == 1
+    assert fn(0, None, None, None, None, None, None, *base[7:]) == 0  # nothing to do, no launch
+    for k in range(1, 7):
+        args = list(base)
+        args[k] = None
+        assert fn(*args) == 1, k
+    for k, bad in ((7, -1.0), (8, 1.0), (9, -0.1), (10, -1e-8), (11, -0.5)):
+        args = list(base)
+        args[k] = bad
+        assert fn(*args) == 1 and "beta" in _err(lib), k
+    args = list(base)
+    args[6] = one(258)  # misaligned step counter
+    assert fn(*args) == 1 and "steps[0]" in _err(lib)
+    args = list(base)
+    args[1] = one(258)  # misaligned parameter
+    assert fn(*args) == 1 and "aligned" in _err(lib)
+    args = list(base)
+    args[2] = one(None)  # NULL gradient of a non-empty tensor
+    assert fn(*args) == 1 and "NULL" in _err(lib)
+    args = list(base)
+    args[5] = (ctypes.c_int64 * 1)(-4)
+    assert fn(*args) == 1 and "numels" in _err(lib)

@@ -3,8 +3,11 @@ comparator route, LUT gather-sum and min-margin STE backward as gfx950 HIP
 kernels in libtropnn_hip.so (C ABI: include/tropnn_hip.h)."""
 from .backends import has_pairwise_hip, pairwise_hip, pairwise_hip_forward, pairwise_hip_route
 from .layers import PairwiseLinear, RoutedLinearBase
+from .optim import FusedAdam, FusedAdamW
 
 __all__ = [
+    "FusedAdam",
+    "FusedAdamW",
     "PairwiseLinear",
     "RoutedLinearBase",
     "has_pairwise_hip",

@@ -26,7 +26,7 @@ from typing import Any
 import torch
 from torch import Tensor
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 LUT_F32, LUT_F16 = 0, 1
 SURROGATE_IDS = {"fast_sigmoid_odd": 0, "izhikevich": 1}
 STE_MIN_MARGIN, STE_FULL = 0, 1
@@ -55,6 +55,7 @@ EXPORTED_SYMBOLS = (
     "tropnn_hip_pairwise_backward",
     "tropnn_hip_build_anchor_index",
     "tropnn_hip_arm_kernel_events",
+    "tropnn_hip_adam_step",
 )
 KERNEL_IDS = {
     "forward": 0,
@@ -96,6 +97,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tropnn_hip_pairwise_backward.restype = i
     lib.tropnn_hip_arm_kernel_events.argtypes = [i, p, p]
     lib.tropnn_hip_arm_kernel_events.restype = i
+    d = ctypes.c_double
+    lib.tropnn_hip_adam_step.argtypes = [i, p, p, p, p, p, p, d, d, d, d, d, i, p]
+    lib.tropnn_hip_adam_step.restype = i
 
 
 def load_library() -> ctypes.CDLL:

@@ -115,6 +115,33 @@ int tropnn_hip_arm_kernel_events(int kernel, void *start_event, void *stop_event
 }
 
 
+int tropnn_hip_adam_step(int n_tensors, float *const *params, const float *const *grads, float *const *exp_avgs,
+                         float *const *exp_avg_sqs, const int64_t *numels, float *const *steps, double lr,
+                         double beta1, double beta2, double eps, double weight_decay, int decoupled_weight_decay,
+                         tropnn_stream_t stream) {
+    if (n_tensors < 0) return fail(TROPNN_ERR_INVALID_ARGUMENT, "n_tensors must be >= 0, got %d", n_tensors);
+    if (n_tensors > 0 && (!params || !grads || !exp_avgs || !exp_avg_sqs || !numels || !steps))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "params, grads, exp_avgs, exp_avg_sqs, numels and steps must be non-NULL");
+    if (!(lr >= 0.0) || !(beta1 >= 0.0 && beta1 < 1.0) || !(beta2 >= 0.0 && beta2 < 1.0) || !(eps >= 0.0) ||
+        !(weight_decay >= 0.0))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "need lr >= 0, 0 <= beta1, beta2 < 1, eps >= 0, weight_decay >= 0");
+    for (int k = 0; k < n_tensors; ++k) {
+        if (!steps[k] || misaligned(steps[k], 4))
+            return fail(TROPNN_ERR_INVALID_ARGUMENT, "steps[%d] must be a 4-byte aligned device float", k);
+        if (numels[k] < 0) return fail(TROPNN_ERR_INVALID_ARGUMENT, "numels[%d] < 0", k);
+        if (numels[k] == 0) continue;
+        if (!params[k] || !grads[k] || !exp_avgs[k] || !exp_avg_sqs[k])
+            return fail(TROPNN_ERR_INVALID_ARGUMENT, "tensor %d has a NULL pointer", k);
+        if (misaligned(params[k], 4) || misaligned(grads[k], 4) || misaligned(exp_avgs[k], 4) ||
+            misaligned(exp_avg_sqs[k], 4))
+            return fail(TROPNN_ERR_INVALID_ARGUMENT, "tensor %d is not 4-byte aligned", k);
+    }
+    hipError_t e = tropnn::launch_adam(n_tensors, params, grads, exp_avgs, exp_avg_sqs, numels, steps, lr, beta1,
+                                       beta2, eps, weight_decay, decoupled_weight_decay, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail("adam launch", e);
+    return ok();
+}
+
 int tropnn_hip_abi_version(void) { return TROPNN_HIP_ABI_VERSION; }
 
 const char *tropnn_hip_last_error(void) { return g_last_error.c_str(); }

@@ -150,6 +150,15 @@ hipError_t launch_kernel(int kernel_id, F kernel, dim3 grid, dim3 block, uint32_
 // Writes n zeros with a kernel (no hipMemsetAsync node in captured graphs).
 hipError_t launch_fill_zero(float *p, size_t n, hipStream_t stream);
 
+// Adam / AdamW step over n f32 tensors (host arrays of device pointers),
+// kAdamGroup tensors per launch, then launches advancing each tensor's device
+// step counter.
+constexpr int kAdamGroup = 16;
+hipError_t launch_adam(int n, float *const *params, const float *const *grads, float *const *exp_avgs,
+                       float *const *exp_avg_sqs, const int64_t *numels, float *const *steps, double lr,
+                       double beta1, double beta2, double eps, double weight_decay, int decoupled,
+                       hipStream_t stream);
+
 // Opts `kernel` into `bytes` of dynamic LDS when that is above the default
 // 64 KB, once per kernel and size (thread-safe; keyed by the kernel's address).
 hipError_t allow_dynamic_lds(const void *kernel, int bytes);
