@@ -579,11 +579,13 @@ def test_backward_is_deterministic():
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("i,t,c", [(37, 29, 5), (2000, 300, 8), (8192, 600, 8)])
+@pytest.mark.parametrize("i,t,c", [(37, 29, 5), (2000, 300, 8), (8192, 600, 8), (1, 70, 3), (3, 700, 8)])
 def test_anchor_index_matches_numpy(i, t, c):
-    """The inverse anchor index against numpy: one LDS chunk of anchors,
-    several chunks with two features per thread, and in_features = 8192
-    (eight features per thread)."""
+    """The inverse anchor index (a stable counting sort) against numpy: one
+    chunk of 1024 anchors, several chunks, in_features = 8192, one feature
+    (no feature bits to compare), and three features shared by 11,200
+    anchors (long runs of equal features inside every wave and across
+    chunks)."""
     from tropnn_amd.backends.pairwise_hip import anchor_index
 
     gen = torch.Generator().manual_seed(3)

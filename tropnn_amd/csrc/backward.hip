@@ -1198,56 +1198,55 @@ __global__ __launch_bounds__(kScatterThreads) void pairwise_bwd_scatter_kernel(S
 
 // Inverse anchor index: for every input feature f, the entries
 // ((t * C + c) << 1) | side of the anchors[t][c][side] equal to f, in
-// increasing order. Thread tid owns features tid, tid + 1024, ... (at most
-// 8: in_features <= 8192) and scans the anchors in order, so the order is
-// fixed; the anchors pass through LDS in chunks as int32 (-1 outside
-// [0, in_f)), so every scan step is one broadcast LDS read for the wave.
+// increasing order: a stable counting sort in one workgroup. LDS counts per
+// feature (integer atomics), one wave's exclusive scan gives the offsets, and
+// the entries are placed in chunks of 1024 in entry order: inside a wave the
+// lanes with the same feature are found with one ballot per feature bit (a
+// lane's rank is the number of such lanes below it), and the chunk's waves
+// take turns, each advancing the features' LDS cursors, so the order is fixed.
+// Anchors outside [0, in_f) are left out.
 constexpr int kIdxThreads = 1024;
-constexpr int kIdxChunk = 4096;    // anchors per LDS chunk
-constexpr int kIdxMaxFeat = 8;     // features per thread
 
 __global__ __launch_bounds__(kIdxThreads) void anchor_index_kernel(const int64_t *anchors, int in_f, int tables,
                                                                   int comps, int32_t *offsets, int32_t *entries) {
     extern __shared__ __align__(16) unsigned char lds[];
-    int *count = reinterpret_cast<int *>(lds);              // [in_f + 1]
-    int *chunk = count + ((in_f + 1 + 3) & ~3);             // [kIdxChunk]
-    const int n = tables * comps * 2, tid = threadIdx.x;
-    int cnt[kIdxMaxFeat], pos[kIdxMaxFeat];
-#pragma unroll
-    for (int j = 0; j < kIdxMaxFeat; ++j) cnt[j] = 0;
-    // pass 0 counts each owned feature's entries, pass 1 writes them
-    for (int pass = 0; pass < 2; ++pass) {
-        for (int k0 = 0; k0 < n; k0 += kIdxChunk) {
-            const int m = min(kIdxChunk, n - k0);
-            __syncthreads();  // the previous chunk is read
-            for (int k = tid; k < m; k += kIdxThreads) {
-                const int64_t v = anchors[k0 + k];
-                chunk[k] = (v >= 0 && v < in_f) ? static_cast<int>(v) : -1;
-            }
-            __syncthreads();
-            for (int k = 0; k < m; ++k) {
-                const int v = chunk[k];
-#pragma unroll
-                for (int j = 0; j < kIdxMaxFeat; ++j) {
-                    if (v == tid + j * kIdxThreads) {
-                        if (pass == 0)
-                            ++cnt[j];
-                        else
-                            entries[pos[j]++] = k0 + k;  // k = ((t * C + c) << 1) | side
-                    }
-                }
-            }
+    int *cursor = reinterpret_cast<int *>(lds);  // [in_f + 1]: counts, then each feature's next position
+    const int n = tables * comps * 2, tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    for (int f = tid; f <= in_f; f += kIdxThreads) cursor[f] = 0;
+    __syncthreads();
+    for (int k = tid; k < n; k += kIdxThreads) {
+        const int64_t v = anchors[k];
+        if (v >= 0 && v < in_f) atomicAdd(&cursor[v], 1);
+    }
+    __syncthreads();
+    if (tid < kWave) wave_exclusive_scan(cursor, in_f, tid);
+    __syncthreads();
+    for (int f = tid; f <= in_f; f += kIdxThreads) offsets[f] = cursor[f];
+    const int fbits = in_f > 1 ? 32 - __clz(in_f - 1) : 0;
+    const uint64_t below = (1ull << lane) - 1ull, upto = below | (1ull << lane);
+    for (int k0 = 0; k0 < n; k0 += kIdxThreads) {
+        const int k = k0 + tid;
+        int v = -1;
+        if (k < n) {
+            const int64_t a = anchors[k];
+            v = a >= 0 && a < in_f ? static_cast<int>(a) : -1;
         }
-        if (pass == 0) {
-#pragma unroll
-            for (int j = 0; j < kIdxMaxFeat; ++j)
-                if (tid + j * kIdxThreads < in_f) count[tid + j * kIdxThreads] = cnt[j];
+        const bool valid = v >= 0;
+        uint64_t same = __ballot(valid);
+        for (int b = 0; b < fbits; ++b) {
+            const bool bit = (v >> b) & 1;
+            const uint64_t ones = __ballot(valid && bit);
+            same &= bit ? ones : ~ones;
+        }
+        const int rank = __popcll(same & below);
+        const bool last = (same & ~upto) == 0;
+        for (int w = 0; w < kIdxThreads / kWave; ++w) {
+            if (wave == w && valid) {
+                const int pos = cursor[v] + rank;  // every lane reads before the group's last lane writes
+                entries[pos] = k;
+                if (last) cursor[v] = pos + 1;
+            }
             __syncthreads();
-            if (tid < kWave) wave_exclusive_scan(count, in_f, tid);
-            __syncthreads();
-            for (int f = tid; f <= in_f; f += kIdxThreads) offsets[f] = count[f];
-#pragma unroll
-            for (int j = 0; j < kIdxMaxFeat; ++j) pos[j] = tid + j * kIdxThreads < in_f ? count[tid + j * kIdxThreads] : 0;
         }
     }
 }
@@ -1350,8 +1349,8 @@ hipError_t launch_fill_zero(float *p, size_t n, hipStream_t stream) {
 
 hipError_t launch_anchor_index(const int64_t *anchors, int in_f, int tables, int comps, int32_t *offsets,
                                int32_t *entries, hipStream_t stream) {
-    hipLaunchKernelGGL(anchor_index_kernel, dim3(1), dim3(kIdxThreads), (((in_f + 1 + 3) & ~3) + kIdxChunk) * 4,
-                       stream, anchors, in_f, tables, comps, offsets, entries);
+    hipLaunchKernelGGL(anchor_index_kernel, dim3(1), dim3(kIdxThreads), (in_f + 1) * 4, stream, anchors, in_f,
+                       tables, comps, offsets, entries);
     return hipGetLastError();
 }
 
