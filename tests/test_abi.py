@@ -186,3 +186,17 @@ def test_adam_rejects_bad_arguments(lib):
     args = list(base)
     args[5] = (ctypes.c_int64 * 1)(-4)
     assert fn(*args) == 1 and "numels" in _err(lib)
+
+
+def test_cross_entropy_rejects_bad_arguments(lib):
+    fn = lib.tropnn_hip_cross_entropy
+    base = [512, 10, 256, 256, -100, 256, 256, None]
+    assert fn(0, *base[1:]) == 1 and "rows" in _err(lib)
+    assert fn(512, 0, *base[2:]) == 1 and "classes" in _err(lib)
+    for k in (2, 3, 5, 6):
+        args = list(base)
+        args[k] = None
+        assert fn(*args) == 1 and "NULL" in _err(lib), k
+    args = list(base)
+    args[3] = 260  # int64 targets need 8-byte alignment
+    assert fn(*args) == 1 and "align" in _err(lib)

@@ -2,7 +2,8 @@
 784 -> 128 -> 128 -> 10 (three PairwiseLinear layers, T = 136, C = 6, seeds
 0, 1, 2), batch 512 of sparse inputs, cross entropy, Adam lr 1e-3
 (examples/emnist.py:121-175, 194-214, 310), against the oracle stack on the
-CPU; the HIP side steps with FusedAdam, the oracle with torch.optim.Adam. Sparse inputs give exact-zero margins (argmin ties, u = 0) in layer 1,
+CPU; the HIP side runs tropnn_amd.cross_entropy and FusedAdam, the oracle
+F.cross_entropy and torch.optim.Adam. Sparse inputs give exact-zero margins (argmin ties, u = 0) in layer 1,
 and layer 3 has O = 10."""
 from __future__ import annotations
 
@@ -12,7 +13,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from oracle import pairwise_torch as orc
-from tropnn_amd import FusedAdam
+from tropnn_amd import FusedAdam, cross_entropy
 from tropnn_amd.examples import EmnistPairwiseClassifier, make_c5_batch, train_step
 
 pytestmark = pytest.mark.gpu
@@ -80,7 +81,7 @@ def test_c5_training_steps_match_oracle():
     opt_hip = FusedAdam(hip.parameters(), lr=1e-3)  # the library's Adam kernel, as in the c5 benchmark
     before = [p.detach().clone() for p in ref.parameters()]
     loss_ref = train_step(ref, opt_ref, x, y)
-    loss_hip = train_step(hip, opt_hip, x.to(DEV), y.to(DEV))
+    loss_hip = train_step(hip, opt_hip, x.to(DEV), y.to(DEV), loss_fn=cross_entropy)  # as the c5 benchmark
     check_step(ref, hip, loss_ref, loss_hip)
     for p0, pr, ph in zip(before, ref.parameters(), hip.parameters()):
         g = pr.grad.abs()

@@ -26,7 +26,7 @@ from typing import Any
 import torch
 from torch import Tensor
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 LUT_F32, LUT_F16 = 0, 1
 SURROGATE_IDS = {"fast_sigmoid_odd": 0, "izhikevich": 1}
 STE_MIN_MARGIN, STE_FULL = 0, 1
@@ -56,6 +56,7 @@ EXPORTED_SYMBOLS = (
     "tropnn_hip_build_anchor_index",
     "tropnn_hip_arm_kernel_events",
     "tropnn_hip_adam_step",
+    "tropnn_hip_cross_entropy",
 )
 KERNEL_IDS = {
     "forward": 0,
@@ -100,6 +101,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     d = ctypes.c_double
     lib.tropnn_hip_adam_step.argtypes = [i, p, p, p, p, p, p, d, d, d, d, d, i, p]
     lib.tropnn_hip_adam_step.restype = i
+    lib.tropnn_hip_cross_entropy.argtypes = [i64, i64, p, p, i64, p, p, p]
+    lib.tropnn_hip_cross_entropy.restype = i
 
 
 def load_library() -> ctypes.CDLL:

@@ -142,6 +142,21 @@ int tropnn_hip_adam_step(int n_tensors, float *const *params, const float *const
     return ok();
 }
 
+int tropnn_hip_cross_entropy(int64_t rows, int64_t classes, const float *logits, const int64_t *target,
+                             int64_t ignore_index, float *loss, float *grad_logits, tropnn_stream_t stream) {
+    if (rows < 1) return fail(TROPNN_ERR_INVALID_ARGUMENT, "rows must be >= 1, got %lld", (long long)rows);
+    if (classes < 1 || classes > (1 << 20))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "classes must be in [1, 2^20], got %lld", (long long)classes);
+    if (!logits || !target || !loss || !grad_logits)
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "logits, target, loss and grad_logits must be non-NULL");
+    if (misaligned(logits, 4) || misaligned(target, 8) || misaligned(loss, 4) || misaligned(grad_logits, 4))
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "logits, loss and grad_logits need 4-byte, target 8-byte alignment");
+    hipError_t e = tropnn::launch_cross_entropy(logits, target, rows, static_cast<int>(classes), ignore_index, loss,
+                                                grad_logits, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail("cross entropy launch", e);
+    return ok();
+}
+
 int tropnn_hip_abi_version(void) { return TROPNN_HIP_ABI_VERSION; }
 
 const char *tropnn_hip_last_error(void) { return g_last_error.c_str(); }

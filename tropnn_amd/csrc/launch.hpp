@@ -159,6 +159,11 @@ hipError_t launch_adam(int n, float *const *params, const float *const *grads, f
                        double beta1, double beta2, double eps, double weight_decay, int decoupled,
                        hipStream_t stream);
 
+// Mean cross entropy over `rows` rows of `classes` f32 logits and its
+// gradient, in one launch.
+hipError_t launch_cross_entropy(const float *logits, const int64_t *target, int64_t rows, int classes,
+                                int64_t ignore_index, float *loss, float *grad_logits, hipStream_t stream);
+
 // Opts `kernel` into `bytes` of dynamic LDS when that is above the default
 // 64 KB, once per kernel and size (thread-safe; keyed by the kernel's address).
 hipError_t allow_dynamic_lds(const void *kernel, int bytes);

@@ -68,11 +68,13 @@ def make_c5_batch(batch: int = 512, input_dim: int = 784, num_classes: int = 10,
     return x, y
 
 
-def train_step(model: nn.Module, optimizer: torch.optim.Optimizer, x: Tensor, y: Tensor) -> Tensor:
-    """One step of the reference's training loop; returns the loss tensor."""
+def train_step(model: nn.Module, optimizer: torch.optim.Optimizer, x: Tensor, y: Tensor, loss_fn=F.cross_entropy) -> Tensor:
+    """One step of the reference's training loop (examples/emnist.py:218-224);
+    returns the loss tensor. loss_fn defaults to the reference's
+    F.cross_entropy; tropnn_amd.cross_entropy is its one-launch HIP form."""
     optimizer.zero_grad(set_to_none=True)
     logits = model(x)
-    loss = F.cross_entropy(logits, y)
+    loss = loss_fn(logits, y)
     loss.backward()
     optimizer.step()
     return loss
