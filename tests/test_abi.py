@@ -78,7 +78,9 @@ def test_workspace_size(lib):
 
     assert ws(64, 1024, 4096, 512, 8, ph.LUT_F16, ph.STE_MIN_MARGIN) == general(64, 4096, 512, 256, 8, 64, False)
     assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_FULL) == general(512, 128, 136, 64, 6, 64, True)
-    assert ws(33, 20, 10, 7, 3, ph.LUT_F32, ph.STE_MIN_MARGIN) == general(33, 10, 7, 8, 3, 16, False)
+    assert ws(33, 20, 10, 7, 3, ph.LUT_F32, ph.STE_MIN_MARGIN) == 7 * 33 * 8  # fused, 2 columns per lane
+    assert ws(33, 20, 34, 7, 3, ph.LUT_F32, ph.STE_MIN_MARGIN) == general(33, 34, 7, 8, 3, 64, False)
+    assert ws(33, 20, 5, 7, 3, ph.LUT_F32, ph.STE_MIN_MARGIN) == general(33, 5, 7, 8, 3, 8, False)
     assert ws(512, 128, 128, 136, 9, ph.LUT_F32, ph.STE_MIN_MARGIN) == 0
     assert ws(512, 128, 128, 136, 6, ph.LUT_F32, 7) == 0 and "ste_mode" in _err(lib)
 

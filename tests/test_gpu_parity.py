@@ -261,7 +261,10 @@ def test_train_parity(i, o, t, c, b, thr_std):
     "i,o,t,c,b,min_margin,surrogate,lut_dtype",
     [
         (128, 128, 136, 6, 512, True, "izhikevich", "f32"),  # fused path
-        (40, 10, 33, 4, 70, True, "izhikevich", "f32"),  # general path
+        (40, 10, 33, 4, 70, True, "izhikevich", "f32"),  # fused path, 2 columns per lane
+        (40, 34, 33, 4, 70, True, "izhikevich", "f32"),  # general path (O % 4 != 0, O > 32)
+        (64, 30, 40, 8, 2100, True, "fast_sigmoid_odd", "f16"),  # fused, 2 columns per lane, R = 256, 3 tiles
+        (16, 2, 9, 2, 33, True, "fast_sigmoid_odd", "f32"),  # fused, one lane per row
         (128, 128, 136, 6, 256, False, "fast_sigmoid_odd", "f32"),  # full STE
         (64, 96, 20, 8, 50, False, "izhikevich", "f32"),
         (16, 7, 5, 1, 19, False, "fast_sigmoid_odd", "f32"),
@@ -271,7 +274,8 @@ def test_train_parity(i, o, t, c, b, thr_std):
         (100, 1000, 12, 7, 40, False, "fast_sigmoid_odd", "f16"),  # 8 f16 columns per lane
         (100, 1000, 12, 7, 300, True, "fast_sigmoid_odd", "f16"),  # general path, 16 column chunks
         (64, 300, 20, 8, 2100, True, "izhikevich", "f32"),  # general path, 5 chunks, 3 sort tiles
-        (40, 6, 50, 3, 500, True, "izhikevich", "f32"),  # general path, 4-lane row groups
+        (40, 3, 50, 3, 500, True, "izhikevich", "f32"),  # general path, 4-lane row groups
+        (40, 6, 50, 3, 500, True, "izhikevich", "f32"),  # fused path, 2 columns per lane
     ],
 )
 def test_train_parity_ste_variants(i, o, t, c, b, min_margin, surrogate, lut_dtype):
@@ -415,7 +419,8 @@ def test_large_batch_forward_multi_item(lut_dtype):
     "i,o,t,c,min_margin,surrogate",
     [
         (64, 32, 20, 5, True, "fast_sigmoid_odd"),
-        (64, 10, 20, 5, True, "fast_sigmoid_odd"),  # general backward path (O % 4 != 0)
+        (64, 10, 20, 5, True, "fast_sigmoid_odd"),  # fused backward, 2 columns per lane, 3 tiles
+        (64, 34, 20, 5, True, "fast_sigmoid_odd"),  # general backward path (O % 4 != 0, O > 32)
         (48, 24, 17, 6, False, "izhikevich"),  # full STE
     ],
 )

@@ -288,11 +288,12 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
     if (margins && misaligned(margins, 4))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "margins must be 4-byte aligned");
     const size_t esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
-    // fused path: LUT chunks of 4 elements, 16-byte grad rows and LUT-grad rows;
-    // general path: the item kernel's and the row kernel's pieces
-    const size_t lut_align = p.fused ? 4 * esize : static_cast<size_t>(p.rows_vec > p.item_vec ? p.rows_vec : p.item_vec) * esize;
-    const size_t gvec = p.fused ? 4 : static_cast<size_t>(p.rows_vec > p.item_vec ? p.rows_vec : p.item_vec);
-    const size_t lut_grad_vec = p.fused ? 4 : static_cast<size_t>(p.rows_vec);
+    // fused path: LUT chunks, grad-row and LUT-grad-row pieces of min(V, 4)
+    // elements; general path: the item kernel's and the row kernel's pieces
+    const size_t fchunk = p.fvec < 4 ? static_cast<size_t>(p.fvec) : 4;
+    const size_t lut_align = p.fused ? fchunk * esize : static_cast<size_t>(p.rows_vec > p.item_vec ? p.rows_vec : p.item_vec) * esize;
+    const size_t gvec = p.fused ? fchunk : static_cast<size_t>(p.rows_vec > p.item_vec ? p.rows_vec : p.item_vec);
+    const size_t lut_grad_vec = p.fused ? fchunk : static_cast<size_t>(p.rows_vec);
     if (misaligned(lut, lut_align) || misaligned(grad_output, gvec * 4) ||
         (grad_lut && misaligned(grad_lut, lut_grad_vec * 4)) || misaligned(route_record, 8))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "a device pointer is not aligned to its element/vector size");

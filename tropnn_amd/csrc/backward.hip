@@ -792,7 +792,7 @@ struct FusedArgs {
     uint32_t lut_bytes, g_bytes;
     uint32_t g_slice;     // bytes of G one workgroup touches (8 XCDs share the table workgroups)
     int surrogate;        // TROPNN_SURROGATE_*
-    uint64_t quad_magic;  // ceil(2^32 / (out_f / 4)): chunk index -> LUT row
+    uint64_t quad_magic;  // ceil(2^32 / (out_f / CH)): staging chunk index -> LUT row
     int items, out_f, tables, comps, rows;
     int slots;  // sorted-list capacity: a tile's items plus K - 1 padding slots per row
     int lut_off, cnt_off, off_off, sorted_off, u_off, dt_off, rowbuf_off, thr_off, wtot_off, part_off, brow_off;  // LDS bytes
@@ -815,7 +815,8 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
     constexpr int kWaves = kFusedThreads / kWave;
     constexpr int NG = kFusedThreads / S;  // row groups
     constexpr int K = kFusedFloats / V;  // items per batch
-    constexpr int kStage = 4;  // LUT chunks (4 elements) a thread stages, R * O <= 16384
+    constexpr int CH = V < 4 ? V : 4;  // elements per staging chunk: O % CH == 0, so none crosses a row
+    constexpr int kStage = 4;  // LUT chunks a thread stages: R * O <= 4096 * CH
     constexpr int P = S * V;   // LDS row pitch in floats
     static_assert(K <= S, "a batch's dots are scattered over the row group");
     extern __shared__ __align__(16) unsigned char lds[];
@@ -866,14 +867,14 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
     //    grad rows the walk gathers are L2 hits by then); the first ballots
     //    need the record only, and the LUT rows go to LDS after them
     uint64_t r0 = tid < a.items ? rec_t[tid] : 0ull;
-    float lv[kStage][4];
-    const int quads = R * O / 4;  // 4-element chunks; O % 4 == 0, so none crosses a row
+    float lv[kStage][CH];
+    const int quads = R * O / CH;  // CH-element chunks
     {
         const int tbase = t * R * O * static_cast<int>(sizeof(T));
 #pragma unroll
         for (int i = 0; i < kStage; ++i) {
             const int q = tid + i * kFusedThreads;
-            buffer_row<T, 4>(lut_rsrc, q < quads ? static_cast<uint32_t>(q) * 4u * sizeof(T) : kOutOfRange, tbase, lv[i]);
+            buffer_row<T, CH>(lut_rsrc, q < quads ? static_cast<uint32_t>(q) * CH * sizeof(T) : kOutOfRange, tbase, lv[i]);
         }
     }
     const uint32_t touch = static_cast<uint32_t>(t >> 3) * a.g_slice + tid * 128u;
@@ -883,17 +884,17 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
     for (int i = 0; i < kStage; ++i) {
         const int q = tid + i * kFusedThreads;
         if (q < quads) {
-            // row = q / (O / 4) by a host-computed reciprocal (exact for q < 2^16)
+            // row = q / (O / CH) by a host-computed reciprocal (exact for q < 2^16)
             const int row = static_cast<int>((static_cast<uint64_t>(q) * a.quad_magic) >> 32);
-            const int col = q * 4 - row * O;
-            vec_t<float, 4> w;
+            const int col = q * CH - row * O;
+            vec_t<float, CH> w;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) w[e] = lv[i][e];
-            *reinterpret_cast<vec_t<float, 4> *>(lut_s + row * P + col) = w;
+            for (int e = 0; e < CH; ++e) w[e] = lv[i][e];
+            *reinterpret_cast<vec_t<float, CH> *>(lut_s + row * P + col) = w;
         }
     }
     if (tid < R)
-        for (int e = O; e < P; e += 4) *reinterpret_cast<vec_t<float, 4> *>(lut_s + tid * P + e) = 0.f;
+        for (int e = O; e < P; e += CH) *reinterpret_cast<vec_t<float, CH> *>(lut_s + tid * P + e) = 0.f;
     if (!single)
         for (int k = tid * 4; k < R * P; k += kFusedThreads * 4) *reinterpret_cast<vec_t<float, 4> *>(rowbuf + k) = 0.f;
     if (tid < kWaves * 8) tp[tid] = 0.f;
@@ -1127,14 +1128,14 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
     //    step of the last tile), scaled, written once
     if (!single && a.grad_lut != nullptr) {
         __syncthreads();
-        constexpr int qp = P / 4;
+        constexpr int qp = P / CH;
         for (int unit = tid; unit < R * qp; unit += kFusedThreads) {
-            const int k = unit / qp, c0 = (unit % qp) * 4;
+            const int k = unit / qp, c0 = (unit % qp) * CH;
             if (c0 < O) {
-                float y[4];
+                float y[CH];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) y[e] = rowbuf[k * P + c0 + e] * a.scale;
-                store_f32_nt<4>(a.grad_lut + (static_cast<size_t>(t) * R + k) * O + c0, y);
+                for (int e = 0; e < CH; ++e) y[e] = rowbuf[k * P + c0 + e] * a.scale;
+                store_f32_nt<CH>(a.grad_lut + (static_cast<size_t>(t) * R + k) * O + c0, y);
             }
         }
     }
@@ -1314,6 +1315,7 @@ hipError_t launch_fused_vs(const FusedArgs &args, const BackwardPlan &p, hipStre
 
 template <typename T>
 hipError_t launch_fused_typed(const FusedArgs &args, const BackwardPlan &p, hipStream_t stream) {
+    if (p.fvec == 2) return launch_fused_vs<T, 2, 16>(args, p, stream);
     if (p.fvec == 4) return launch_fused_vs<T, 4, 16>(args, p, stream);
     if (p.fslices == 16) return launch_fused_vs<T, 8, 16>(args, p, stream);
     return launch_fused_vs<T, 8, 32>(args, p, stream);
@@ -1415,11 +1417,12 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     p.scatter_lds_bytes = p.item_lds_bytes;
 
     // fused path: the row group spans the row, lanes own whole V-column
-    // pieces of it (V = 4 up to 64 columns, else V = 8 and O % 8 == 0), and
-    // the table's rows fit in LDS
+    // pieces of it (V = 2 for up to 32 columns with O % 4 != 0, V = 4 up to
+    // 64 columns, else V = 8 and O % 8 == 0), and the table's rows fit in LDS
     p.fused = false;
-    if (!p.full && d.out_f % 4 == 0 && (d.out_f <= 64 || (d.out_f % 8 == 0 && d.out_f <= 256))) {
-        p.fvec = d.out_f <= 64 ? 4 : 8;
+    if (!p.full && ((d.out_f % 4 == 0 && (d.out_f <= 64 || (d.out_f % 8 == 0 && d.out_f <= 256))) ||
+                    (d.out_f % 2 == 0 && d.out_f <= 32))) {
+        p.fvec = d.out_f % 4 != 0 ? 2 : d.out_f <= 64 ? 4 : 8;
         p.fslices = d.out_f <= 128 ? 16 : 32;
         p.fpitch = p.fvec * p.fslices;
         const bool single = d.items <= kFusedThreads;
@@ -1507,7 +1510,8 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
         f.comps = d.comps;
         f.rows = d.rows;
         f.g_slice = static_cast<uint32_t>(((g_bytes + (d.tables + 7) / 8 - 1) / ((d.tables + 7) / 8) + 127) & ~127u);
-        f.quad_magic = ((uint64_t{1} << 32) + d.out_f / 4 - 1) / (d.out_f / 4);
+        const int per_row = d.out_f / (p.fvec < 4 ? p.fvec : 4);  // staging chunks per LUT row
+        f.quad_magic = ((uint64_t{1} << 32) + per_row - 1) / per_row;
         f.part_off = p.f_part_off;
         f.brow_off = p.f_brow_off;
         f.slots = p.f_slots;
