@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TROPNN_HIP_ABI_VERSION 8
+#define TROPNN_HIP_ABI_VERSION 9
 
 /* status codes */
 #define TROPNN_OK 0
@@ -199,6 +199,21 @@ int tropnn_hip_adam_step(int n_tensors, float *const *params, const float *const
                          float *const *exp_avg_sqs, const int64_t *numels, float *const *steps, double lr,
                          double beta1, double beta2, double eps, double weight_decay, int decoupled_weight_decay,
                          tropnn_stream_t stream);
+
+/*
+ * Mean cross entropy of the classifier's training step (the reference's
+ * F.cross_entropy(logits, y), examples/emnist.py:221) and its gradient, in
+ * one launch: loss[0] = sum over rows i with target[i] != ignore_index of
+ * (logsumexp(logits[i]) - logits[i][target[i]]), divided by their count;
+ * grad_logits[i][j] = (softmax(logits[i])[j] - [j == target[i]]) / count
+ * (0 on ignored rows), i.e. d loss / d logits. logits f32 [rows][classes],
+ * target int64 [rows], loss f32 [1], grad_logits f32 [rows][classes]: DEVICE
+ * pointers, 4-byte (target 8-byte) aligned. A target outside [0, classes)
+ * that is not ignore_index gives a NaN loss; every row ignored gives NaN
+ * (0 / 0), as torch.
+ */
+int tropnn_hip_cross_entropy(int64_t rows, int64_t classes, const float *logits, const int64_t *target,
+                             int64_t ignore_index, float *loss, float *grad_logits, tropnn_stream_t stream);
 
 /*
  * Profiling hook (no counterpart in the reference, whose harness times whole

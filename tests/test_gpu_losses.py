@@ -1,7 +1,7 @@
 """tropnn_amd.cross_entropy (tropnn_hip_cross_entropy) against F.cross_entropy
 in f64 on the CPU: loss and logits gradient, with ignored rows, every row
-ignored, large logits, one class, many classes, a non-unit incoming gradient
-and graph replays.
+ignored, large logits, one class, many classes (several LDS tiles, rows wider
+than a tile), a non-unit incoming gradient and graph replays.
 
 Tolerance: loss |Δ| <= 2e-6 |ref| + 1e-6, gradient |Δ| <= 1e-5 |ref| + 1e-8
 (f32 exp / log per element and a fixed-order f32 sum over rows)."""
@@ -28,7 +28,15 @@ def reference(logits: torch.Tensor, target: torch.Tensor, scale: float = 1.0):
 
 @pytest.mark.parametrize(
     "rows,classes,shift,ignored",
-    [(512, 10, 0.0, 0), (3, 1, 0.0, 0), (2000, 37, 0.0, 300), (7, 1000, 0.0, 2), (64, 10, 1e4, 5), (1030, 5, -50.0, 0)],
+    [
+        (512, 10, 0.0, 0),
+        (3, 1, 0.0, 0),
+        (2000, 37, 0.0, 300),  # LDS tiles of 332 rows
+        (7, 1000, 0.0, 2),  # tiles of 12 rows
+        (64, 10, 1e4, 5),
+        (1030, 5, -50.0, 0),  # tiles of 1024 rows
+        (3, 13000, 0.0, 0),  # rows wider than a tile: read from global memory
+    ],
 )
 def test_matches_torch(rows, classes, shift, ignored):
     gen = torch.Generator().manual_seed(rows + classes)

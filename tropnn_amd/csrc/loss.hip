@@ -5,7 +5,8 @@
 // answer needs one pass over the logits.
 //
 // One workgroup of 1024 threads; thread tid takes rows tid, tid + 1024, ...
-// in order, so every sum has a fixed order:
+// (of the whole input, or of each LDS tile of up to 1024 rows), in order, so
+// every sum has a fixed order:
 //   count  = number of rows whose target is not ignore_index
 //   loss   = sum_i (log(sum_j exp(x_ij - max_i)) - (x_i,y_i - max_i)) / count
 //   grad_ij = (exp(x_ij - max_i) / sum_i - [j == y_i]) / count  (0 on ignored rows)
@@ -20,6 +21,7 @@ namespace tropnn {
 namespace {
 
 constexpr int kCeThreads = 1024;
+constexpr int kCeTileFloats = 12288;  // 48 KB of LDS: a tile of rows
 
 __device__ float block_sum(float v, float *red, int tid) {
 #pragma unroll
@@ -33,38 +35,78 @@ __device__ float block_sum(float v, float *red, int tid) {
     return s;
 }
 
+// One row: the loss term (as log_softmax: no rounding at the logits'
+// magnitude) added to `part`, the gradient row written through `g` (which may
+// alias `x`: each x[j] is read before g[j] is written).
+__device__ __forceinline__ void ce_row(const float *x, float *g, int64_t y, int classes, int64_t ignore_index,
+                                       float inv, float &part) {
+    if (y == ignore_index) {
+        for (int j = 0; j < classes; ++j) g[j] = 0.f;
+        return;
+    }
+    float mx = -INFINITY;
+    for (int j = 0; j < classes; ++j) mx = fmaxf(mx, x[j]);
+    float s = 0.f;
+    for (int j = 0; j < classes; ++j) s += expf(x[j] - mx);
+    if (y < 0 || y >= classes) {
+        part += NAN;
+        for (int j = 0; j < classes; ++j) g[j] = NAN;
+        return;
+    }
+    part += logf(s) - (x[y] - mx);
+    const float rs = 1.f / s;
+    for (int j = 0; j < classes; ++j) g[j] = (expf(x[j] - mx) * rs - (j == y ? 1.f : 0.f)) * inv;
+}
+
+// tile_rows > 0: rows pass through LDS in tiles of tile_rows (coalesced loads
+// and stores, one thread per row on the LDS copy); 0 (rows wider than the
+// tile): each thread reads its rows from global memory.
 __global__ __launch_bounds__(kCeThreads) void cross_entropy_kernel(const float *__restrict__ logits,
                                                                   const int64_t *__restrict__ target, int64_t rows,
-                                                                  int classes, int64_t ignore_index,
+                                                                  int classes, int64_t ignore_index, int tile_rows,
                                                                   float *__restrict__ loss,
                                                                   float *__restrict__ grad) {
     __shared__ float red[kCeThreads / kWave];
+    __shared__ __align__(16) float tile[kCeTileFloats];
     const int tid = threadIdx.x;
+    // the first tile's logits and targets are loaded with the target count's
+    // loads, all in flight together (the kernel is a chain of round trips)
+    constexpr int kLoads = kCeTileFloats / kCeThreads;
+    float v[kLoads];
+    int64_t y = 0;
+    auto load_tile = [&](int64_t r0, int nr) {
+        const float *src = logits + r0 * classes;
+        const int n = nr * classes;
+#pragma unroll
+        for (int u = 0; u < kLoads; ++u) v[u] = tid + u * kCeThreads < n ? src[tid + u * kCeThreads] : 0.f;
+        y = tid < nr ? target[r0 + tid] : 0;
+    };
+    auto tile_rows_at = [&](int64_t r0) { return static_cast<int>(rows - r0 < tile_rows ? rows - r0 : tile_rows); };
+    if (tile_rows > 0) load_tile(0, tile_rows_at(0));
     float counted = 0.f;
     for (int64_t i = tid; i < rows; i += kCeThreads) counted += target[i] != ignore_index ? 1.f : 0.f;
     const float count = block_sum(counted, red, tid);
     const float inv = 1.f / count;
     float part = 0.f;
-    for (int64_t i = tid; i < rows; i += kCeThreads) {
-        const float *x = logits + i * classes;
-        float *g = grad + i * classes;
-        const int64_t y = target[i];
-        if (y == ignore_index) {
-            for (int j = 0; j < classes; ++j) g[j] = 0.f;
-            continue;
+    if (tile_rows > 0) {
+        for (int64_t r0 = 0; r0 < rows; r0 += tile_rows) {
+            const int nr = tile_rows_at(r0), n = nr * classes;
+#pragma unroll
+            for (int u = 0; u < kLoads; ++u)
+                if (tid + u * kCeThreads < n) tile[tid + u * kCeThreads] = v[u];
+            __syncthreads();
+            if (tid < nr) ce_row(tile + tid * classes, tile + tid * classes, y, classes, ignore_index, inv, part);
+            __syncthreads();
+            float *dst = grad + r0 * classes;
+#pragma unroll
+            for (int u = 0; u < kLoads; ++u)
+                if (tid + u * kCeThreads < n) dst[tid + u * kCeThreads] = tile[tid + u * kCeThreads];
+            if (r0 + tile_rows < rows) load_tile(r0 + tile_rows, tile_rows_at(r0 + tile_rows));
+            __syncthreads();
         }
-        float mx = -INFINITY;
-        for (int j = 0; j < classes; ++j) mx = fmaxf(mx, x[j]);
-        float s = 0.f;
-        for (int j = 0; j < classes; ++j) s += expf(x[j] - mx);
-        if (y < 0 || y >= classes) {
-            part += NAN;
-            for (int j = 0; j < classes; ++j) g[j] = NAN;
-            continue;
-        }
-        part += logf(s) - (x[y] - mx);  // as log_softmax: no rounding at the logits' magnitude
-        const float rs = 1.f / s;
-        for (int j = 0; j < classes; ++j) g[j] = (expf(x[j] - mx) * rs - (j == y ? 1.f : 0.f)) * inv;
+    } else {
+        for (int64_t i = tid; i < rows; i += kCeThreads)
+            ce_row(logits + i * classes, grad + i * classes, target[i], classes, ignore_index, inv, part);
     }
     const float total = block_sum(part, red, tid);
     if (tid == 0) *loss = total / count;
@@ -74,8 +116,10 @@ __global__ __launch_bounds__(kCeThreads) void cross_entropy_kernel(const float *
 
 hipError_t launch_cross_entropy(const float *logits, const int64_t *target, int64_t rows, int classes,
                                 int64_t ignore_index, float *loss, float *grad_logits, hipStream_t stream) {
+    int tile_rows = kCeTileFloats / classes;
+    if (tile_rows > kCeThreads) tile_rows = kCeThreads;
     hipLaunchKernelGGL(cross_entropy_kernel, dim3(1), dim3(kCeThreads), 0, stream, logits, target, rows, classes,
-                       ignore_index, loss, grad_logits);
+                       ignore_index, tile_rows, loss, grad_logits);
     return hipGetLastError();
 }
 

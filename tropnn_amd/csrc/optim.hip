@@ -20,7 +20,7 @@ namespace tropnn {
 namespace {
 
 constexpr int kAdamThreads = 256;
-constexpr int kAdamMaxBlocks = 2048;
+constexpr int kAdamMaxBlocks = 65536;  // a quad per thread up to 16 M quads
 
 struct AdamArgs {
     float *p[kAdamGroup];
