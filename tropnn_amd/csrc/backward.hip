@@ -106,6 +106,7 @@ struct SortArgs {
     const float *grad_out;  // G [B][O]
     float *g_chunked;     // G copied chunk-major: [chunks][B][P] (P = the row kernel's chunk width)
     int full;             // full STE: gu of every comparison
+    int nb_pack;          // slot offsets' low bits: 1: the neighbour row nb = code ^ (1 << r); 0: r
     int items, out_f, comps, rows, slots;
     int chunk_cols, chunk_vec, chunks;  // P, the row kernel's V, ceil(O / P)
 };
@@ -479,9 +480,11 @@ __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArg
                 base[tid] = run;
             }
             __syncthreads();
-            if (valid)
-                so[cnt[wave * R + code] + rank] =
-                    (static_cast<uint32_t>(b) * static_cast<uint32_t>(a.chunk_cols) * 4u) | static_cast<uint32_t>(rec_r(rr) & 7);
+            if (valid) {
+                const int r = rec_r(rr) & 7;
+                const uint32_t low = a.nb_pack ? static_cast<uint32_t>((code ^ (1 << r)) & (R - 1)) : static_cast<uint32_t>(r);
+                so[cnt[wave * R + code] + rank] = (static_cast<uint32_t>(b) * static_cast<uint32_t>(a.chunk_cols) * 4u) | low;
+            }
             __syncthreads();  // the next tile rewrites the counts
         }
 
@@ -542,12 +545,15 @@ __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArg
 // row crossing the range's start (end) leaves its sum in the group's slot 0
 // (1), and a combine step adds the pieces in range order and writes the
 // row. Empty rows are written as zeros, so grad_lut is fully overwritten.
-template <typename T, int V, int S, bool DOTS>
+template <typename T, int V, int S, bool DOTS, bool NBP>
 __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArgs a) {
     constexpr int NG = kRowsThreads / S;  // row groups
     constexpr int K = kRowsBatch;
     constexpr int P = S * V;  // columns of the chunk
     constexpr int KR = K <= S ? K : S;  // dots per reduce-scatter
+    // a slot offset's low bits below the item offset: nb (NBP, P * 4 >= R) or r
+    constexpr uint32_t kLow = NBP ? static_cast<uint32_t>(P * 4 - 1) : 7u;
+    static_assert(!NBP || DOTS, "nb in the slot offsets serves the STE dots");
     extern __shared__ __align__(16) unsigned char lds[];
     int *rs = reinterpret_cast<int *>(lds);                       // [R + 1] row starts (slots)
     float *part = reinterpret_cast<float *>(lds + a.part_off);    // [groups][2][P] split rows
@@ -644,7 +650,7 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
         for (int u = 0; u < K; ++u) off[u] = offn[u];
         float gv[K][V];
 #pragma unroll
-        for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, ((off[u] & ~7u) + gcol) | coldead, 0, gv[u]);
+        for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, ((off[u] & ~kLow) + gcol) | coldead, 0, gv[u]);
         meta(bt + 1, offn, rown);  // the next batch's offsets, while these rows arrive
         if (bt < b_end && k != cur) {
             if (cur >= 0) finish(cur);
@@ -667,7 +673,8 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
             float d[K];
 #pragma unroll
             for (int u = 0; u < K; ++u) {
-                const int nb = (kk ^ (1 << (off[u] & 7u))) & (R - 1);  // the mask keeps a corrupt record in range
+                // NBP: the sort kernel left nb in the offset's low bits (< R)
+                const int nb = NBP ? static_cast<int>(off[u] & kLow) : (kk ^ (1 << (off[u] & 7u))) & (R - 1);
                 const vec_t<float, V> nv = *reinterpret_cast<const vec_t<float, V> *>(lut_s + nb * P + j * V);
                 float sd = 0.f;
 #pragma unroll
@@ -752,7 +759,7 @@ __global__ __launch_bounds__(kReduceThreads) void pairwise_bwd_reduce_kernel(Red
             }
             for (; c < a.chunks; ++c) dot += pd[static_cast<size_t>(c) * a.slots + q];
         }
-        const int r = static_cast<int>(off & 7u);
+        const int r = rec_r(rr) & 7;  // the slot's low bits may hold the neighbour row instead
         const float gu = live ? dot * a.scale * surrogate_grad(rec_u(rr), a.surrogate) : 0.f;
         if (live && a.gurec != nullptr)
             a.gurec[static_cast<size_t>(t) * a.items + b] =
@@ -1261,7 +1268,8 @@ hipError_t allow_lds(K kernel, int bytes) {
 
 template <typename T, int V, int S, bool DOTS>
 hipError_t launch_rows_vs(const RowsArgs &args, const BackwardPlan &p, int tables, hipStream_t stream) {
-    auto kernel = pairwise_bwd_rows_kernel<T, V, S, DOTS>;
+    auto kernel = DOTS && p.rows_nb_pack ? pairwise_bwd_rows_kernel<T, V, S, DOTS, DOTS>
+                                         : pairwise_bwd_rows_kernel<T, V, S, DOTS, false>;
     const int lds = DOTS ? p.rows_lds_dots_bytes : p.rows_lds_bytes;
     if (hipError_t e = allow_lds(kernel, lds); e != hipSuccess) return e;
     return launch_kernel(TROPNN_KERNEL_BACKWARD_TABLE, kernel, dim3(tables * p.rows_chunks), dim3(kRowsThreads), lds,
@@ -1391,6 +1399,8 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     p.rows_lds_bytes = p.rows_part_off + (kRowsThreads / p.rows_slices) * 2 * rows_chunk * 4;
     p.rows_lut_off = (p.rows_lds_bytes + 15) & ~15;  // with dots: the LUT chunk [R][P] f32
     p.rows_lds_dots_bytes = p.rows_lut_off + d.rows * rows_chunk * 4;
+    // the neighbour row fits below the item offset (a multiple of P * 4 bytes)
+    p.rows_nb_pack = rows_chunk * 4 >= d.rows;
     p.sort_lds_bytes = ((kSortThreads / kWave) * d.rows + d.rows + kSortThreads / kWave) * 4 + (kSortThreads / kWave) * 8 * 4;
     // the sorted slots of a table: its items plus up to K - 1 padding slots
     // per row, rounded up to whole batches
@@ -1589,6 +1599,7 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
     so.chunk_vec = p.rows_vec;
     so.chunks = p.rows_chunks;
     so.full = p.full ? 1 : 0;
+    so.nb_pack = dots && p.rows_nb_pack ? 1 : 0;
     so.items = d.items;
     so.out_f = d.out_f;
     so.comps = d.comps;

@@ -64,6 +64,7 @@ struct BackwardPlan {
     int rows_lds_bytes;
     int rows_lut_off;   // with partial STE dots: LDS byte offset of the LUT chunk
     int rows_lds_dots_bytes;
+    bool rows_nb_pack;       // slot offsets carry the neighbour row (min-margin dots, P * 4 >= R)
     // sort kernel
     int sort_lds_bytes;
     int sort_slots;     // sorted-slot capacity of a table (items + padding to whole batches)
