@@ -68,9 +68,36 @@ __global__ __launch_bounds__(kAdamThreads) void adam_kernel(AdamArgs a) {
     }
     __syncthreads();
     const int64_t total = a.qstart[a.n];
+    const int lane = threadIdx.x % 64;
     int k = 0;  // the tensor holding quad q: quads only grow along the loop
     for (int64_t q = blockIdx.x * static_cast<int64_t>(kAdamThreads) + threadIdx.x; q < total;
          q += static_cast<int64_t>(gridDim.x) * kAdamThreads) {
+        // A wave's 64 quads are consecutive. When they lie in one tensor whose
+        // pointers are 16-byte aligned and none is its partial last quad (the
+        // common case), the tensor index and pointers are wave-uniform: scalar
+        // loads of the arguments instead of per-lane ones.
+        const int64_t qw = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(q - lane)) |
+                           (static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>((q - lane) >> 32))) << 32);
+        int kw = 0;
+        while (qw >= a.qstart[kw + 1]) ++kw;
+        if (qw + 64 <= a.qstart[kw + 1] && (a.vec_mask >> kw & 1u) && (qw + 64 - a.qstart[kw]) * 4 <= a.numel[kw]) {
+            const int64_t i = (q - a.qstart[kw]) * 4;
+            const AdamScalars s = sc[kw];
+            float *pp = a.p[kw], *mp = a.m[kw], *vp = a.v[kw];
+            const float *gp = a.g[kw];
+            float4 p = *reinterpret_cast<const float4 *>(pp + i);
+            const float4 g = *reinterpret_cast<const float4 *>(gp + i);
+            float4 m = *reinterpret_cast<const float4 *>(mp + i);
+            float4 v = *reinterpret_cast<const float4 *>(vp + i);
+            adam_one(p.x, g.x, m.x, v.x, a, s);
+            adam_one(p.y, g.y, m.y, v.y, a, s);
+            adam_one(p.z, g.z, m.z, v.z, a, s);
+            adam_one(p.w, g.w, m.w, v.w, a, s);
+            *reinterpret_cast<float4 *>(pp + i) = p;
+            *reinterpret_cast<float4 *>(mp + i) = m;
+            *reinterpret_cast<float4 *>(vp + i) = v;
+            continue;
+        }
         while (q >= a.qstart[k + 1]) ++k;
         const int64_t i = (q - a.qstart[k]) * 4;
         const AdamScalars s = sc[k];
