@@ -61,12 +61,31 @@ __device__ __forceinline__ void ce_row(const float *x, float *g, int64_t y, int 
 // tile_rows > 0: rows pass through LDS in tiles of tile_rows (coalesced loads
 // and stores, one thread per row on the LDS copy); 0 (rows wider than the
 // tile): each thread reads its rows from global memory.
+// (count, loss) pairs summed over the workgroup in a fixed order.
+__device__ float2 block_sum2(float2 v, float2 *red, int tid) {
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) {
+        v.x += __shfl_xor(v.x, d, kWave);
+        v.y += __shfl_xor(v.y, d, kWave);
+    }
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = v;
+    __syncthreads();
+    float2 s = make_float2(0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < kCeThreads / kWave; ++w) {
+        s.x += red[w].x;
+        s.y += red[w].y;
+    }
+    return s;
+}
+
 __global__ __launch_bounds__(kCeThreads) void cross_entropy_kernel(const float *__restrict__ logits,
                                                                   const int64_t *__restrict__ target, int64_t rows,
                                                                   int classes, int64_t ignore_index, int tile_rows,
                                                                   float *__restrict__ loss,
                                                                   float *__restrict__ grad) {
     __shared__ float red[kCeThreads / kWave];
+    __shared__ float2 red2[kCeThreads / kWave];
     __shared__ __align__(16) float tile[kCeTileFloats];
     const int tid = threadIdx.x;
     // the first tile's logits and targets are loaded with the target count's
@@ -83,6 +102,25 @@ __global__ __launch_bounds__(kCeThreads) void cross_entropy_kernel(const float *
     };
     auto tile_rows_at = [&](int64_t r0) { return static_cast<int>(rows - r0 < tile_rows ? rows - r0 : tile_rows); };
     if (tile_rows > 0) load_tile(0, tile_rows_at(0));
+    if (tile_rows >= rows) {
+        // one tile: the rows' unscaled gradients go to LDS while the target
+        // count and the loss sum share one reduction, then the scaled store
+        const int nr = static_cast<int>(rows), n = nr * classes;
+#pragma unroll
+        for (int u = 0; u < kLoads; ++u)
+            if (tid + u * kCeThreads < n) tile[tid + u * kCeThreads] = v[u];
+        __syncthreads();
+        float part = 0.f;
+        if (tid < nr) ce_row(tile + tid * classes, tile + tid * classes, y, classes, ignore_index, 1.f, part);
+        const float counted = tid < nr && y != ignore_index ? 1.f : 0.f;
+        float2 cp = block_sum2(make_float2(counted, part), red2, tid);
+        const float inv = cp.x > 0.f ? 1.f / cp.x : 0.f;  // every row ignored: zero gradients, NaN loss
+#pragma unroll
+        for (int u = 0; u < kLoads; ++u)
+            if (tid + u * kCeThreads < n) grad[tid + u * kCeThreads] = tile[tid + u * kCeThreads] * inv;
+        if (tid == 0) *loss = cp.y / cp.x;
+        return;
+    }
     float counted = 0.f;
     for (int64_t i = tid; i < rows; i += kCeThreads) counted += target[i] != ignore_index ? 1.f : 0.f;
     const float count = block_sum(counted, red, tid);
