@@ -47,3 +47,30 @@ def test_no_grad_is_a_no_op():
     opt = FusedAdam([p])
     opt.step()
     assert len(opt.state) == 0 and torch.equal(p.detach(), torch.zeros(3))
+
+
+def test_loaded_amsgrad_group_raises():
+    """A torch.optim.Adam state dict carries its group flags; FusedAdam
+    refuses a loaded amsgrad group instead of ignoring it."""
+    p = torch.nn.Parameter(torch.zeros(3))
+    src = torch.optim.Adam([p], amsgrad=True)
+    opt = FusedAdam([p])
+    opt.load_state_dict(src.state_dict())
+    with pytest.raises(NotImplementedError, match="amsgrad"):
+        opt.step()
+
+
+def test_loaded_step_becomes_f32_on_the_parameter_device():
+    """torch's loader keeps "step" as saved unless the group is capturable or
+    fused; FusedAdam converts it to a 0-dim f32 tensor on the parameter's
+    device (here the CPU, the only device without a GPU)."""
+    p = torch.nn.Parameter(torch.zeros(3))
+    src = torch.optim.Adam([p])
+    p.grad = torch.ones(3)
+    src.step()
+    sd = src.state_dict()
+    sd["state"][0]["step"] = torch.tensor(1.0, dtype=torch.float64)
+    opt = FusedAdam([p])
+    opt.load_state_dict(sd)
+    step = opt.state[p]["step"]
+    assert step.dtype == torch.float32 and step.dim() == 0 and float(step) == 1.0

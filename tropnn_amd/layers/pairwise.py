@@ -32,7 +32,10 @@ class PairwiseLinear(RoutedLinearBase):
       device_lut_dtype  "f32" (default) or "f16": the LUT element type the
                         kernels read. "f16" reads an RNE-rounded copy of the
                         f32 parameter, refreshed whenever the parameter's
-                        version changes; gradients still go to the f32 LUT.
+                        version changes (in-place torch ops and FusedAdam
+                        bump it) and cast afresh by every replay of a forward
+                        captured in a HIP graph; gradients still go to the
+                        f32 LUT.
     Attribute `cache_route_debug` (default True, as the reference's shell
     assumes) keeps `_last_indices` [B,S,T] int64 and `_last_margins`
     [B,S,T,C] f32 of the last call; False skips writing them; "lazy" writes
@@ -123,6 +126,15 @@ class PairwiseLinear(RoutedLinearBase):
         layers/pairwise.py:82-92)."""
         if self.device_lut_dtype == "f32":
             return self.lut
+        if self.lut.is_cuda and torch.cuda.is_current_stream_capturing():
+            # A captured forward casts on every replay: an optimizer step
+            # replayed in the same graph updates the f32 LUT without running
+            # any Python, so no version key could tell that the copy is stale.
+            # The graph's copy is not cached for eager calls either.
+            self._lut_f16 = None
+            self._lut_f16_key = None
+            with torch.no_grad():
+                return self.lut.detach().to(torch.float16)
         key = (self.lut._version, self.lut.data_ptr(), tuple(self.lut.shape), self.lut.device)
         if self._lut_f16 is None or self._lut_f16_key != key:
             with torch.no_grad():

@@ -4,11 +4,18 @@ The reference trains its classifiers with torch.optim.AdamW(weight_decay=0)
 (examples/emnist.py:310). FusedAdam is a drop-in torch.optim.Optimizer for
 that role: the same update as torch's Adam (non-amsgrad, op order of its
 single-tensor path), the same per-parameter state ("step", "exp_avg",
-"exp_avg_sq", so state dicts move between the two), computed by
-tropnn_hip_adam_step in libtropnn_hip.so. The step counters live on the
-device, so a training step captured in a HIP graph replays with the current
-count; lr and the other hyperparameters are read when step() runs (a captured
-graph keeps the values it was captured with).
+"exp_avg_sq", so state dicts move between the two in both directions),
+computed by tropnn_hip_adam_step in libtropnn_hip.so. The step counters live
+on the device, so a training step captured in a HIP graph replays with the
+current count; lr and the other hyperparameters are read when step() runs (a
+captured graph keeps the values it was captured with).
+
+The kernel writes the tensors through raw device pointers, so step() bumps
+the autograd version counter of every tensor it updates, as torch's in-place
+optimizers do: caches keyed by a parameter's version (PairwiseLinear's f16
+LUT copy, the lazy route-debug guard) see the update. A replayed HIP graph
+runs no Python and bumps nothing; PairwiseLinear re-casts its f16 copy inside
+a captured forward for that reason.
 
 Only dense f32 parameters on a GPU are supported; anything else raises (there
 is no CPU fallback).
@@ -63,6 +70,9 @@ def adam_step_hip(params, grads, exp_avgs, exp_avg_sqs, steps, *, lr: float, bet
         _stream(dev),
     )
     _check(rc, "tropnn_hip_adam_step")
+    # the launch wrote these through raw pointers: tell autograd and the
+    # version-keyed caches, as an in-place torch op would
+    torch.autograd.graph.increment_version(params + exp_avgs + exp_avg_sqs + steps)
 
 
 class FusedAdam(torch.optim.Optimizer):
@@ -91,6 +101,22 @@ class FusedAdam(torch.optim.Optimizer):
                         decoupled_weight_decay=decoupled_weight_decay)
         super().__init__(params, defaults)
 
+    def load_state_dict(self, state_dict) -> None:
+        """torch's loader leaves "step" where it was saved unless the group is
+        capturable or fused (Optimizer._process_value_according_to_param_policy),
+        e.g. on the CPU for a torch.optim.Adam state dict or a checkpoint
+        loaded with map_location="cpu"; the kernel reads it from the
+        parameter's device as f32."""
+        super().load_state_dict(state_dict)
+        for p, state in self.state.items():
+            step = state.get("step")
+            if step is None:
+                continue
+            if not isinstance(step, torch.Tensor):
+                step = torch.tensor(float(step))
+            if step.device != p.device or step.dtype != torch.float32 or step.dim() != 0:
+                state["step"] = step.detach().reshape(()).to(device=p.device, dtype=torch.float32)
+
     @torch.no_grad()
     def step(self, closure=None):
         loss = None
@@ -98,6 +124,9 @@ class FusedAdam(torch.optim.Optimizer):
             with torch.enable_grad():
                 loss = closure()
         for group in self.param_groups:
+            if group.get("amsgrad") or group.get("maximize"):
+                # a loaded torch.optim.Adam state dict can carry these flags
+                raise NotImplementedError("FusedAdam supports amsgrad=False and maximize=False only")
             by_device: dict[torch.device, list] = defaultdict(lambda: ([], [], [], [], []))
             for p in group["params"]:
                 if p.grad is None:
