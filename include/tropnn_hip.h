@@ -15,7 +15,9 @@
  *     (the reference's Zig ABI has no error channel; its Python wrappers
  *     validate first, and so does this library, before any launch);
  *   - stateless and re-entrant: calls on different streams may overlap as
- *     long as they write disjoint buffers.
+ *     long as they write disjoint buffers (the one exception is
+ *     tropnn_hip_pairwise_backward_noalloc, whose calls on one GPU share a
+ *     library-held buffer).
  */
 #ifndef TROPNN_HIP_H
 #define TROPNN_HIP_H
@@ -27,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TROPNN_HIP_ABI_VERSION 9
+#define TROPNN_HIP_ABI_VERSION 10
 
 /* status codes */
 #define TROPNN_OK 0
@@ -175,6 +177,28 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
                                  const int32_t *index_offsets, const int32_t *index_entries, float output_scale,
                                  int ste_mode, int surrogate, float *grad_latent, float *grad_thresholds,
                                  float *grad_lut, void *workspace, size_t workspace_bytes, tropnn_stream_t stream);
+
+/*
+ * Allocation-free variant of tropnn_hip_pairwise_backward. It has no
+ * counterpart in the reference; it is for callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving or training loops,
+ * harnesses that forbid hipMalloc. Same arguments, results and errors, minus
+ * the workspace: the kernels use a device buffer of
+ * TROPNN_NOALLOC_WORKSPACE_BYTES that the library holds, one per GPU, from
+ * the first call on that GPU until the process ends. The call allocates
+ * nothing. A shape whose workspace (tropnn_hip_pairwise_backward_workspace_size)
+ * is larger fails with TROPNN_ERR_UNSUPPORTED before any launch. Every call
+ * on one GPU shares that GPU's buffer: calls that overlap on one GPU (other
+ * streams, other threads, without ordering between them) race on it and give
+ * wrong gradients; serialise them. The buffer needs no clearing between calls.
+ */
+#define TROPNN_NOALLOC_WORKSPACE_BYTES (32u << 20)
+int tropnn_hip_pairwise_backward_noalloc(int64_t items, int64_t in_features, int64_t out_features, int64_t tables,
+                                         int64_t comparisons, const float *grad_output, const void *lut,
+                                         int lut_dtype, const tropnn_route_record *route_record, const float *margins,
+                                         const int32_t *index_offsets, const int32_t *index_entries,
+                                         float output_scale, int ste_mode, int surrogate, float *grad_latent,
+                                         float *grad_thresholds, float *grad_lut, tropnn_stream_t stream);
 
 /*
  * Adam / AdamW step over n_tensors f32 tensors: the optimizer of the

@@ -202,3 +202,22 @@ def test_cross_entropy_rejects_bad_arguments(lib):
     args = list(base)
     args[3] = 260  # int64 targets need 8-byte alignment
     assert fn(*args) == 1 and "align" in _err(lib)
+
+
+def test_noalloc_backward_rejects_before_any_launch(lib):
+    """The allocation-free backward refuses a shape whose workspace exceeds its
+    TROPNN_NOALLOC_WORKSPACE_BYTES buffer (c4's layer needs ~1.2 GB) and bad
+    enums, with the documented codes, before it looks up its device buffer."""
+    m = re.search(r"#define TROPNN_NOALLOC_WORKSPACE_BYTES \((\d+)u << (\d+)\)", HEADER.read_text())
+    assert m
+    limit = int(m.group(1)) << int(m.group(2))
+    dims = (8192, 1024, 4096, 512, 8)
+    assert lib.tropnn_hip_pairwise_backward_workspace_size(*dims, ph.LUT_F16, ph.STE_MIN_MARGIN) > limit
+    fake = 1 << 20
+    rc = lib.tropnn_hip_pairwise_backward_noalloc(*dims, fake, fake, ph.LUT_F16, fake, None, fake, fake, 1.0,
+                                                  ph.STE_MIN_MARGIN, 0, fake, fake, fake, None)
+    assert rc == 2 and b"allocation-free" in lib.tropnn_hip_last_error()
+    assert lib.tropnn_hip_pairwise_backward_noalloc(4, 8, 8, 2, 2, fake, fake, 0, fake, None, fake, fake, 1.0,
+                                                    7, 0, fake, fake, fake, None) == 1
+    assert lib.tropnn_hip_pairwise_backward_noalloc(4, 8, 8, 2, 99, fake, fake, 0, fake, None, fake, fake, 1.0,
+                                                    0, 0, fake, fake, fake, None) == 2

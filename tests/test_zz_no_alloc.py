@@ -1,0 +1,102 @@
+"""tropnn_hip_pairwise_backward_noalloc, the allocation-free backward, against
+tropnn_hip_pairwise_backward with a caller workspace, through the C ABI.
+
+Both run the same kernels in the same order, so their gradients are
+bit-identical (torch.equal; the kernels are deterministic). Each case makes
+two calls in a row, the second with fewer items, so the second call finds the
+library's buffer holding the first call's contents. The outputs start as NaN,
+so an element either entry point leaves unwritten shows.
+"""
+from __future__ import annotations
+
+import importlib
+
+import pytest
+import torch
+
+ph = importlib.import_module("tropnn_amd.backends.pairwise_hip")
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    yield
+    torch.cuda.synchronize()
+
+
+def _inputs(items, i, o, t, c, lut_dtype, full, seed):
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(items, 1, i, generator=gen).to(DEV)
+    anchors = torch.randint(0, i, (t, c, 2), generator=gen).to(DEV)
+    thr = (0.3 * torch.randn(t, c, generator=gen)).to(DEV)
+    lut = (0.02 * torch.randn(t, 1 << c, o, generator=gen)).to(DEV)
+    lut = lut.to(torch.float16) if lut_dtype == "f16" else lut
+    g = torch.randn(items, o, generator=gen).to(DEV)
+    _, rec, _, _, margins = ph._route_forward(
+        x, anchors, thr, lut, output_scale=0.125, want_record=True, return_route=False, want_margins=full
+    )
+    offsets, entries = ph.anchor_index(anchors, i)
+    return g, lut, rec, margins, offsets, entries
+
+
+def _backward(noalloc, dims, g, lut, rec, margins, offsets, entries, ste_mode):
+    items, i, o, t, c = dims
+    lib = ph.load_library()
+    lut_dtype = ph.LUT_F16 if lut.dtype == torch.float16 else ph.LUT_F32
+    nan = float("nan")
+    gx = torch.full((items, i), nan, device=DEV)
+    gthr = torch.full((t, c), nan, device=DEV)
+    glut = torch.full((t, 1 << c, o), nan, device=DEV)
+    stream = torch.cuda.current_stream(DEV).cuda_stream
+    args = (items, i, o, t, c, g.data_ptr(), lut.data_ptr(), lut_dtype, rec.data_ptr(),
+            None if margins is None else margins.data_ptr(), offsets.data_ptr(), entries.data_ptr(), 0.125,
+            ste_mode, ph.SURROGATE_IDS["fast_sigmoid_odd"], gx.data_ptr(), gthr.data_ptr(), glut.data_ptr())
+    if noalloc:
+        rc = lib.tropnn_hip_pairwise_backward_noalloc(*args, stream)
+    else:
+        ws_bytes = lib.tropnn_hip_pairwise_backward_workspace_size(items, i, o, t, c, lut_dtype, ste_mode)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+        rc = lib.tropnn_hip_pairwise_backward(*args, ws.data_ptr(), ws_bytes, stream)
+    ph._check(rc, "noalloc" if noalloc else "backward")
+    torch.cuda.synchronize()
+    return gx, gthr, glut
+
+
+@pytest.mark.parametrize(
+    "i,o,t,c,lut_dtype,full,sizes",
+    [
+        (128, 128, 136, 6, "f32", False, (512, 200)),  # c2's layer: fused table kernel + scatter
+        (96, 300, 24, 6, "f16", False, (700, 257)),  # general path: sort, row, reduce, scatter
+        (64, 48, 20, 5, "f32", True, (600, 130)),  # full STE: item, sort, row
+    ],
+)
+def test_noalloc_backward_matches_workspace_backward(i, o, t, c, lut_dtype, full, sizes):
+    ste_mode = ph.STE_FULL if full else ph.STE_MIN_MARGIN
+    lib = ph.load_library()
+    for call, items in enumerate(sizes):
+        ws_bytes = lib.tropnn_hip_pairwise_backward_workspace_size(items, i, o, t, c, 0, ste_mode)
+        assert 0 < ws_bytes <= 32 << 20
+        print(f"[noalloc] call {call}: items={items} i={i} o={o} t={t} c={c} {lut_dtype} full={full}", flush=True)
+        inputs = _inputs(items, i, o, t, c, lut_dtype, full, seed=17 * call + items)
+        dims = (items, i, o, t, c)
+        ref = _backward(False, dims, *inputs, ste_mode)
+        got = _backward(True, dims, *inputs, ste_mode)
+        for name, a, b in zip(("grad_latent", "grad_thresholds", "grad_lut"), got, ref):
+            assert not torch.isnan(b).any(), f"call {call}: {name} of the workspace entry point has unwritten elements"
+            assert torch.equal(a, b), f"call {call}: {name} differs, max {float((a - b).abs().max()):.3e}"
+
+
+def test_noalloc_rejects_a_workspace_over_its_buffer():
+    lib = ph.load_library()
+    dims = (8192, 1024, 4096, 512, 8)  # c4's layer: ~1.2 GB of workspace
+    need = lib.tropnn_hip_pairwise_backward_workspace_size(*dims, ph.LUT_F16, ph.STE_MIN_MARGIN)
+    assert need > 32 << 20
+    rc = lib.tropnn_hip_pairwise_backward_noalloc(*dims, None, None, ph.LUT_F16, None, None, None, None, 1.0,
+                                                  ph.STE_MIN_MARGIN, 0, None, None, None,
+                                                  torch.cuda.current_stream(DEV).cuda_stream)
+    assert rc == 2
+    assert b"allocation-free" in lib.tropnn_hip_last_error()

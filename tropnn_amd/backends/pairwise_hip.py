@@ -26,7 +26,7 @@ from typing import Any
 import torch
 from torch import Tensor
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 LUT_F32, LUT_F16 = 0, 1
 SURROGATE_IDS = {"fast_sigmoid_odd": 0, "izhikevich": 1}
 STE_MIN_MARGIN, STE_FULL = 0, 1
@@ -53,6 +53,7 @@ EXPORTED_SYMBOLS = (
     "tropnn_hip_pairwise_route",
     "tropnn_hip_pairwise_backward_workspace_size",
     "tropnn_hip_pairwise_backward",
+    "tropnn_hip_pairwise_backward_noalloc",
     "tropnn_hip_build_anchor_index",
     "tropnn_hip_arm_kernel_events",
     "tropnn_hip_adam_step",
@@ -96,6 +97,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tropnn_hip_build_anchor_index.restype = i
     lib.tropnn_hip_pairwise_backward.argtypes = [i64, i64, i64, i64, i64, p, p, i, p, p, p, p, f, i, i, p, p, p, p, sz, p]
     lib.tropnn_hip_pairwise_backward.restype = i
+    lib.tropnn_hip_pairwise_backward_noalloc.argtypes = [i64, i64, i64, i64, i64, p, p, i, p, p, p, p, f, i, i, p, p, p, p]
+    lib.tropnn_hip_pairwise_backward_noalloc.restype = i
     lib.tropnn_hip_arm_kernel_events.argtypes = [i, p, p]
     lib.tropnn_hip_arm_kernel_events.restype = i
     d = ctypes.c_double

@@ -1,6 +1,13 @@
 // C ABI of libtropnn_hip.so (declared in include/tropnn_hip.h): argument
 // validation, the per-thread error channel, launch planning and dispatch.
 // Nothing here allocates memory or synchronises the device.
+//
+// The allocation-free backward (tropnn_hip_pairwise_backward_noalloc) takes
+// its workspace from `scratch` below, a file-scope device array: every GPU
+// that loads the library holds its own copy, at its own address, until the
+// process ends. In host code the name `scratch` is only a handle for the HIP
+// runtime; the copy's device address comes from hipGetSymbolAddress, once per
+// device, with that device current, and only that address reaches a kernel.
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -83,6 +90,47 @@ int check_forward_ptrs(const tropnn::Dims &d, const tropnn::ForwardPlan &p, cons
 
 std::mutex g_events_mu;
 tropnn::ArmedEvents g_armed[TROPNN_KERNEL_FORWARD_ROUTE + 1];
+
+}  // namespace
+
+// Workspace of the allocation-free backward, one copy per GPU. Never zeroed:
+// every byte of it that a backward reads, the same backward wrote first.
+static __device__ __align__(256) unsigned char scratch[TROPNN_NOALLOC_WORKSPACE_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];  // device address of each GPU's copy of `scratch`
+
+// The device address of `scratch` on the GPU that `stream` runs on, looked up
+// on the first call for that GPU (with the GPU made current for the lookup)
+// and kept. No allocation: the array is part of the loaded code object.
+int scratch_for_stream(hipStream_t stream, void **out) {
+    int dev = 0;
+    hipError_t e = stream != nullptr ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail("device of the stream", e);
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(TROPNN_ERR_UNSUPPORTED, "device %d: the allocation-free entry point serves devices 0-%d", dev,
+                    kMaxDevices - 1);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        int cur = 0;
+        if ((e = hipGetDevice(&cur)) != hipSuccess) return hip_fail("hipGetDevice", e);
+        if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return hip_fail("hipSetDevice", e);
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (cur != dev) {
+            const hipError_t back = hipSetDevice(cur);
+            if (e == hipSuccess) e = back;
+        }
+        if (e != hipSuccess) return hip_fail("hipGetSymbolAddress(scratch)", e);
+        if (ptr == nullptr) return fail(TROPNN_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return TROPNN_OK;
+}
 
 }  // namespace
 
@@ -327,6 +375,32 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
                                            grad_lut, static_cast<float *>(workspace), static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail("pairwise backward launch", e);
     return ok();
+}
+
+int tropnn_hip_pairwise_backward_noalloc(int64_t items, int64_t in_features, int64_t out_features, int64_t tables,
+                                         int64_t comparisons, const float *grad_output, const void *lut,
+                                         int lut_dtype, const tropnn_route_record *route_record, const float *margins,
+                                         const int32_t *index_offsets, const int32_t *index_entries,
+                                         float output_scale, int ste_mode, int surrogate, float *grad_latent,
+                                         float *grad_thresholds, float *grad_lut, tropnn_stream_t stream) {
+    tropnn::Dims d{};
+    if (int rc = make_dims(items, in_features, out_features, tables, comparisons, lut_dtype, d)) return rc;
+    if (ste_mode != TROPNN_STE_MIN_MARGIN && ste_mode != TROPNN_STE_FULL)
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "ste_mode must be TROPNN_STE_MIN_MARGIN or TROPNN_STE_FULL");
+    const size_t need = tropnn::plan_backward(d, ste_mode).workspace_bytes;
+    if (need > sizeof scratch)
+        return fail(TROPNN_ERR_UNSUPPORTED,
+                    "this backward needs %zu bytes of workspace, over the %zu bytes of the allocation-free entry "
+                    "point's device buffer; call tropnn_hip_pairwise_backward with a workspace of that size",
+                    need, sizeof scratch);
+    void *ws = nullptr;
+    if (d.items > 0 && (grad_latent || grad_thresholds || grad_lut)) {
+        if (int rc = scratch_for_stream(static_cast<hipStream_t>(stream), &ws)) return rc;
+    }
+    return tropnn_hip_pairwise_backward(items, in_features, out_features, tables, comparisons, grad_output, lut,
+                                        lut_dtype, route_record, margins, index_offsets, index_entries, output_scale,
+                                        ste_mode, surrogate, grad_latent, grad_thresholds, grad_lut, ws,
+                                        ws != nullptr ? sizeof scratch : 0, stream);
 }
 
 }  // extern "C"
