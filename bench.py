@@ -11,23 +11,38 @@ Timed regions (both full fwd+bwd of the module API, no work skipped):
             steps per graph, one on each of 4 distinct resident (x, G)
             batches: exactly K steps are timed (K // 4 four-step replays, then
             K % 4 one-step replays), after >= 0.3 s of replays (the GPU clocks
-            ramp up under sustained load). This is `value`. A c2 step is a few
-            kernels of ~22 us; one graph launch costs 14-19 us of host time
-            and ~5 us on the device, so capturing the launch-bound loop four
-            steps at a time keeps the GPU busy. The rate with one step per
-            graph is reported beside it.
-  eager  -- up to 200 plain autograd steps right after the graph phase; the
-            three kernels of each step carry HIP events that their own
-            dispatch stamps (library hook tropnn_hip_arm_kernel_events, via
-            hipExtLaunchKernel), giving the per-kernel average durations used
-            for `roofline`. c2's backward is the fused table kernel plus the
-            input-gradient scatter kernel.
-cpu_baseline: the oracle's torch restatement of the reference torch path, same
-step on the host CPU for a bounded number of steps (rank 0, N=1 only).
+            ramp up under sustained load). This is `value`. One graph launch
+            costs 14-19 us of host time and ~5 us on the device, so capturing
+            the launch-bound loop four steps at a time keeps the GPU busy. The
+            rate with one step per graph is reported beside it.
+  eager  -- plain autograd steps back to back (as the reference harness
+            times its train step, tools/benchmarking/benchmark.py:105-118);
+            the kernels of each step carry HIP events that their own dispatch
+            stamps (library hook tropnn_hip_arm_kernel_events, via
+            hipExtLaunchKernel), giving the per-kernel durations `roofline`
+            uses.
 
-Other BASELINE.json configs, each its own JSON line (--workload): c3, the f16
-eval forward sweep at batch 1 / 64 / 8192; c4, the large f16-LUT layer fwd+bwd
-at batch 8192; c5, the EMNIST classifier training step.
+roofline (the dominant kernel, the longest average duration):
+  achieved / frac -- HBM bytes per launch as rocprofv3 counts them
+            (FETCH_SIZE + WRITE_SIZE, scaled by a calibration copy; committed
+            in profiles/traffic*.json for the kernel sources they were taken
+            from) / the launch duration measured here / 8 TB/s;
+  algorithmic_* -- the gather convention (every (item, table) moves its LUT
+            rows once): how fast the algorithm's work is done, which exceeds
+            the HBM peak where rows come from LDS and L2;
+  compulsory_*  -- each tensor the kernel must touch, once;
+  l2_hit_rate   -- TCC_HIT / (TCC_HIT + TCC_MISS) from the same profile.
+
+cpu_baseline: the oracle's torch restatement of the reference torch path
+(kind "port"), the same step on every host core this process may use
+(os.sched_getaffinity), rank 0 at N = 1 only; cpu_baselines adds the
+Zig-equivalent C forward (oracle/lut_cpu.c, the reference backend="zig" path,
+inference only) on the same cores.
+
+Other BASELINE.json configs, each its own JSON line (--workload): c1, the
+small f32 eval forward at batch 8 (latency); c3, the f16 eval forward sweep
+at batch 1 / 64 / 8192; c4, the large f16-LUT layer fwd+bwd at batch 8192;
+c5, the EMNIST classifier training step and its 100-step loss curve.
 
 Prints ONE JSON line.
 """
@@ -35,7 +50,6 @@ from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -50,6 +64,9 @@ HBM_PEAK_GBS = 8000.0
 B, I, O, T, C = 512, 128, 128, 136, 6
 R = 1 << C
 E = 4  # f32 LUT element bytes
+C1 = {"b": 8, "i": 256, "o": 512, "t": 16, "c": 6}
+C4 = {"b": 8192, "i": 1024, "o": 4096, "t": 512, "c": 8}
+C4_CPU_BATCH = 8
 
 
 def algorithmic_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = T, c: int = C, e: int = E,
@@ -91,6 +108,39 @@ def algorithmic_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = 
             "backward_reduce": 4 * t * c, "backward_scatter": x_side}
 
 
+def compulsory_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = T, c: int = C, e: int = E,
+                     streamed: bool = False) -> dict[str, int]:
+    """Per-launch compulsory bytes: each tensor a kernel must read or write,
+    once, with the LUT capped at the min(B, 2^C) rows per table that items
+    can touch. Each kernel counts what it must move by itself, so the LUT,
+    which the forward and the backward each read, counts in both:
+      forward: x, anchors + thresholds, the LUT, y, one code byte per
+        (item, table) kept for the backward (streamed: the route kernel
+        takes x, anchors + thresholds and the codes, the gather the LUT and y);
+      backward_fused / backward_table: G, the codes, the LUT (for the STE
+        dots), grad_lut (every row, untouched rows as zeros), and for the
+        fused kernel grad_thr;
+      backward_reduce: grad_thr;
+      backward_scatter: grad_x and the anchors;
+      backward_sort: nothing.
+    The step total at c2 is 14,589,824 B: SURVEY's 9,981,056 B (every
+    tensor once), plus the code bytes and the backward's second LUT read."""
+    r = 1 << c
+    lut = e * t * min(b, r) * o
+    grad_lut = 4 * t * r * o
+    fwd = 4 * b * i + 20 * t * c + lut + 4 * b * o + b * t
+    bwd_rows = 4 * b * o + b * t + lut + grad_lut
+    scatter = 4 * b * i + 16 * t * c
+    if fused:
+        return {"forward": fwd, "backward_fused": bwd_rows + 4 * t * c, "backward_scatter": scatter}
+    head = {"forward": fwd}
+    if streamed:
+        route = 4 * b * i + 20 * t * c + b * t
+        head = {"forward_route": route, "forward": fwd - route}
+    return {**head, "backward_sort": 0, "backward_table": bwd_rows, "backward_reduce": 4 * t * c,
+            "backward_scatter": scatter}
+
+
 def fused_backward() -> bool:
     """Whether the library runs c2's backward as the fused table kernel plus
     the scatter kernel (its workspace then holds 8-byte {gu, r} records)."""
@@ -130,117 +180,344 @@ def source_digest() -> str:
     return h.hexdigest()
 
 
-def measured_traffic(kernel: str, workload: str = "c2") -> int | None:
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
-    summary of the workload (profiles/traffic.json for c2,
-    profiles/traffic_<workload>.json otherwise: FETCH_SIZE and WRITE_SIZE
-    scaled by a calibration copy), used only while the kernel sources
-    (comments aside) still hash to the profiled ones; otherwise None."""
+def profile_record(kernel: str, workload: str = "c2") -> dict | None:
+    """The committed rocprofv3 counter summary of one kernel of a workload
+    (profiles/traffic.json for c2, profiles/traffic_<workload>.json
+    otherwise): fetch_bytes and write_bytes (FETCH_SIZE and WRITE_SIZE
+    scaled by a calibration copy) and, where the profile has them, TCC_HIT /
+    TCC_MISS per launch. Used only while the kernel sources (comments aside)
+    still hash to the profiled ones; otherwise None."""
     path = ROOT / "profiles" / ("traffic.json" if workload == "c2" else f"traffic_{workload}.json")
     if not path.exists():
         return None
     rec = json.loads(path.read_text())
     if rec.get("source_digest") != source_digest() or kernel not in rec.get("kernels", {}):
         return None
-    k = rec["kernels"][kernel]
-    return int(k["fetch_bytes"] + k["write_bytes"])
+    return rec["kernels"][kernel]
 
 
-def cpu_baseline(budget_s: float) -> dict:
-    """The oracle (torch restatement of the reference torch path) on the host
-    cores: same c2 fwd+bwd step, full batch, as many steps as fit the budget."""
-    import torch
+def measured_traffic(kernel: str, workload: str = "c2") -> int | None:
+    """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE) from the
+    committed profile, or None (see profile_record)."""
+    k = profile_record(kernel, workload)
+    return None if k is None else int(k["fetch_bytes"] + k["write_bytes"])
 
+
+def l2_hit_rate(kernel: str, workload: str = "c2") -> float | None:
+    k = profile_record(kernel, workload)
+    if k is None or "tcc_hit" not in k:
+        return None
+    total = k["tcc_hit"] + k["tcc_miss"]
+    return round(k["tcc_hit"] / total, 4) if total > 0 else None
+
+
+def roofline(kernel: str, avg_us: float, algo: int, comp: int, workload: str) -> dict:
+    """The roofline object of one kernel: HBM bytes per launch from the
+    committed counter profile / the live launch duration / 8 TB/s, beside the
+    algorithmic (gather convention) and compulsory figures. Without a
+    profile of the current sources, `achieved` falls back to the compulsory
+    bytes and `basis` says so."""
+    t = avg_us * 1e-6
+    traffic = measured_traffic(kernel, workload)
+    hbm_bytes = traffic if traffic is not None else comp
+    achieved = hbm_bytes / t / 1e9
+    return {
+        "bound": "hbm",
+        "kernel": kernel,
+        "basis": ("rocprofv3 FETCH_SIZE + WRITE_SIZE bytes per launch (calibrated; profiles/"
+                  + ("traffic.json" if workload == "c2" else f"traffic_{workload}.json") + ") / live launch duration")
+        if traffic is not None else "compulsory bytes / live launch duration (no counter profile of these sources)",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": traffic,
+        "avg_us": round(avg_us, 3),
+        "l2_hit_rate": l2_hit_rate(kernel, workload),
+        "mall_hit_rate": None,  # gfx950's rocprofv3 exposes no MALL (Infinity Cache) counter
+        "algorithmic_bytes": algo,
+        "algorithmic_GBs": round(algo / t / 1e9, 1),
+        "algorithmic_frac": round(algo / t / 1e9 / HBM_PEAK_GBS, 4),
+        "compulsory_bytes": comp,
+        "compulsory_frac": round(comp / t / 1e9 / HBM_PEAK_GBS, 4),
+    }
+
+
+# ---------------------------------------------------------------- CPU legs
+def host_threads() -> int:
+    """Host cores this process may run on (os.sched_getaffinity): every CPU
+    leg uses all of them, torch through torch.set_num_threads and the
+    Zig-equivalent through tropnn_set_num_threads."""
+    return len(os.sched_getaffinity(0))
+
+
+def _median_time(fn, budget_s: float, min_iters: int = 3) -> tuple[float, int]:
+    """Median wall time of fn() over as many calls as fit `budget_s` (at
+    least min_iters), after one warmup call."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < min_iters:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def _oracle_layer(i: int, o: int, t: int, c: int, seed: int = 0):
     from oracle.pairwise_torch import OraclePairwiseLinear
 
-    threads = torch.get_num_threads()
-    layer = OraclePairwiseLinear(I, O, tables=T, comparisons=C, seed=0).train()
-    x = torch.randn(B, I, generator=torch.Generator().manual_seed(0)).requires_grad_(True)
-    g = torch.randn(B, 1, O, generator=torch.Generator().manual_seed(1))
+    return OraclePairwiseLinear(i, o, tables=t, comparisons=c, seed=seed)
+
+
+def cpu_torch_train(i: int, o: int, t: int, c: int, b: int, budget_s: float, label: str) -> dict:
+    """The oracle (torch restatement of the reference torch path) fwd + STE
+    bwd on the host cores: y = layer(x); y.backward(G), x needing grad."""
+    import torch
+
+    n = host_threads()
+    torch.set_num_threads(n)
+    layer = _oracle_layer(i, o, t, c).train()
+    x = torch.randn(b, i, generator=torch.Generator().manual_seed(0)).requires_grad_(True)
+    g = torch.randn(b, 1, o, generator=torch.Generator().manual_seed(1))
 
     def step() -> None:
         layer.zero_grad(set_to_none=True)
         x.grad = None
         layer(x).backward(g)
 
-    step()  # warmup
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
+    med, n_it = _median_time(step, budget_s)
     return {
-        "value": B / med,
+        "value": b / med,
         "unit": "samples/s",
-        "cores": threads,
+        "cores": n,
         "kind": "port",
-        "sample": f"c2 fwd+bwd, full batch {B}, {len(times)} steps (median {med * 1e3:.1f} ms/step), "
-        f"oracle/pairwise_torch.py torch-CPU restatement, torch.set_num_threads={threads}",
+        "path": "torch-CPU (reference backend='torch')",
+        "ms_per_call": round(med * 1e3, 4),
+        "sample": f"{label} fwd+bwd at batch {b}, {n_it} steps (median {med * 1e3:.2f} ms/step), "
+        f"oracle/pairwise_torch.py torch-CPU restatement, torch.set_num_threads={n} "
+        f"(all cores in os.sched_getaffinity)",
     }
 
 
-C5_LAYER_BYTES = 313_619_648  # the three layers' FwdBwd algorithmic bytes per c5 step (CE and Adam not counted)
-
-
-def cpu_baseline_c5(budget_s: float) -> dict:
-    """The oracle classifier (the three oracle layers, seeds 0, 1, 2) with
-    torch Adam on the host cores: the same c5 training step, full batch."""
+def cpu_torch_eval(i: int, o: int, t: int, c: int, b: int, budget_s: float, label: str) -> dict:
+    """The oracle's eval forward (torch.no_grad, f32 LUT: the reference torch
+    path reads the f32 parameter) on the host cores, calls back to back like
+    tools/benchmarking/benchmark.py:91-102."""
     import torch
-    import torch.nn.functional as F
 
-    from oracle.pairwise_torch import OraclePairwiseLinear
-    from tropnn_amd.examples import make_c5_batch
+    n = host_threads()
+    torch.set_num_threads(n)
+    layer = _oracle_layer(i, o, t, c).eval()
+    x = torch.randn(b, i, generator=torch.Generator().manual_seed(0))
 
-    threads = torch.get_num_threads()
-    dims = (784, 128, 128, 10)
-    layers = torch.nn.ModuleList(
-        [OraclePairwiseLinear(a, b, tables=T, comparisons=C, seed=k) for k, (a, b) in enumerate(zip(dims[:-1], dims[1:]))]
-    )
-    opt = torch.optim.Adam(layers.parameters(), lr=1e-3)
-    x, y = make_c5_batch(512, seed=0)
+    def call() -> None:
+        with torch.no_grad():
+            layer(x)
 
-    def step() -> None:
-        opt.zero_grad(set_to_none=True)
-        h = x.unsqueeze(1)
-        for layer in layers:
-            h = layer(h)
-        F.cross_entropy(h.squeeze(1), y).backward()
-        opt.step()
-
-    step()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
+    med, n_it = _median_time(call, budget_s)
     return {
-        "value": 512 / med,
+        "value": b / med,
         "unit": "samples/s",
-        "cores": threads,
+        "cores": n,
         "kind": "port",
-        "sample": f"c5 train step (3 oracle layers + CE + torch Adam), batch 512, {len(times)} steps "
-        f"(median {med * 1e3:.1f} ms/step), torch.set_num_threads={threads}",
+        "path": "torch-CPU (reference backend='torch')",
+        "ms_per_call": round(med * 1e3, 4),
+        "sample": f"{label} eval forward at batch {b}, f32 LUT, {n_it} calls (median {med * 1e3:.3f} ms/call), "
+        f"oracle/pairwise_torch.py, torch.set_num_threads={n}",
     }
+
+
+def cpu_zig_eval(i: int, o: int, t: int, c: int, b: int, lut_dtype: str, budget_s: float, label: str) -> dict:
+    """The Zig-equivalent CPU forward (oracle/lut_cpu.c, the C restatement of
+    kernels/src/lut.zig:248-318) on the host cores, called as
+    pairwise_zig_forward calls the Zig library (backends/pairwise_zig.py:
+    35-103): the LUT in the read dtype prepared once (the reference caches
+    its f16 copy by version, layers/pairwise.py:82-92), per call an output
+    allocation and the C call, which zeroes and fills it."""
+    import torch
+
+    from oracle import lut_cpu
+
+    n = host_threads()
+    torch.set_num_threads(n)
+    lib = lut_cpu.load()
+    lib.tropnn_set_num_threads(n)
+    layer = _oracle_layer(i, o, t, c)
+    x = torch.randn(b, i, generator=torch.Generator().manual_seed(0)).contiguous()
+    anchors = layer.anchors.contiguous()
+    thr = layer.thresholds.detach().contiguous()
+    w = layer.lut.detach().to(torch.float16 if lut_dtype == "f16" else torch.float32).contiguous()
+    fn = lib.lut_forward_batch_f16_no_cache if lut_dtype == "f16" else lib.lut_forward_batch_with_offsets_no_cache
+
+    def call() -> None:
+        out = torch.empty(b, o, dtype=torch.float32)
+        fn(b, t, c, i, o, w.data_ptr(), anchors.data_ptr(), thr.data_ptr(), x.data_ptr(), out.data_ptr())
+
+    med, n_it = _median_time(call, budget_s)
+    return {
+        "value": b / med,
+        "unit": "samples/s",
+        "cores": n,
+        "kind": "port",
+        "path": f"Zig-equivalent CPU (reference backend='zig', {lut_dtype} LUT)",
+        "ms_per_call": round(med * 1e3, 4),
+        "sample": f"{label} eval forward at batch {b}, {lut_dtype} LUT, {n_it} calls (median {med * 1e3:.3f} ms/call), "
+        f"oracle/lut_cpu.c (-O3 -march=x86-64-v3), tropnn_set_num_threads={n}",
+    }
+
+
+# ---------------------------------------------------------------- GPU helpers
+def _kernel_events(names, n):
+    import torch
+
+    evs = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+           for k in names}
+    stream = torch.cuda.current_stream()
+    for k in names:  # create the event handles
+        for e0, e1 in evs[k]:
+            e0.record(stream)
+            e1.record(stream)
+    return evs
+
+
+def _graph_per_call_us(graphs, steps: int, warmup: int) -> float:
+    """us per replay over `steps` replays of `graphs` round robin, after
+    >= 0.3 s (and >= warmup replays) of warmup."""
+    import torch
+
+    torch.cuda.synchronize()
+    t0, w = time.perf_counter(), 0
+    while w < warmup or time.perf_counter() - t0 < 0.3:
+        graphs[w % len(graphs)].replay()
+        w += 1
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        graphs[k % len(graphs)].replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e6 / steps
+
+
+def _eval_forward_gpu(layer, xs, steps: int, warmup: int) -> dict:
+    """GPU times of the module's eval forward on resident inputs: back to back
+    eager calls (benchmark.py:91-102's loop), the median latency of one call
+    to its result (call, then synchronize), one HIP graph per call replayed
+    back to back, and the forward kernel's own duration (events stamped by
+    its dispatch)."""
+    import torch
+
+    from tropnn_amd.backends.pairwise_hip import arm_kernel_events
+
+    nb = len(xs)
+    with torch.no_grad():
+        for x in xs:
+            layer(x)
+        torch.cuda.synchronize()
+        t0, w = time.perf_counter(), 0
+        while w < warmup or time.perf_counter() - t0 < 0.3:
+            layer(xs[w % nb])
+            w += 1
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(steps):
+            layer(xs[k % nb])
+        torch.cuda.synchronize()
+        eager_us = (time.perf_counter() - t0) * 1e6 / steps
+        lat = []
+        for k in range(min(steps, 200)):
+            t0 = time.perf_counter()
+            layer(xs[k % nb])
+            torch.cuda.synchronize()
+            lat.append(time.perf_counter() - t0)
+        lat.sort()
+        sync_us = lat[len(lat) // 2] * 1e6
+        graphs = []
+        for x in xs:
+            gph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gph):
+                layer(x)
+            graphs.append(gph)
+    graph_us = _graph_per_call_us(graphs, steps, warmup)
+    evs = _kernel_events(("forward",), 100)["forward"]
+    with torch.no_grad():
+        for k, (e0, e1) in enumerate(evs):
+            arm_kernel_events("forward", e0, e1)
+            layer(xs[k % nb])
+    torch.cuda.synchronize()
+    kus = sorted(1e3 * e0.elapsed_time(e1) for e0, e1 in evs)[len(evs) // 2]
+    return {"eager_us_per_call": eager_us, "sync_latency_us": sync_us, "graph_us_per_call": graph_us, "kernel_us": kus}
+
+
+# ---------------------------------------------------------------- workloads
+def bench_c1(args, dev) -> dict:
+    """c1: PairwiseLinear(256 -> 512, T = 16,
+    C = 6), f32 eval forward at batch 8, seeded init (seed 0), x ~ N(0,1)
+    from seed 0: a latency configuration. `value` is the module's eval
+    forward time per call with calls back to back, as the reference harness
+    times it (benchmark.py:91-102); beside it the latency of one call to its
+    result, the per-call time of graph replays, the kernel's own duration,
+    and both reference CPU paths on the same host cores."""
+    import torch
+
+    from tropnn_amd import PairwiseLinear
+
+    b = C1["b"]
+    layer = PairwiseLinear(C1["i"], C1["o"], tables=C1["t"], comparisons=C1["c"], seed=0).to(dev).eval()
+    gen = torch.Generator().manual_seed(0)
+    xs = [torch.randn(b, C1["i"], generator=gen).to(dev) for _ in range(4)]
+    gpu = _eval_forward_gpu(layer, xs, args.steps, args.warmup)
+    log("c1: " + ", ".join(f"{k}={v:.2f}" for k, v in gpu.items()))
+    algo = 4 * b * C1["i"] + 20 * C1["t"] * C1["c"] + 4 * b * C1["t"] * C1["o"] + 4 * b * C1["o"]
+    cpus = []
+    if args.cpu_budget > 0:
+        budget = min(args.cpu_budget, 5.0)
+        cpus.append(cpu_zig_eval(C1["i"], C1["o"], C1["t"], C1["c"], b, "f32", budget, "c1"))
+        cpus.append(cpu_torch_eval(C1["i"], C1["o"], C1["t"], C1["c"], b, budget, "c1"))
+        for c in cpus:
+            log(f"c1 cpu {c['path']}: {c['ms_per_call'] * 1e3:.1f} us/call on {c['cores']} cores")
+    us = gpu["eager_us_per_call"]
+    out = {
+        "metric": "PairwiseLinear c1 eval forward time per call (256->512, T=16, C=6, f32 LUT, B=8), calls back to back",
+        "value": round(us, 3),
+        "unit": "us/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us * 1e-3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: x ~ N(0,1) from seed 0, 4 resident inputs; seeded module init (seed 0)",
+        "config": {"workload": "c1: PairwiseLinear(256->512, tables=16, comparisons=6) eval forward, f32 LUT "
+                   "[16,64,512], batch 8", "batch": b, "mode": "eager module calls under torch.no_grad"},
+        "sync_latency_us": round(gpu["sync_latency_us"], 3),
+        "graph_us_per_call": round(gpu["graph_us_per_call"], 3),
+        "kernel_us": round(gpu["kernel_us"], 3),
+        "roofline": roofline("forward", gpu["kernel_us"], algo,
+                             compulsory_bytes(True, b=b, i=C1["i"], o=C1["o"], t=C1["t"], c=C1["c"])["forward"] - b * C1["t"],
+                             "c1"),
+        "cpu_baseline": cpus[0] if cpus else None,
+        "cpu_baselines": cpus,
+    }
+    if cpus:
+        out["speedup_vs_cpu"] = {c["path"]: round(c["ms_per_call"] * 1e3 / us, 2) for c in cpus}
+    return out
 
 
 def bench_c3(args, dev) -> dict:
     """c3: the c2 layer (128 -> 128, T = 136,
     C = 6) as eval forward only with f16 LUT reads, at batch 1, 64 and 8192:
-    time per call (one HIP graph per call, replayed back to back over 4
-    resident inputs; at small batches this is the host launch path), the
-    forward kernel's own duration (events its dispatch stamps; the device
-    latency), and the algorithmic-byte rate, F_eval = 4BI + 20TC + 2BTO + 4BO
-    per call."""
+    per call with eager calls back to back, one call's latency to its result,
+    graph replays, the kernel's own duration, and the algorithmic-byte rate,
+    F_eval = 4BI + 20TC + 2BTO + 4BO per call; beside each, the Zig-
+    equivalent CPU forward (f16 LUT, as the reference's zig path reads it)
+    and the torch-CPU forward (f32 LUT) on the same host cores."""
     import torch
 
     from tropnn_amd import PairwiseLinear
-    from tropnn_amd.backends.pairwise_hip import arm_kernel_events
 
     layer = PairwiseLinear(I, O, tables=T, comparisons=C, seed=0, device_lut_dtype="f16").to(dev).eval()
     layer.cache_route_debug = False
@@ -248,51 +525,30 @@ def bench_c3(args, dev) -> dict:
     for b in (1, 64, 8192):
         gen = torch.Generator().manual_seed(0)
         xs = [torch.randn(b, I, generator=gen).to(dev) for _ in range(4)]
-        with torch.no_grad():
-            for x in xs:  # warm the f16 read copy and the allocator
-                layer(x)
-            torch.cuda.synchronize()
-            graphs = []
-            for x in xs:
-                gph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(gph):
-                    layer(x)
-                graphs.append(gph)
-        torch.cuda.synchronize()
-        t0, w = time.perf_counter(), 0
-        while w < args.warmup or time.perf_counter() - t0 < 0.3:
-            graphs[w % 4].replay()
-            w += 1
-        torch.cuda.synchronize()
-        n = args.steps
-        t0 = time.perf_counter()
-        for k in range(n):
-            graphs[k % 4].replay()
-        torch.cuda.synchronize()
-        us = (time.perf_counter() - t0) * 1e6 / n
-        # the kernel's own duration over eager calls
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(100)]
-        stream = torch.cuda.current_stream(dev)
-        for e0, e1 in evs:
-            e0.record(stream)
-            e1.record(stream)
-        with torch.no_grad():
-            for k, (e0, e1) in enumerate(evs):
-                arm_kernel_events("forward", e0, e1)
-                layer(xs[k % 4])
-        torch.cuda.synchronize()
-        kus = sorted(1e3 * e0.elapsed_time(e1) for e0, e1 in evs)[len(evs) // 2]
+        gpu = _eval_forward_gpu(layer, xs, args.steps, args.warmup)
         algo = 4 * b * I + 20 * T * C + 2 * b * T * O + 4 * b * O
-        results[str(b)] = {
-            "kernel_us": round(kus, 3),
+        us = gpu["graph_us_per_call"]
+        res = {
+            "kernel_us": round(gpu["kernel_us"], 3),
             "us_per_call": round(us, 3),
+            "eager_us_per_call": round(gpu["eager_us_per_call"], 3),
+            "sync_latency_us": round(gpu["sync_latency_us"], 3),
             "samples_per_s": round(b / (us * 1e-6), 1),
             "algorithmic_bytes": algo,
             "algorithmic_GBs": round(algo / (us * 1e-6) / 1e9, 1),
         }
-        log(f"c3 batch {b}: {us:.2f} us/call, kernel {kus:.2f} us")
+        log(f"c3 batch {b}: graph {us:.2f} us/call, eager {gpu['eager_us_per_call']:.2f}, kernel {gpu['kernel_us']:.2f} us")
+        if args.cpu_budget > 0:
+            budget = min(args.cpu_budget, 4.0)
+            cpus = [cpu_zig_eval(I, O, T, C, b, "f16", budget, "c3"), cpu_torch_eval(I, O, T, C, b, budget, "c3")]
+            res["cpu_baselines"] = cpus
+            res["speedup_vs_cpu"] = {c["path"]: round(c["ms_per_call"] * 1e3 / us, 1) for c in cpus}
+            for c in cpus:
+                log(f"c3 batch {b} cpu {c['path']}: {c['ms_per_call']:.3f} ms/call")
+        results[str(b)] = res
     big = results["8192"]
-    return {
+    comp = compulsory_bytes(True, b=8192, e=2)["forward"] - 8192 * T
+    out = {
         "metric": "PairwiseLinear c3 eval forward, f16 LUT reads (128->128, T=136, C=6): samples/s at batch 8192, latency at 1 and 64",
         "value": big["samples_per_s"],
         "unit": "samples/s",
@@ -305,11 +561,13 @@ def bench_c3(args, dev) -> dict:
         "vs_baseline": None,
         "dtype": "f16 LUT reads, f32 accumulate",
         "data": "synthetic: x ~ N(0,1), 4 resident inputs per batch size; seeded module init (seed 0)",
-        "config": {"workload": "c3: PairwiseLinear(128->128, tables=136, comparisons=6) eval forward, f16 LUT [136,64,128]", "batches": [1, 64, 8192]},
+        "config": {"workload": "c3: PairwiseLinear(128->128, tables=136, comparisons=6) eval forward, f16 LUT [136,64,128]",
+                   "batches": [1, 64, 8192], "mode": "one HIP graph per call, replayed back to back"},
         "per_batch": results,
-        "roofline_8192": {"bound": "hbm", "achieved": big["algorithmic_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                          "frac": round(big["algorithmic_GBs"] / HBM_PEAK_GBS, 4)},
+        "roofline": roofline("forward", big["kernel_us"], big["algorithmic_bytes"], comp, "c3"),
+        "cpu_baseline": results["8192"].get("cpu_baselines", [None])[0],
     }
+    return out
 
 
 def bench_c5(args, dev) -> dict:
@@ -319,7 +577,9 @@ def bench_c5(args, dev) -> dict:
     entropy (tropnn_amd.cross_entropy: the library's one-launch loss and
     gradient), backward, Adam (lr 1e-3) step (FusedAdam: the library's Adam
     kernel), captured in one HIP graph per resident batch (4, round-robin)
-    and timed over replays like c2."""
+    and timed over replays like c2. Then the 100-step loss curve
+    (examples/emnist.py:203-228's loop on fresh seeded batches) of the HIP
+    stack and of the oracle stack with torch Adam, from the same init."""
     import torch
 
     from tropnn_amd import FusedAdam, cross_entropy
@@ -364,6 +624,7 @@ def bench_c5(args, dev) -> dict:
     torch.cuda.synchronize()
     us = (time.perf_counter() - t0) * 1e6 / args.steps
     log(f"c5 graph {us:.1f} us/step")
+    curve = c5_loss_curve(dev, args.curve_steps) if args.curve_steps > 0 else None
     cpu = cpu_baseline_c5(args.cpu_budget) if args.cpu_budget > 0 else None
     value = 512 / (us * 1e-6)
     out = {
@@ -389,14 +650,107 @@ def bench_c5(args, dev) -> dict:
         "layer_algorithmic_bytes_per_step": C5_LAYER_BYTES,
         "layer_algorithmic_GBs": round(C5_LAYER_BYTES / (us * 1e-6) / 1e9, 1),
         "cpu_baseline": cpu,
+        "loss_curve": curve,
     }
     if cpu:
         out["speedup_vs_cpu"] = round(value / cpu["value"], 1)
     return out
 
 
-C4 = {"b": 8192, "i": 1024, "o": 4096, "t": 512, "c": 8}
-C4_CPU_BATCH = 8
+C5_LAYER_BYTES = 313_619_648  # the three layers' FwdBwd algorithmic bytes per c5 step (CE and Adam not counted)
+
+
+def c5_loss_curve(dev, steps: int) -> dict:
+    """`steps` training steps of the HIP classifier (tropnn_amd.cross_entropy,
+    FusedAdam) and of the oracle classifier on the CPU (F.cross_entropy,
+    torch.optim.Adam), from the same seeded init, on the same fresh batch per
+    step (make_c5_batch with seed 1000 + step), eager. Per step: both losses,
+    and whether every layer's route codes agree bit for bit. Route flips
+    (a margin within rounding of zero) make the two trajectories part; the
+    first step with differing codes is reported."""
+    import torch
+    import torch.nn.functional as F
+
+    from tropnn_amd import FusedAdam, cross_entropy
+    from tropnn_amd.examples import EmnistPairwiseClassifier, make_c5_batch
+
+    n = host_threads()
+    torch.set_num_threads(n)
+    model = EmnistPairwiseClassifier().to(dev).train()
+    dims = (784, 128, 128, 10)
+    ref_layers = torch.nn.ModuleList(
+        [_oracle_layer(a, b, T, C, seed=k) for k, (a, b) in enumerate(zip(dims[:-1], dims[1:]))]
+    ).train()
+    opt = FusedAdam(model.parameters(), lr=1e-3)
+    opt_ref = torch.optim.Adam(ref_layers.parameters(), lr=1e-3, foreach=False)
+    hip_loss, ref_loss, same_codes = [], [], []
+    t0 = time.perf_counter()
+    for k in range(steps):
+        x, y = make_c5_batch(512, seed=1000 + k)
+        opt.zero_grad(set_to_none=True)
+        loss = cross_entropy(model(x.to(dev)), y.to(dev))
+        loss.backward()
+        opt.step()
+        opt_ref.zero_grad(set_to_none=True)
+        h = x.unsqueeze(1)
+        for layer in ref_layers:
+            h = layer(h)
+        loss_r = F.cross_entropy(h.squeeze(1), y)
+        loss_r.backward()
+        opt_ref.step()
+        hip_loss.append(float(loss))
+        ref_loss.append(float(loss_r))
+        same_codes.append(all(torch.equal(a._last_indices.cpu(), b._last_indices) for a, b in zip(model.layers, ref_layers)))
+    first_diff = next((k for k, s in enumerate(same_codes) if not s), None)
+    rel = [abs(a - b) / abs(b) for a, b in zip(hip_loss, ref_loss)]
+    upto = first_diff if first_diff is not None else steps
+    log(f"c5 loss curve: {steps} steps in {time.perf_counter() - t0:.1f} s, codes first differ at step {first_diff}, "
+        f"loss {hip_loss[0]:.4f} -> {hip_loss[-1]:.4f} (oracle {ref_loss[0]:.4f} -> {ref_loss[-1]:.4f})")
+    return {
+        "steps": steps,
+        "batches": "make_c5_batch(512, seed=1000 + step), a fresh batch per step",
+        "hip": [round(v, 6) for v in hip_loss],
+        "oracle": [round(v, 6) for v in ref_loss],
+        "codes_equal": same_codes,
+        "first_step_codes_differ": first_diff,
+        "max_rel_loss_diff_while_codes_equal": max(rel[:upto]) if upto > 0 else None,
+        "max_rel_loss_diff": max(rel),
+        "oracle_threads": n,
+    }
+
+
+def cpu_baseline_c5(budget_s: float) -> dict:
+    """The oracle classifier (the three oracle layers, seeds 0, 1, 2) with
+    torch Adam on the host cores: the same c5 training step, full batch."""
+    import torch
+    import torch.nn.functional as F
+
+    from tropnn_amd.examples import make_c5_batch
+
+    n = host_threads()
+    torch.set_num_threads(n)
+    dims = (784, 128, 128, 10)
+    layers = torch.nn.ModuleList([_oracle_layer(a, b, T, C, seed=k) for k, (a, b) in enumerate(zip(dims[:-1], dims[1:]))])
+    opt = torch.optim.Adam(layers.parameters(), lr=1e-3)
+    x, y = make_c5_batch(512, seed=0)
+
+    def step() -> None:
+        opt.zero_grad(set_to_none=True)
+        h = x.unsqueeze(1)
+        for layer in layers:
+            h = layer(h)
+        F.cross_entropy(h.squeeze(1), y).backward()
+        opt.step()
+
+    med, n_it = _median_time(step, budget_s)
+    return {
+        "value": 512 / med,
+        "unit": "samples/s",
+        "cores": n,
+        "kind": "port",
+        "sample": f"c5 train step (3 oracle layers + CE + torch Adam), batch 512, {n_it} steps "
+        f"(median {med * 1e3:.1f} ms/step), torch.set_num_threads={n}",
+    }
 
 
 def cpu_baseline_c4(budget_s: float) -> dict:
@@ -405,47 +759,16 @@ def cpu_baseline_c4(budget_s: float) -> dict:
     STE bwd, at a reduced batch of 8 items: the full batch of 8192 would hold
     ~64 GiB of saved STE rows (one [B, tables, 4096] f32 neighbour difference
     per route chunk). Reported per sample."""
-    import torch
-
-    from oracle.pairwise_torch import OraclePairwiseLinear
-
-    threads = torch.get_num_threads()
-    layer = OraclePairwiseLinear(C4["i"], C4["o"], tables=C4["t"], comparisons=C4["c"], seed=0).train()
-    gen = torch.Generator().manual_seed(0)
-    x = torch.randn(C4_CPU_BATCH, C4["i"], generator=gen).requires_grad_(True)
-    g = torch.randn(C4_CPU_BATCH, 1, C4["o"], generator=gen)
-
-    def step() -> None:
-        layer.zero_grad(set_to_none=True)
-        x.grad = None
-        layer(x).backward(g)
-
-    step()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    return {
-        "value": C4_CPU_BATCH / med,
-        "unit": "samples/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"c4 layer fwd+bwd at batch {C4_CPU_BATCH} (the full 8192 needs ~64 GiB of saved STE rows), "
-        f"f32 LUT, {len(times)} steps (median {med * 1e3:.0f} ms/step), oracle/pairwise_torch.py "
-        f"torch-CPU restatement, torch.set_num_threads={threads}",
-    }
+    return cpu_torch_train(C4["i"], C4["o"], C4["t"], C4["c"], C4_CPU_BATCH, budget_s,
+                           f"c4 layer (the full batch 8192 needs ~64 GiB of saved STE rows; f32 LUT)")
 
 
 def bench_c4(args, dev) -> dict:
     """c4: PairwiseLinear(1024 -> 4096, T = 512,
     C = 8) reading an f16 LUT (the RNE copy of the f32 master; 1 GiB), batch
     8192, one step = forward + min-margin STE backward with x, thresholds and
-    f32 LUT (2 GiB) gradients. A step takes tens of milliseconds, so plain
-    eager module steps are timed (K steps after the warmup); each kernel's
+    f32 LUT (2 GiB) gradients. A step takes milliseconds, so plain eager
+    module steps are timed (K steps after the warmup); each kernel's
     duration comes from events its own dispatch stamps, over the same steps.
     The forward takes the streamed path (route-record kernel, then the
     streamed gather) and the backward the general path (sort, row, reduce and
@@ -473,13 +796,9 @@ def bench_c4(args, dev) -> dict:
         step(w % nb)
     torch.cuda.synchronize()
     algo = algorithmic_bytes(False, e=2, streamed=True, **C4)
+    comp = compulsory_bytes(False, e=2, streamed=True, **C4)
     names = tuple(algo)
-    stream = torch.cuda.current_stream(dev)
-    evs = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)] for n in names}
-    for n in names:
-        for e0, e1 in evs[n]:
-            e0.record(stream)
-            e1.record(stream)
+    evs = _kernel_events(names, args.steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for k in range(args.steps):
@@ -491,7 +810,6 @@ def bench_c4(args, dev) -> dict:
     kern_us = {n: 1e3 * sum(e0.elapsed_time(e1) for e0, e1 in evs[n]) / args.steps for n in names}
     log(f"c4 {step_ms:.2f} ms/step; kernels (ms): " + ", ".join(f"{n}={v * 1e-3:.3f}" for n, v in kern_us.items()))
     dom = max(names, key=lambda n: kern_us[n])
-    achieved = algo[dom] / (kern_us[dom] * 1e-6) / 1e9
     if args.calibrate_copy_bytes > 0:
         calibration_copy(args.calibrate_copy_bytes, dev)
     cpu = None
@@ -501,6 +819,8 @@ def bench_c4(args, dev) -> dict:
         log(f"cpu baseline {cpu['value']:.1f} samples/s on {cpu['cores']} threads")
     value = b / (step_ms * 1e-3)
     total_algo = sum(algo.values())
+    traffic = {n: measured_traffic(n, "c4") for n in names}
+    step_traffic = sum(traffic.values()) if all(v is not None for v in traffic.values()) else None
     out = {
         "metric": "PairwiseLinear c4 samples/s fwd+bwd (1024->4096, T=512, C=8, f16 LUT, B=8192) + achieved HBM GB/s vs peak",
         "value": round(value, 1),
@@ -526,20 +846,19 @@ def bench_c4(args, dev) -> dict:
             "lut_dtype": "f16",
             "mode": "eager module fwd+bwd",
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": dom,
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(dom, "c4"),
-        },
+        "roofline": roofline(dom, kern_us[dom], algo[dom], comp[dom], "c4"),
         "cpu_baseline": cpu,
-        "step_algorithmic_GBs": round(total_algo / (step_ms * 1e-3) / 1e9, 1),
-        "step_roofline_frac": round(total_algo / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "step": {
+            "hbm_traffic_bytes": step_traffic,
+            "hbm_frac": round(step_traffic / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if step_traffic else None,
+            "compulsory_bytes": sum(comp.values()),
+            "compulsory_frac": round(sum(comp.values()) / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": total_algo,
+            "algorithmic_frac": round(total_algo / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        },
         "kernels": {
-            n: {"avg_us": round(kern_us[n], 1), "algorithmic_bytes": algo[n],
+            n: {"avg_us": round(kern_us[n], 1), "algorithmic_bytes": algo[n], "compulsory_bytes": comp[n],
+                "hbm_traffic_bytes": traffic[n], "l2_hit_rate": l2_hit_rate(n, "c4"),
                 "achieved_GBs": round(algo[n] / (kern_us[n] * 1e-6) / 1e9, 1) if kern_us[n] > 0 else None}
             for n in names
         },
@@ -563,54 +882,11 @@ def calibration_copy(nbytes: int, dev) -> None:
     log(f"calibration copy of {n * 4} bytes done")
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument(
-        "--workload",
-        choices=("c2", "c3", "c4", "c5"),
-        default="c2",
-        help="c2: the BASELINE metric (default); c3: f16 eval forward at batch 1 / 64 / 8192; "
-        "c4: the large f16-LUT layer fwd+bwd at batch 8192; c5: the EMNIST classifier training step",
-    )
-    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 500; 20 for c4)")
-    ap.add_argument("--warmup", type=int, default=None, help="warmup steps (default 50; 3 for c4)")
-    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work (0 = skip)")
-    ap.add_argument(
-        "--calibrate-copy-bytes",
-        type=int,
-        default=0,
-        help="also run one plain device copy of this many bytes (the reference dispatch that scales "
-        "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)",
-    )
-    args = ap.parse_args()
-    if args.steps is None:
-        args.steps = 20 if args.workload == "c4" else 500
-    if args.warmup is None:
-        args.warmup = 3 if args.workload == "c4" else 50
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(
-            "bench.py measures one GPU only: the PairwiseLinear path is built and measured on a single MI355X "
-            "(multi-GPU sharding is a design note, not part of this build). Run with --gpus 1.",
-            file=sys.stderr,
-        )
-        return 2
-
+def bench_c2(args, dev) -> dict:
     import torch
 
     from tropnn_amd import PairwiseLinear
-    from tropnn_amd.backends.pairwise_hip import arm_kernel_events, library_path
-
-    if not torch.cuda.is_available():
-        print("bench.py needs a GPU", file=sys.stderr)
-        return 2
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    log(f"device {torch.cuda.get_device_name(dev)}, library {library_path()}")
-    if args.workload != "c2":
-        runner = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.workload]
-        print(json.dumps(runner(args, dev)))
-        return 0
+    from tropnn_amd.backends.pairwise_hip import arm_kernel_events
 
     layer = PairwiseLinear(I, O, tables=T, comparisons=C, seed=0).to(dev).train()
     layer.cache_route_debug = False  # route debug tensors are not part of the step
@@ -670,41 +946,48 @@ def main() -> int:
         return (time.perf_counter() - t0) * 1e6 / steps
 
     graphs = [capture([k]) for k in range(nb)]
-    graph1_us = replay_rate(graphs, 1, args.steps)
+    graph1_us = replay_rate(graphs, 1, max(args.steps, 200))
     log(f"graph {graph1_us:.1f} us/step (one step per graph)")
     graphs4 = [capture([(j + i) % nb for i in range(4)]) for j in range(nb)]
     graph_us = replay_rate(graphs4, 4, args.steps, tail=graphs)
     graph_ms = graph_us * 1e-3
     log(f"graph {graph_us:.1f} us/step (four steps per graph)")
 
-    # ---- per-kernel durations: eager steps right after the graph phase (GPU
-    # clocks still up); each kernel's own dispatch stamps the armed events
-    algo = algorithmic_bytes(fused_backward())
-    names = tuple(algo)
-    ksteps = min(args.steps, 200)
-    evs = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(ksteps)] for n in names}
-    for n in names:  # create the event handles
-        for e0, e1 in evs[n]:
-            e0.record(stream)
-            e1.record(stream)
+    # ---- eager steps back to back: the host-bound rate of plain autograd
+    # steps (the reference harness's loop), then per-kernel durations over
+    # eager steps whose kernels stamp armed events
+    esteps = max(args.steps, 200)
     for w in range(nb):
         step(w)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    for k in range(esteps):
+        step(k % nb)
+    torch.cuda.synchronize()
+    eager_us = (time.perf_counter() - t0) * 1e6 / esteps
+    log(f"eager {eager_us:.1f} us/step")
+    fused = fused_backward()
+    algo = algorithmic_bytes(fused)
+    comp = compulsory_bytes(fused)
+    names = tuple(algo)
+    ksteps = min(max(args.steps, 100), 200)
+    evs = _kernel_events(names, ksteps)
+    torch.cuda.synchronize()
     for k in range(ksteps):
         for n in names:
             arm_kernel_events(n, *evs[n][k])
         step(k % nb)
     torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - t0) * 1e3 / ksteps
     kern_us = {n: 1e3 * sum(e0.elapsed_time(e1) for e0, e1 in evs[n]) / ksteps for n in names}
-    log(f"eager {eager_ms * 1e3:.1f} us/step; kernels (us): " + ", ".join(f"{n}={v:.2f}" for n, v in kern_us.items()))
+    log("kernels (us): " + ", ".join(f"{n}={v:.2f}" for n, v in kern_us.items()))
 
-    # ---- roofline of the dominant kernel
     dom = max(names, key=lambda n: kern_us[n])
-    achieved = algo[dom] / (kern_us[dom] * 1e-6) / 1e9
+    traffic = {n: measured_traffic(n) for n in names}
     kernels = {
-        n: {"avg_us": round(kern_us[n], 3), "algorithmic_bytes": algo[n], "achieved_GBs": round(algo[n] / (kern_us[n] * 1e-6) / 1e9, 1)}
+        n: {"avg_us": round(kern_us[n], 3), "algorithmic_bytes": algo[n], "compulsory_bytes": comp[n],
+            "hbm_traffic_bytes": traffic[n], "l2_hit_rate": l2_hit_rate(n),
+            "hbm_frac": round(traffic[n] / (kern_us[n] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if traffic[n] else None,
+            "algorithmic_GBs": round(algo[n] / (kern_us[n] * 1e-6) / 1e9, 1)}
         for n in names
     }
 
@@ -712,13 +995,17 @@ def main() -> int:
         calibration_copy(args.calibrate_copy_bytes, dev)
 
     cpu = None
+    cpus = []
     if args.cpu_budget > 0:
-        log("timing the CPU baseline")
-        cpu = cpu_baseline(args.cpu_budget)
-        log(f"cpu baseline {cpu['value']:.0f} samples/s on {cpu['cores']} threads")
+        log("timing the CPU baselines")
+        cpu = cpu_torch_train(I, O, T, C, B, args.cpu_budget, "c2")
+        cpus = [cpu, cpu_zig_eval(I, O, T, C, B, "f32", min(args.cpu_budget, 3.0), "c2 (forward only: the zig path has no backward)")]
+        log(f"cpu baseline {cpu['value']:.0f} samples/s on {cpu['cores']} cores; zig-equivalent forward "
+            f"{cpus[1]['ms_per_call']:.3f} ms/call")
 
     value = B / (graph_ms * 1e-3)
     total_algo = sum(algo.values())
+    step_traffic = sum(traffic.values()) if all(v is not None for v in traffic.values()) else None
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -743,24 +1030,75 @@ def main() -> int:
             "lut_dtype": "f32",
             "mode": "hip-graph replay of the module fwd+bwd, four steps (one per resident batch) per graph",
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": dom,
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(dom),
-        },
+        "roofline": roofline(dom, kern_us[dom], algo[dom], comp[dom], "c2"),
         "cpu_baseline": cpu,
-        "step_algorithmic_GBs": round(total_algo / (graph_ms * 1e-3) / 1e9, 1),
+        "cpu_baselines": cpus,
+        "step": {
+            "hbm_traffic_bytes": step_traffic,
+            "hbm_frac": round(step_traffic / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if step_traffic else None,
+            "compulsory_bytes": sum(comp.values()),
+            "compulsory_frac": round(sum(comp.values()) / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": total_algo,
+            "algorithmic_GBs": round(total_algo / (graph_ms * 1e-3) / 1e9, 1),
+            "algorithmic_frac": round(total_algo / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        },
         "us_per_step_one_step_per_graph": round(graph1_us, 3),
-        "eager_ms_per_step": round(eager_ms, 6),
+        "eager_us_per_step": round(eager_us, 3),
         "kernels": kernels,
     }
     if cpu:
         out["speedup_vs_cpu"] = round(value / cpu["value"], 1)
-    print(json.dumps(out))
+        out["eager_speedup_vs_cpu"] = round(B / (eager_us * 1e-6) / cpu["value"], 1)
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument(
+        "--workload",
+        choices=("c1", "c2", "c3", "c4", "c5"),
+        default="c2",
+        help="c2: the BASELINE metric (default); c1: the small f32 eval forward at batch 8 (latency); "
+        "c3: f16 eval forward at batch 1 / 64 / 8192; c4: the large f16-LUT layer fwd+bwd at batch 8192; "
+        "c5: the EMNIST classifier training step and its loss curve",
+    )
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 500; 20 for c4)")
+    ap.add_argument("--warmup", type=int, default=None, help="warmup steps (default 50; 3 for c4)")
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work (0 = skip)")
+    ap.add_argument("--curve-steps", type=int, default=100, help="c5: steps of the loss curve (0 = skip)")
+    ap.add_argument(
+        "--calibrate-copy-bytes",
+        type=int,
+        default=0,
+        help="also run one plain device copy of this many bytes (the reference dispatch that scales "
+        "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)",
+    )
+    args = ap.parse_args()
+    if args.steps is None:
+        args.steps = 20 if args.workload == "c4" else 500
+    if args.warmup is None:
+        args.warmup = 3 if args.workload == "c4" else 50
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(
+            "bench.py measures one GPU only: the PairwiseLinear path is built and measured on a single MI355X "
+            "(multi-GPU sharding is a design note, not part of this build). Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from tropnn_amd.backends.pairwise_hip import library_path
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"device {torch.cuda.get_device_name(dev)}, library {library_path()}, host cores {host_threads()}")
+    runner = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.workload]
+    print(json.dumps(runner(args, dev)))
     return 0
 
 

@@ -519,8 +519,19 @@ def test_single_hip_runtime_in_process():
 def test_c4_large_layer_properties():
     """c4: PairwiseLinear(1024->4096, T=512, C=8), f16 LUT reads, B=8192.
 
-    The full-size oracle is out of reach on the CPU, so parity is checked on
-    properties that do not depend on size:
+    The full-size oracle is out of reach on the CPU, so parity is checked
+    against the closed forms of the backward (layers/pairwise.py:137-166 with
+    the autograd of the gather) and on properties that do not depend on size:
+      * every one of the 8192 x 512 route codes against the numpy route;
+      * for six tables (both ends, the middle and three seeded picks), over
+        all 8192 items, in float64 from the HIP codes, the numpy margins and
+        the f16 values the kernels read:
+          grad_lut[t, r, :] = s * sum_{b: code[b,t] = r} G[b, :],
+          D[b] = s * sum_o G[b, o] * (L[t, nb, o] - L[t, code, o]),
+          nb = code ^ 2^r*, r* = first argmin_c |m[b, t, c]|, u = m[b, t, r*],
+          grad_thresholds[t, c] = -sum_{b: r* = c} D[b] * fast_sigmoid_odd'(u)
+        (an item placed in the wrong row of a later sort tile, or a wrong
+        sign or comparison in the threshold gradient, fails these);
       * forward and input gradient of a row depend on that row only: a random
         subset of rows is compared with the oracle run on those rows alone;
       * every item adds its scaled grad row to exactly one row per table, so
@@ -533,7 +544,7 @@ def test_c4_large_layer_properties():
     assert torch.equal(hip.anchors.cpu(), ref.anchors)
     x = seeded((b, i), seed=0).to(DEV)
     gfull = seeded((b, 1, o), seed=1).to(DEV)
-    sub = torch.randperm(b, generator=torch.Generator().manual_seed(0))[:16]
+    sub = torch.randperm(b, generator=torch.Generator().manual_seed(0))[:32]
 
     def run(g):
         hip.zero_grad(set_to_none=True)
@@ -543,17 +554,37 @@ def test_c4_large_layer_properties():
         return y.detach(), xg.grad.detach(), hip.thresholds.grad.detach().clone(), hip.lut.grad.detach().clone()
 
     y, gx, gthr, glut = run(gfull)
-    codes = hip._last_indices.view(b, t)
-    want_codes = routing_np.route_codes(x[sub].cpu().numpy(), ref.anchors.numpy(), ref.thresholds.detach().numpy())
-    np.testing.assert_array_equal(codes[sub.to(DEV)].cpu().numpy(), want_codes)
+    codes = hip._last_indices.view(b, t).cpu().numpy()
+    x_np = x.cpu().numpy()
+    margins = routing_np.margins_f32(x_np, ref.anchors.numpy(), ref.thresholds.detach().numpy())
+    np.testing.assert_array_equal(codes, routing_np.codes_from_margins(margins))
 
-    x_sub = x[sub].cpu().requires_grad_(True)
+    s = hip.output_scale
+    lut16 = hip._lut_f16.cpu().double()  # the f16 read copy the kernels used
+    g64 = gfull.view(b, o).cpu().double()
+    picks = torch.randperm(t - 2, generator=torch.Generator().manual_seed(5))[:3] + 1
+    tables = [0, t // 2, t - 1] + [int(v) for v in picks]
+    gthr_cpu, glut_t = gthr.cpu(), None
+    for tt in tables:
+        code_t = torch.from_numpy(codes[:, tt])
+        want_lut = torch.zeros(1 << c, o, dtype=torch.float64).index_add_(0, code_t, g64) * s
+        glut_t = glut[tt].cpu()
+        assert rel_err(glut_t, want_lut) <= F32_TOL, f"grad_lut of table {tt}"
+        m = margins[:, tt, :]
+        r_star = torch.from_numpy(routing_np.min_margin_index(m))
+        u = torch.from_numpy(m).double().gather(1, r_star.view(-1, 1)).view(-1)
+        nb = code_t ^ (1 << r_star)
+        d = s * ((lut16[tt][nb] - lut16[tt][code_t]) * g64).sum(1)
+        gu = d * (-0.5 * torch.sign(u) / (1.0 + u.abs()).square())
+        want_thr = -torch.zeros(c, dtype=torch.float64).index_add_(0, r_star, gu)
+        assert rel_err(gthr_cpu[tt], want_thr) <= 1e-4, f"grad_thresholds of table {tt}"
+
+    x_sub = x[sub.to(DEV)].cpu().requires_grad_(True)
     y_sub = ref.train()(x_sub)
     y_sub.backward(gfull[sub.to(DEV)].cpu())
     assert rel_err(y[sub.to(DEV)], y_sub) <= F16_TOL
     assert rel_err(gx[sub.to(DEV)], x_sub.grad) <= F16_TOL
 
-    s = hip.output_scale
     row_sums = glut.sum(dim=1)  # [T, O]
     want = (gfull.view(b, o).double().sum(0) * s).float()
     assert rel_err(row_sums, want.expand(t, o)) <= 1e-4

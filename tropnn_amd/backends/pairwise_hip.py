@@ -173,7 +173,9 @@ def arm_kernel_events(kernel: str, start: "torch.cuda.Event | None", stop: "torc
 
 
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw hipStream_t of the device's current stream (no Stream object)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 def _ptr(t: Tensor | None) -> int | None:
@@ -181,10 +183,12 @@ def _ptr(t: Tensor | None) -> int | None:
 
 
 def _require_gpu(*tensors: Tensor) -> None:
-    if not torch.cuda.is_available():
-        raise RuntimeError("PairwiseLinear backend='hip' requires a visible AMD GPU (torch.cuda.is_available() is False)")
     for t in tensors:
         if not t.is_cuda:
+            if not torch.cuda.is_available():
+                raise RuntimeError(
+                    "PairwiseLinear backend='hip' requires a visible AMD GPU (torch.cuda.is_available() is False)"
+                )
             raise ValueError("PairwiseLinear backend='hip' requires GPU tensors")
 
 
