@@ -810,8 +810,6 @@ def bench_c4(args, dev) -> dict:
     kern_us = {n: 1e3 * sum(e0.elapsed_time(e1) for e0, e1 in evs[n]) / args.steps for n in names}
     log(f"c4 {step_ms:.2f} ms/step; kernels (ms): " + ", ".join(f"{n}={v * 1e-3:.3f}" for n, v in kern_us.items()))
     dom = max(names, key=lambda n: kern_us[n])
-    if args.calibrate_copy_bytes > 0:
-        calibration_copy(args.calibrate_copy_bytes, dev)
     cpu = None
     if args.cpu_budget > 0:
         log("timing the CPU baseline")
@@ -991,9 +989,6 @@ def bench_c2(args, dev) -> dict:
         for n in names
     }
 
-    if args.calibrate_copy_bytes > 0:
-        calibration_copy(args.calibrate_copy_bytes, dev)
-
     cpu = None
     cpus = []
     if args.cpu_budget > 0:
@@ -1098,7 +1093,10 @@ def main() -> int:
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_name(dev)}, library {library_path()}, host cores {host_threads()}")
     runner = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.workload]
-    print(json.dumps(runner(args, dev)))
+    out = runner(args, dev)
+    if args.calibrate_copy_bytes > 0:
+        calibration_copy(args.calibrate_copy_bytes, dev)
+    print(json.dumps(out))
     return 0
 
 
