@@ -83,3 +83,15 @@ def test_graph_replays_match_eager():
         want = cross_entropy(x, y)
         _ = torch.ones(64, device=DEV).sum().item()
         assert torch.equal(out, want), rep
+
+
+def test_empty_batch_gives_nan_loss():
+    """No rows: the mean over nothing is NaN, as F.cross_entropy returns, and
+    the gradient is empty; no kernel is launched."""
+    logits = torch.empty(0, 10, device=DEV, requires_grad=True)
+    target = torch.empty(0, dtype=torch.int64, device=DEV)
+    loss = cross_entropy(logits, target)
+    ref = F.cross_entropy(logits.detach().cpu().double(), target.cpu())
+    assert math.isnan(float(loss)) and math.isnan(float(ref))
+    loss.backward()
+    assert logits.grad is not None and logits.grad.shape == (0, 10)

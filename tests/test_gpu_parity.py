@@ -713,3 +713,28 @@ def test_large_tables_times_comparisons(i, o, t, c, b, min_margin):
     x = seeded((b, i), seed=8)
     g = seeded((b, 1, o), seed=9)
     assert_train_parity(ref, hip, *train_step(ref, hip, x, g))
+
+
+# ---------------------------------------------------------------- fused backward over table counts and code skews
+@pytest.mark.parametrize(
+    "i,o,t,c,b,thr_std",
+    [
+        (96, 64, 40, 6, 512, 0.3),
+        (128, 128, 150, 6, 512, 0.3),
+        (128, 128, 136, 6, 512, 4.0),  # skewed: most items in a few rows
+        (64, 96, 200, 5, 300, 0.3),
+        (64, 32, 300, 4, 512, 0.3),  # more tables than compute units
+        (80, 10, 136, 6, 511, 0.3),  # O = 10, two columns per lane
+        (48, 128, 7, 6, 1, 0.3),  # one item
+    ],
+)
+def test_fused_backward_table_counts(i, o, t, c, b, thr_std):
+    """The fused backward (one workgroup per table) from 7 to 300 tables,
+    with large thresholds that put most items into a few rows of each table
+    (long rows crossing many row-group ranges, many empty rows), and a
+    single item."""
+    ref, hip = make_pair(i, o, t, c, seed=t + b, thr_std=thr_std, gen_seed=b)
+    x = seeded((b, i), seed=i + t)
+    g = seeded((b, 1, o), seed=o + b)
+    yx_ref, yx_hip = train_step(ref, hip, x, g)
+    assert_train_parity(ref, hip, yx_ref, yx_hip)

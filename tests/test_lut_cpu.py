@@ -85,3 +85,21 @@ def test_thread_counts_are_bit_identical(lib):
     x = torch.randn(300, 1, 48, generator=torch.Generator().manual_seed(1))
     outs = [lut_cpu.forward(x, ref.anchors, ref.thresholds.detach(), ref.lut.detach(), threads=n) for n in (1, 2, 5)]
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+def test_restatement_is_clean_under_sanitizers(tmp_path):
+    """oracle/sanitize_check.c drives both forwards over every loop of the
+    restatement (row- and table-major, remainders after the table groups and
+    the vector steps, 1 to 8 comparisons, 1 to 8 threads) built with
+    AddressSanitizer + UndefinedBehaviorSanitizer, then with
+    ThreadSanitizer: any report aborts the run."""
+    import shutil
+    import subprocess
+    from pathlib import Path
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    here = Path(lut_cpu.__file__).resolve().parent
+    out = subprocess.run(["make", "-s", "-C", str(here), "sanitize", f"SAN_DIR={tmp_path}"], capture_output=True, text=True)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert out.stdout.count("sanitize_check ok") == 2
