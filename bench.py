@@ -513,8 +513,9 @@ def bench_c1(args, dev) -> dict:
 def bench_c3(args, dev) -> dict:
     """c3: the c2 layer (128 -> 128, T = 136,
     C = 6) as eval forward only with f16 LUT reads, at batch 1, 64 and 8192:
-    per call with eager calls back to back, one call's latency to its result,
-    graph replays, the kernel's own duration, and the algorithmic-byte rate,
+    per call with calls back to back (eager or graph replays, the faster of
+    the two), one call's latency to its result, the kernel's own duration,
+    and the algorithmic-byte rate,
     F_eval = 4BI + 20TC + 2BTO + 4BO per call; beside each, the Zig-
     equivalent CPU forward (f16 LUT, as the reference's zig path reads it)
     and the torch-CPU forward (f32 LUT) on the same host cores."""
@@ -530,17 +531,24 @@ def bench_c3(args, dev) -> dict:
         xs = [torch.randn(b, I, generator=gen).to(dev) for _ in range(4)]
         gpu = _eval_forward_gpu(layer, xs, args.steps, args.warmup)
         algo = 4 * b * I + 20 * T * C + 2 * b * T * O + 4 * b * O
-        us = gpu["graph_us_per_call"]
+        # calls back to back, eager (the reference harness's loop) or as graph
+        # replays, whichever the box runs faster: at small batches the graph
+        # skips the Python path, at large ones eager calls pipeline behind the
+        # kernels while each graph launch adds its own host and device cost
+        us = min(gpu["eager_us_per_call"], gpu["graph_us_per_call"])
         res = {
             "kernel_us": round(gpu["kernel_us"], 3),
             "us_per_call": round(us, 3),
+            "mode": "eager" if us == gpu["eager_us_per_call"] else "graph",
             "eager_us_per_call": round(gpu["eager_us_per_call"], 3),
+            "graph_us_per_call": round(gpu["graph_us_per_call"], 3),
             "sync_latency_us": round(gpu["sync_latency_us"], 3),
             "samples_per_s": round(b / (us * 1e-6), 1),
             "algorithmic_bytes": algo,
             "algorithmic_GBs": round(algo / (us * 1e-6) / 1e9, 1),
         }
-        log(f"c3 batch {b}: graph {us:.2f} us/call, eager {gpu['eager_us_per_call']:.2f}, kernel {gpu['kernel_us']:.2f} us")
+        log(f"c3 batch {b}: graph {gpu['graph_us_per_call']:.2f} us/call, eager {gpu['eager_us_per_call']:.2f}, "
+            f"kernel {gpu['kernel_us']:.2f} us")
         if args.cpu_budget > 0:
             budget = min(args.cpu_budget, 4.0)
             cpus = [cpu_zig_eval(I, O, T, C, b, "f16", budget, "c3"), cpu_torch_eval(I, O, T, C, b, budget, "c3")]
@@ -565,7 +573,9 @@ def bench_c3(args, dev) -> dict:
         "dtype": "f16 LUT reads, f32 accumulate",
         "data": "synthetic: x ~ N(0,1), 4 resident inputs per batch size; seeded module init (seed 0)",
         "config": {"workload": "c3: PairwiseLinear(128->128, tables=136, comparisons=6) eval forward, f16 LUT [136,64,128]",
-                   "batches": [1, 64, 8192], "mode": "one HIP graph per call, replayed back to back"},
+                   "batches": [1, 64, 8192],
+                   "mode": "module eval calls back to back under torch.no_grad: eager or one HIP graph per call, "
+                   "the faster (per_batch.mode)"},
         "per_batch": results,
         "roofline": roofline("forward", big["kernel_us"], big["algorithmic_bytes"], comp, "c3"),
         "cpu_baseline": results["8192"].get("cpu_baselines", [None])[0],

@@ -126,7 +126,7 @@ struct RowsArgs {
     const void *lut;       // [T][R][O] f32 or f16
     uint32_t lut_bytes;
     float *pdot;           // [T][chunks][slots] per sorted slot: sum over the chunk's columns of G (L[nb] - L[code]), unscaled
-    int items, chunks, lut_off;
+    int items, chunks, lut_off, rs_off;  // LDS byte offsets: LUT chunk (0 with dots), row starts
 };
 
 // Reduce kernel (general path, min-margin), one workgroup per table.
@@ -554,8 +554,12 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
     // a slot offset's low bits below the item offset: nb (NBP, P * 4 >= R) or r
     constexpr uint32_t kLow = NBP ? static_cast<uint32_t>(P * 4 - 1) : 7u;
     static_assert(!NBP || DOTS, "nb in the slot offsets serves the STE dots");
+    // the neighbour row's LDS address from one byte permute: the LUT chunk at
+    // LDS offset 0 with 256-byte rows, nb (< 256) in the slot offset's low
+    // byte, the lane's column offset (< 256) in the address's low byte
+    constexpr bool kNbPerm = NBP && P * 4 == 256;
     extern __shared__ __align__(16) unsigned char lds[];
-    int *rs = reinterpret_cast<int *>(lds);                       // [R + 1] row starts (slots)
+    int *rs = reinterpret_cast<int *>(lds + a.rs_off);            // [R + 1] row starts (slots)
     float *part = reinterpret_cast<float *>(lds + a.part_off);    // [groups][2][P] split rows
     float *lut_s = reinterpret_cast<float *>(lds + a.lut_off);    // DOTS: [R][P] the table's LUT chunk
     // unit = chunk * T + table, each XCD taking one contiguous block of units:
@@ -568,9 +572,17 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
     const int col = chunk * P + j * V;
     const bool col_ok = col < O;  // V divides O: a lane's columns are all in or all out
     // grad-row piece of slot offset s: s + chunk base + lane offset; padding
-    // (s = kSlotPad) and dead columns fall past the copy and read zeros
+    // (s = kSlotPad) and dead columns fall past the copy and read zeros. With
+    // NBP the item offset is a multiple of P * 4 and the lane's column offset
+    // j * V * 4 < P * 4 fills the bits nb leaves once masked off (one
+    // and-or), the chunk base is the scalar offset, and kOutOfRange in the
+    // lane term makes a dead column, or a batch past the group's range, read
+    // zeros
     const uint32_t gcol = static_cast<uint32_t>(chunk) * a.chunk_bytes + static_cast<uint32_t>(j * V) * 4u;
     const uint32_t coldead = col_ok ? 0u : kOutOfRange;
+    const uint32_t lane_col = static_cast<uint32_t>(j * V) * 4u | coldead;
+    const int chunk_base = static_cast<int>(static_cast<uint32_t>(chunk) * a.chunk_bytes);
+    const uint32_t lane_lds = static_cast<uint32_t>(j * V) * 4u;
     const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.g_chunked, a.gc_bytes);
     const uint32_t *so = a.slot_off + static_cast<size_t>(t) * a.slots;
     const int32_t *br = a.batch_row + static_cast<size_t>(t) * (a.slots / K);
@@ -622,17 +634,20 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
             *reinterpret_cast<vec_t<float, V> *>(part + (g * 2 + (fb < b_begin ? 0 : 1)) * P + j * V) = w;
         }
     };
-    // a batch's slot offsets and row (past the range: out-of-range slots)
+    // a batch's slot offsets and row. Past the range: without NBP
+    // out-of-range slots; with NBP the table's last batch (its loads are
+    // masked out by the lane term, its row is not used)
     auto meta = [&](int bt, uint32_t(&off)[K], int &row) {
-        if (bt < b_end) {
-            const vec_t<uint32_t, 4> *src = reinterpret_cast<const vec_t<uint32_t, 4> *>(so + static_cast<size_t>(bt) * K);
+        if (NBP || bt < b_end) {
+            const int bc = NBP ? min(bt, nb_all - 1) : bt;
+            const vec_t<uint32_t, 4> *src = reinterpret_cast<const vec_t<uint32_t, 4> *>(so + static_cast<size_t>(bc) * K);
 #pragma unroll
             for (int q = 0; q < K / 4; ++q) {
                 const vec_t<uint32_t, 4> w = src[q];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) off[4 * q + e] = w[e];
             }
-            row = br[bt];
+            row = br[bc];
         } else {
 #pragma unroll
             for (int u = 0; u < K; ++u) off[u] = kSlotPad;
@@ -649,8 +664,14 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
 #pragma unroll
         for (int u = 0; u < K; ++u) off[u] = offn[u];
         float gv[K][V];
+        if constexpr (NBP) {
+            const uint32_t lane_eff = lane_col | (bt < b_end ? 0u : kOutOfRange);
 #pragma unroll
-        for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, ((off[u] & ~kLow) + gcol) | coldead, 0, gv[u]);
+            for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, (off[u] & ~kLow) | lane_eff, chunk_base, gv[u]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, ((off[u] & ~kLow) + gcol) | coldead, 0, gv[u]);
+        }
         meta(bt + 1, offn, rown);  // the next batch's offsets, while these rows arrive
         if (bt < b_end && k != cur) {
             if (cur >= 0) finish(cur);
@@ -670,15 +691,29 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
         if constexpr (DOTS) {
             // a group past its range has cur's row (or row 0) and reads zeros
             const int kk = bt < b_end ? k : max(cur, 0);
+            // the batch's neighbour rows, all reads issued before the dots
+            vec_t<float, V> nv[K];
+#pragma unroll
+            for (int u = 0; u < K; ++u) {
+                if constexpr (kNbPerm) {
+                    // byte 0: the lane's column offset, byte 1: nb (v_perm_b32
+                    // selectors 0-3 pick bytes of the second source, 4-7 of the
+                    // first, 0x0c gives zero); the LUT chunk starts at LDS
+                    // address 0, so this is the LDS address itself
+                    const uint32_t addr = __builtin_amdgcn_perm(off[u], lane_lds, 0x0c0c0400u);
+                    nv[u] = *reinterpret_cast<const __attribute__((address_space(3))) vec_t<float, V> *>(addr);
+                } else {
+                    // NBP: the sort kernel left nb in the offset's low bits (< R)
+                    const int nb = NBP ? static_cast<int>(off[u] & kLow) : (kk ^ (1 << (off[u] & 7u))) & (R - 1);
+                    nv[u] = *reinterpret_cast<const vec_t<float, V> *>(lut_s + nb * P + j * V);
+                }
+            }
             float d[K];
 #pragma unroll
             for (int u = 0; u < K; ++u) {
-                // NBP: the sort kernel left nb in the offset's low bits (< R)
-                const int nb = NBP ? static_cast<int>(off[u] & kLow) : (kk ^ (1 << (off[u] & 7u))) & (R - 1);
-                const vec_t<float, V> nv = *reinterpret_cast<const vec_t<float, V> *>(lut_s + nb * P + j * V);
                 float sd = 0.f;
 #pragma unroll
-                for (int e = 0; e < V; ++e) sd += gv[u][e] * (nv[e] - lkv[e]);
+                for (int e = 0; e < V; ++e) sd += gv[u][e] * (nv[u][e] - lkv[e]);
                 d[u] = sd;
             }
 #pragma unroll
@@ -1397,8 +1432,12 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     p.rows_chunks = (d.out_f + rows_chunk - 1) / rows_chunk;
     p.rows_part_off = ((d.rows + 1) * 4 + 15) & ~15;
     p.rows_lds_bytes = p.rows_part_off + (kRowsThreads / p.rows_slices) * 2 * rows_chunk * 4;
-    p.rows_lut_off = (p.rows_lds_bytes + 15) & ~15;  // with dots: the LUT chunk [R][P] f32
-    p.rows_lds_dots_bytes = p.rows_lut_off + d.rows * rows_chunk * 4;
+    // with dots: the LUT chunk [R][P] f32 at offset 0 (its rows' addresses
+    // are then byte permutes), then the row starts and the split-row slots
+    p.rows_lut_off = 0;
+    p.rows_dots_rs_off = d.rows * rows_chunk * 4;
+    p.rows_dots_part_off = (p.rows_dots_rs_off + (d.rows + 1) * 4 + 15) & ~15;
+    p.rows_lds_dots_bytes = p.rows_dots_part_off + (kRowsThreads / p.rows_slices) * 2 * rows_chunk * 4;
     // the neighbour row fits below the item offset (a multiple of P * 4 bytes)
     p.rows_nb_pack = rows_chunk * 4 >= d.rows;
     p.sort_lds_bytes = ((kSortThreads / kWave) * d.rows + d.rows + kSortThreads / kWave) * 4 + (kSortThreads / kWave) * 8 * 4;
@@ -1622,7 +1661,8 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
     r.rows = d.rows;
     r.tables = d.tables;
     r.slots = p.sort_slots;
-    r.part_off = p.rows_part_off;
+    r.part_off = dots ? p.rows_dots_part_off : p.rows_part_off;
+    r.rs_off = dots ? p.rows_dots_rs_off : 0;
     r.lut = lut;
     r.lut_bytes = static_cast<uint32_t>(static_cast<size_t>(d.tables) * d.rows * d.out_f * esize);
     r.pdot = dots ? reinterpret_cast<float *>(ws + p.ws_pdot) : nullptr;

@@ -62,7 +62,8 @@ struct BackwardPlan {
     int rows_chunks;    // column chunks of P
     int rows_part_off;  // LDS byte offset of the split-row slots
     int rows_lds_bytes;
-    int rows_lut_off;   // with partial STE dots: LDS byte offset of the LUT chunk
+    int rows_lut_off;   // with partial STE dots: LDS byte offset of the LUT chunk (0)
+    int rows_dots_rs_off, rows_dots_part_off;  // with partial STE dots: row starts, split-row slots
     int rows_lds_dots_bytes;
     bool rows_nb_pack;       // slot offsets carry the neighbour row (min-margin dots, P * 4 >= R)
     // sort kernel
