@@ -863,7 +863,7 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
     static_assert(K <= S, "a batch's dots are scattered over the row group");
     extern __shared__ __align__(16) unsigned char lds[];
     float *lut_s = reinterpret_cast<float *>(lds + a.lut_off);             // [R][pitch] table rows, f32
-    int *cnt = reinterpret_cast<int *>(lds + a.cnt_off);                   // [waves][R] counts -> offsets
+    int *cnt = reinterpret_cast<int *>(lds + a.cnt_off);                   // [R][waves] counts -> offsets
     int *off = reinterpret_cast<int *>(lds + a.off_off);                   // [R + 1] row starts
     uint2 *ent = reinterpret_cast<uint2 *>(lds + a.sorted_off);           // [slots] sorted entries (see below)
     float *us = reinterpret_cast<float *>(lds + a.u_off);                  // [slots] margin u, by position
@@ -887,12 +887,14 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
 
     // 1. one ballot per code bit gives each item the mask of equal codes in
     //    its wave: its rank is the count below it, and the first item of
-    //    each code writes the code's count to cnt[wave][code] after the wave
-    //    has zeroed its counts (one wave's LDS operations complete in order)
+    //    each code writes the code's count to cnt[code][wave] after the wave
+    //    has zeroed its counts (one wave's LDS operations complete in order).
+    //    A row's counts of all waves are contiguous: the scan reads and
+    //    writes them as vectors at one base address.
     auto ballots = [&](uint64_t rr, int n_tile) -> int {
         const bool valid = tid < n_tile;
         const int code = rec_code(rr) & (R - 1);  // masks keep a corrupt record in range
-        for (int k = lane; k < R; k += kWave) cnt[wave * R + k] = 0;
+        for (int k = lane; k < R; k += kWave) cnt[k * kWaves + wave] = 0;
         if (wave * kWave >= n_tile) return 0;
         uint64_t same = __ballot(valid);
         for (int c = 0; c < C; ++c) {
@@ -900,7 +902,7 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
             same &= ((code >> c) & 1) ? bc : ~bc;
         }
         const int rank = __popcll(same & ((1ull << lane) - 1ull));
-        if (valid && rank == 0) cnt[wave * R + code] = __popcll(same);
+        if (valid && rank == 0) cnt[code * kWaves + wave] = __popcll(same);
         return rank;
     };
 
@@ -965,11 +967,17 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
         int padded = 0;
         if (tid < nscan) {
             const int kr = min(tidl, R - 1);  // in-bounds reads, zeroed past R
+            int x[kWaves];
+#pragma unroll
+            for (int w = 0; w < kWaves; w += 4) {
+                const vec_t<int, 4> v = *reinterpret_cast<const vec_t<int, 4> *>(cnt + kr * kWaves + w);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[w + e] = v[e];
+            }
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) {
-                const int x = cnt[w * R + kr];
                 h[w] = total;
-                total += tidl < R ? x : 0;
+                total += tidl < R ? x[w] : 0;
             }
             padded = (total + K - 1) / K * K;
             incl = wave_inclusive_scan(padded);
@@ -985,7 +993,12 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
             off[tidl] = excl;
             if (tid == R - 1) off[R] = incl;
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) cnt[w * R + tidl] = excl + h[w];
+            for (int w = 0; w < kWaves; w += 4) {
+                vec_t<int, 4> v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = excl + h[w + e];
+                *reinterpret_cast<vec_t<int, 4> *>(cnt + tidl * kWaves + w) = v;
+            }
             for (int q = excl + total; q < excl + padded; ++q) {
                 ent[q] = make_uint2(kOutOfRange, kPadSlot);
                 us[q] = 0.f;
@@ -999,7 +1012,7 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
         //    neighbour row nb | r << 18 | item << 21.
         if (tid < n_tile) {
             const int code = rec_code(r0) & (R - 1), r = rec_r(r0) & 7;
-            const int pos = cnt[wave * R + code] + rank;
+            const int pos = cnt[code * kWaves + wave] + rank;
             const uint32_t nbo = static_cast<uint32_t>((code ^ (1 << r)) & (R - 1)) * (P * 4u);
             ent[pos] = make_uint2(static_cast<uint32_t>(tile0 + tidl) * static_cast<uint32_t>(O) * 4u,
                                   nbo | (static_cast<uint32_t>(r) << 18) | (static_cast<uint32_t>(tidl) << 21));
