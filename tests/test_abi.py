@@ -221,3 +221,29 @@ def test_noalloc_backward_rejects_before_any_launch(lib):
                                                     7, 0, fake, fake, fake, None) == 1
     assert lib.tropnn_hip_pairwise_backward_noalloc(4, 8, 8, 2, 99, fake, fake, 0, fake, None, fake, fake, 1.0,
                                                     0, 0, fake, fake, fake, None) == 2
+
+
+def test_autograd_operator_loads_and_binds(lib):
+    """The autograd operator library loads without a GPU, is bound to this
+    library's entry points, refuses another ABI version, and rejects CPU
+    tensors before any call into the library."""
+    import torch
+
+    if not ph.OPS_LIBRARY.exists():
+        pytest.skip("libtropnn_hip_torch.so not built (run __graft_entry__.build())")
+    op = ph._pairwise_op()
+    args = [a.name for a in op._schema.arguments]
+    assert args == ["latent", "anchors", "thresholds", "lut", "lut_read", "index_offsets", "index_entries",
+                    "ste", "min_margin", "surrogate", "output_scale", "route_mode"]
+    assert len(op._schema.returns) == 3
+    addr = ctypes.cast(lib.tropnn_hip_pairwise_forward, ctypes.c_void_p).value
+    with pytest.raises(RuntimeError, match="ABI version"):
+        torch.ops.tropnn_hip.bind_abi(addr, addr, addr, addr, ph.ABI_VERSION + 1)
+    x = torch.zeros(2, 1, 8)
+    anchors = torch.zeros(3, 2, 2, dtype=torch.int64)
+    with pytest.raises(ValueError, match="one GPU"):
+        op(x, anchors, torch.zeros(3, 2), torch.zeros(3, 4, 5), torch.zeros(3, 4, 5), None, None,
+           True, True, 0, 1.0, 0)
+    with pytest.raises(ValueError, match="surrogate"):
+        op(x, anchors, torch.zeros(3, 2), torch.zeros(3, 4, 5), torch.zeros(3, 4, 5), None, None,
+           True, True, 7, 1.0, 0)

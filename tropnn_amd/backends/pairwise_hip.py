@@ -1,9 +1,9 @@
 """HIP backend of PairwiseLinear: ctypes binding of libtropnn_hip.so plus the
-autograd Function around it.
+autograd operator around it.
 
 Public entry points mirror the reference's backend wrappers:
   * pairwise_hip(...)          -- like pairwise_tilelang (backends/pairwise_tilelang.py:537-549):
-                                  autograd Function, returns (output, indices, margins)
+                                  autograd operator, returns (output, indices, margins)
   * pairwise_hip_forward(...)  -- like pairwise_zig_forward (backends/pairwise_zig.py:35-103):
                                   eval-only forward with an f32 or f16 LUT
   * has_pairwise_hip()         -- capability probe like has_pairwise_zig / has_tilelang
@@ -35,8 +35,13 @@ ERR_NAMES = {1: "invalid argument", 2: "unsupported", 3: "HIP error"}
 
 _PKG_DIR = Path(__file__).resolve().parent.parent
 DEFAULT_LIBRARY = _PKG_DIR / "libtropnn_hip.so"
+# host-only torch operator library (csrc/autograd_op.cpp): the autograd
+# operator behind pairwise_hip, which calls the C ABI of the library above
+OPS_LIBRARY = _PKG_DIR / "libtropnn_hip_torch.so"
 _LOCK = threading.Lock()
 _LIB: ctypes.CDLL | None = None
+_PAIRWISE_OP: Any = None
+_ROUTE_MODES = {False: 0, True: 1, "codes": 2}
 # Per-anchors-tensor caches live as attributes of the anchors tensor object
 # itself (not in a table keyed by address: the caching allocator reuses the
 # addresses of freed tensors), validated by the tensor's version counter,
@@ -140,12 +145,50 @@ def load_library() -> ctypes.CDLL:
     return _LIB
 
 
+def _pairwise_op() -> Any:
+    """torch.ops.tropnn_hip.pairwise, loaded once and bound to the entry
+    points of the libtropnn_hip.so that load_library() loaded and checked.
+    Raises RuntimeError if the operator library is not built."""
+    global _PAIRWISE_OP
+    if _PAIRWISE_OP is not None:
+        return _PAIRWISE_OP
+    lib = load_library()
+    with _LOCK:
+        if _PAIRWISE_OP is not None:
+            return _PAIRWISE_OP
+        if not OPS_LIBRARY.exists():
+            raise RuntimeError(
+                f"PairwiseLinear backend='hip' needs {OPS_LIBRARY}, which is not built; "
+                "build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                "or `make -C tropnn_amd/csrc`"
+            )
+        if not hasattr(torch.ops.tropnn_hip, "bind_abi"):
+            try:
+                torch.ops.load_library(str(OPS_LIBRARY))
+            except OSError as exc:
+                raise RuntimeError(f"cannot load {OPS_LIBRARY}: {exc}") from exc
+
+        def addr(name: str) -> int:
+            return ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+
+        torch.ops.tropnn_hip.bind_abi(
+            addr("tropnn_hip_pairwise_forward"),
+            addr("tropnn_hip_pairwise_backward"),
+            addr("tropnn_hip_pairwise_backward_workspace_size"),
+            addr("tropnn_hip_last_error"),
+            lib.tropnn_hip_abi_version(),
+        )
+        _PAIRWISE_OP = torch.ops.tropnn_hip.pairwise.default
+    return _PAIRWISE_OP
+
+
 def has_pairwise_hip() -> bool:
-    """True when the native library loads and a GPU is visible."""
+    """True when the native libraries load and a GPU is visible."""
     if not torch.cuda.is_available():
         return False
     try:
         load_library()
+        _pairwise_op()
     except RuntimeError:
         return False
     return True
@@ -214,6 +257,11 @@ def anchor_index(anchors: Tensor, in_features: int) -> tuple[Tensor, Tensor]:
     hit = getattr(anchors, _INDEX_ATTR, None)
     if hit is not None and hit[0] == key:
         return hit[1], hit[2]
+    if anchors.dtype != torch.int64:
+        raise TypeError(f"anchors must be int64, got {anchors.dtype}")
+    if anchors.ndim != 3 or anchors.shape[2] != 2:
+        raise ValueError(f"anchors must have shape [tables, comparisons, 2], got {tuple(anchors.shape)}")
+    _require_gpu(anchors)
     tables, comps, _ = anchors.shape
     offsets = torch.empty(in_features + 1, device=anchors.device, dtype=torch.int32)
     entries = torch.empty(max(2 * tables * comps, 1), device=anchors.device, dtype=torch.int32)
@@ -319,106 +367,6 @@ def _route_forward(
     return out.view(batch, steps, out_features), record, idx_view, mar_view, saved
 
 
-class _PairwiseHipFunction(torch.autograd.Function):
-    """Forward: fused route + gather + scale. Backward: table-major LUT
-    gradient + min-margin or full STE (fast_sigmoid_odd or izhikevich
-    surrogate), then input / threshold gradients. The full STE needs every
-    comparison's margin, which the forward then keeps. Contract of
-    _PairwiseTileLangFunction (backends/pairwise_tilelang.py:460-534): the
-    gradient tuple is (latent, None, thresholds, lut, None, ...), indices and
-    margins are non-differentiable."""
-
-    @staticmethod
-    def forward(  # type: ignore[override]
-        ctx: Any,
-        latent: Tensor,
-        anchors: Tensor,
-        thresholds: Tensor,
-        lut: Tensor,
-        lut_read: Tensor,
-        ste: bool,
-        min_margin: bool,
-        surrogate: str,
-        output_scale: float,
-        return_route: bool | str,
-    ) -> tuple[Tensor, Tensor, Tensor]:
-        needs_lut = ctx.needs_input_grad[3]
-        needs_route = ste and (ctx.needs_input_grad[0] or ctx.needs_input_grad[2])
-        want_record = needs_lut or needs_route
-        out, record, indices, margins, saved_margins = _route_forward(
-            latent,
-            anchors,
-            thresholds,
-            lut_read,
-            output_scale=output_scale,
-            want_record=want_record,
-            return_route=return_route,
-            want_margins=needs_route and not min_margin,
-        )
-        # the anchor index is built (once per anchors version) at forward
-        # time, outside any backward-pass graph capture
-        ctx.index = anchor_index(anchors, latent.shape[2]) if (ste and ctx.needs_input_grad[0]) else None
-        ctx.save_for_backward(record, anchors, lut_read, saved_margins)
-        ctx.dims = tuple(latent.shape) + (lut_read.shape[2],)
-        ctx.ste = ste
-        ctx.ste_mode = STE_MIN_MARGIN if min_margin else STE_FULL
-        ctx.surrogate = surrogate
-        ctx.output_scale = float(output_scale)
-        ctx.mark_non_differentiable(indices, margins)
-        return out, indices, margins
-
-    @staticmethod
-    def backward(ctx: Any, grad_output: Tensor, grad_indices: Tensor | None, grad_margins: Tensor | None):  # type: ignore[override]
-        del grad_indices, grad_margins
-        record, anchors, lut_read, saved_margins = ctx.saved_tensors
-        batch, steps, in_features, out_features = ctx.dims
-        tables, comps, _ = anchors.shape
-        items = batch * steps
-        dev = grad_output.device
-        want_x = ctx.ste and ctx.needs_input_grad[0]
-        want_thr = ctx.ste and ctx.needs_input_grad[2]
-        want_lut = ctx.needs_input_grad[3]
-        if not (want_x or want_thr or want_lut):
-            return (None,) * 10
-        g = grad_output.reshape(items, out_features).to(torch.float32).contiguous()
-        grad_x = torch.empty((items, in_features), device=dev, dtype=torch.float32) if want_x else None
-        grad_thr = torch.empty((tables, comps), device=dev, dtype=torch.float32) if want_thr else None
-        grad_lut = torch.empty((tables, 1 << comps, out_features), device=dev, dtype=torch.float32) if want_lut else None
-        lib = load_library()
-        lut_dtype = LUT_F16 if lut_read.dtype == torch.float16 else LUT_F32
-        ws_bytes = lib.tropnn_hip_pairwise_backward_workspace_size(
-            items, in_features, out_features, tables, comps, lut_dtype, ctx.ste_mode
-        )
-        workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
-        offsets, entries = ctx.index if want_x else (None, None)
-        rc = lib.tropnn_hip_pairwise_backward(
-            items,
-            in_features,
-            out_features,
-            tables,
-            comps,
-            _ptr(g),
-            _ptr(lut_read),
-            lut_dtype,
-            _ptr(record),
-            _ptr(saved_margins),
-            _ptr(offsets),
-            _ptr(entries),
-            ctx.output_scale,
-            ctx.ste_mode,
-            SURROGATE_IDS[ctx.surrogate],
-            _ptr(grad_x),
-            _ptr(grad_thr),
-            _ptr(grad_lut),
-            _ptr(workspace),
-            ws_bytes,
-            _stream(dev),
-        )
-        _check(rc, "tropnn_hip_pairwise_backward")
-        gx = grad_x.view(batch, steps, in_features) if grad_x is not None else None
-        return gx, None, grad_thr, grad_lut, None, None, None, None, None, None
-
-
 def pairwise_hip(
     latent: Tensor,
     anchors: Tensor,
@@ -449,38 +397,49 @@ def pairwise_hip(
     layers/pairwise.py:245-247). output_scale defaults to 1.0, the
     pairwise_tilelang contract (the module scales afterwards); the package's
     PairwiseLinear passes its 1/sqrt(T) here so the scale is fused.
+
+    The autograd operator (torch.ops.tropnn_hip.pairwise, csrc/autograd_op.cpp)
+    has the contract of _PairwiseTileLangFunction
+    (backends/pairwise_tilelang.py:460-534): gradients flow to latent,
+    thresholds and lut; indices and margins are non-differentiable. Forward:
+    one fused route + gather + scale launch, which also writes the per-(table,
+    item) route record the backward reads when a gradient will be asked for
+    (none under torch.no_grad). Backward: table-major LUT gradient + min-margin
+    or full STE (fast_sigmoid_odd or izhikevich surrogate), then input /
+    threshold gradients; only the gradients the backward pass asks for are
+    computed. The full STE needs every comparison's margin, which the forward
+    then keeps.
     """
-    if surrogate not in SURROGATE_IDS:
+    surrogate_id = SURROGATE_IDS.get(surrogate)
+    if surrogate_id is None:
         raise ValueError(f"Pairwise HIP backend does not support surrogate={surrogate!r}")
-    if return_route not in (True, False, "codes"):
+    route_mode = _ROUTE_MODES.get(return_route) if isinstance(return_route, (bool, str)) else None
+    if route_mode is None:
         raise ValueError(f"return_route must be True, False or 'codes', got {return_route!r}")
     _require_gpu(latent, anchors, thresholds, lut)
-    if lut_read is None:
-        lut_read = lut
-    if not torch.is_grad_enabled():
-        # no graph will be recorded (inference under torch.no_grad): the
-        # kernels write no route record; outputs as the Function returns them
-        out, _, indices, margins, _ = _route_forward(
-            latent.detach(),
-            anchors,
-            thresholds.detach(),
-            lut_read.detach(),
-            output_scale=float(output_scale),
-            want_record=False,
-            return_route=return_route if return_route == "codes" else bool(return_route),
-        )
-        return out, indices, margins
-    return _PairwiseHipFunction.apply(
+    op = _pairwise_op()
+    if latent.ndim != 3:
+        raise ValueError(f"latent must have shape [batch, steps, in_features], got {tuple(latent.shape)}")
+    in_features = latent.shape[2]
+    check_anchors(anchors, in_features)
+    offsets = entries = None
+    if ste and latent.requires_grad and torch.is_grad_enabled():
+        # built once per anchors version, at forward time (outside any
+        # backward-pass graph capture)
+        offsets, entries = anchor_index(anchors, in_features)
+    return op(
         latent,
         anchors,
         thresholds,
         lut,
-        lut_read.detach(),
+        lut if lut_read is None else lut_read,
+        offsets,
+        entries,
         bool(ste),
         bool(use_min_margin_ste),
-        surrogate,
+        surrogate_id,
         float(output_scale),
-        return_route if return_route == "codes" else bool(return_route),
+        route_mode,
     )
 
 

@@ -145,4 +145,4 @@ class RoutedLinearBase(nn.Module, ABC):
             self._route_debug = RouteDebug(indices=indices.detach(), margins=margins.detach())
         else:
             self._route_debug = None
-        return output.to(dtype=input_dtype)
+        return output if output.dtype == input_dtype else output.to(dtype=input_dtype)

@@ -118,7 +118,7 @@ class PairwiseLinear(RoutedLinearBase):
         )
 
     def _project_input(self, x: Tensor, compute_dtype: torch.dtype) -> Tensor:
-        return x.to(compute_dtype)
+        return x if x.dtype == compute_dtype else x.to(compute_dtype)
 
     def _lut_for_reading(self) -> Tensor:
         """The LUT tensor the kernels read: the f32 parameter, or its f16 copy
