@@ -52,6 +52,7 @@ struct FwdArgs {
     int row_bytes, table_bytes;
     int lpt_log2, per_wave, codes_pitch;
     int codes_off, red_off;
+    int wave_lpr_log2, wave_tile_bytes, wave_x_off;  // wave-item kernel
 };
 
 // Ballots whose comparators a wave prefetches: two cover 16 tables of up to
@@ -401,6 +402,227 @@ __global__ __launch_bounds__(1024) void pairwise_forward_multi_kernel(FwdArgs a)
     }
 }
 
+// Large batches whose LUT row (or column tile of it) is 128, 256, 512 or 1024
+// bytes: every wave owns whole items, so no wave waits for another after the
+// comparators are staged. Lane (g, j) of a wave holds 16 bytes at byte 16 j of
+// item g's row tile (P = 64 / (tile bytes / 16) items per wave).
+//   1. The comparators of every table go to LDS once per workgroup, 8 bytes
+//      each (both anchors as 16-bit indices, the threshold's bits), and each
+//      wave stages its items' input rows: the workgroup's only barrier.
+//   2. Route with one lane per table (64 tables a round): the comparisons in
+//      order, each margin the same two f32 subtractions as the other
+//      kernels', the min-margin pick by the same key order (NaN first, then
+//      the smaller |m|, then the lower comparison); codes to LDS.
+//   3. Gather: per block of per_wave tables, 16-byte row loads of every table
+//      of the block (the next block's loads issued before this one's are
+//      summed), the rows summed in table order and the blocks in block order,
+//      as the other forward kernels sum them: the outputs are bit-identical.
+constexpr int kWaveThreads = 256;
+constexpr int kWaveWaves = kWaveThreads / kWave;
+constexpr int kWaveBlock = 16;    // tables per block, at most (the plan's per_wave)
+constexpr int kWaveMinItems = 2048;
+constexpr int kWaveMinWaves = 1024;  // below, the one-item and multi-item kernels spread the work wider
+constexpr int kWaveRing = 2;         // blocks of row loads in flight (3 and 4 measured slower)
+
+struct WaveComparator {
+    uint32_t ab;  // anchors a | b << 16
+    float thr;
+};
+
+template <typename T, int P, int K, bool TRAIN, bool DEBUG>
+__global__ __launch_bounds__(kWaveThreads) void pairwise_forward_wave_kernel(FwdArgs a) {
+    constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements of a 16-byte load
+    constexpr int kC = TROPNN_MAX_COMPARISONS;
+    constexpr int lpr_log2 = P == 1 ? 6 : P == 2 ? 5 : P == 4 ? 4 : 3;  // lanes per row tile: 64 / P
+    static_assert(P == 1 || P == 2 || P == 4 || P == 8, "1, 2, 4 or 8 items per wave");
+    using u32x4 = vec_t<uint32_t, 4>;
+    extern __shared__ __align__(16) unsigned char lds[];
+    WaveComparator *cmp = reinterpret_cast<WaveComparator *>(lds);  // [T][kC]
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    float *xs = reinterpret_cast<float *>(lds + a.wave_x_off) + wave * P * a.in_f;  // [in_f][P]: items interleaved
+    uint8_t *cw = lds + a.codes_off + wave * P * a.codes_pitch;  // [P][blocks][16]
+    const int item0 = (blockIdx.x * kWaveWaves + wave) * P;
+    const int nitems = max(0, min(P, a.items - item0));
+    const int C = a.comps;
+
+    // 1. comparators (kC slots per table; the unused ones compare x[0] with
+    // itself); this wave's input rows
+#pragma unroll 4
+    for (int k = tid; k < a.tables * kC; k += kWaveThreads) {
+        const int t = k / kC, c = k - t * kC;
+        const size_t tc = static_cast<size_t>(t) * C + min(c, C - 1);  // loads issued unconditionally
+        const uint32_t ia = static_cast<uint32_t>(clamp_index(a.anchors[2 * tc], a.in_f));
+        const uint32_t ib = static_cast<uint32_t>(clamp_index(a.anchors[2 * tc + 1], a.in_f));
+        const float th = a.thr[tc];
+        cmp[k] = c < C ? WaveComparator{ia | (ib << 16), th} : WaveComparator{0u, 0.f};
+    }
+    {
+        // element f of item i at xs[f * P + i], so that one vector read gets
+        // feature f of all P items; absent items read zeros
+        const float *src = a.x + static_cast<size_t>(item0) * a.in_f;
+        const int n = nitems * a.in_f;
+        if ((a.in_f & 3) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+            for (int k = 4 * lane; k < P * a.in_f; k += 4 * kWave) {
+                const int i = k / a.in_f, f = k - i * a.in_f;
+                vec_t<float, 4> v = {0.f, 0.f, 0.f, 0.f};
+                if (k < n) v = *reinterpret_cast<const vec_t<float, 4> *>(src + k);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xs[(f + e) * P + i] = v[e];
+            }
+        } else {
+            for (int k = lane; k < P * a.in_f; k += kWave) {
+                const int i = k / a.in_f, f = k - i * a.in_f;
+                xs[f * P + i] = k < n ? src[k] : 0.f;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 2. route: lane = table (lanes past the last table idle), its C
+    // comparisons in order, each read of an input giving all P items' values
+    const bool tile0 = blockIdx.y == 0;
+    for (int t0 = 0; t0 < a.tables; t0 += kWave) {
+        const int t = t0 + lane;
+        if (t < a.tables) {
+            const int tblk = t / a.per_wave;
+            const int cpos = tblk * kWaveBlock + (t - tblk * a.per_wave);  // the code's byte in the list
+            uint32_t code[P], key[P];  // min-margin pick: key 0 for NaN, else bits(|m|) + 1
+            int pick[P];
+            float pm[P];
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                code[i] = 0u;
+                key[i] = 0xFFFFFFFFu;
+                pick[i] = 0;
+                pm[i] = 0.f;
+            }
+            for (int c = 0; c < C; ++c) {
+                const WaveComparator q = cmp[t * kC + c];
+                const vec_t<float, P> xa = *reinterpret_cast<const vec_t<float, P> *>(xs + (q.ab & 0xFFFFu) * P);
+                const vec_t<float, P> xb = *reinterpret_cast<const vec_t<float, P> *>(xs + (q.ab >> 16) * P);
+#pragma unroll
+                for (int i = 0; i < P; ++i) {
+                    const float m = (xa[i] - xb[i]) - q.thr;
+                    code[i] |= (m > 0.f ? 1u : 0u) << c;
+                    if constexpr (TRAIN) {
+                        const float mag = fabsf(m);
+                        const uint32_t k = mag != mag ? 0u : __builtin_bit_cast(uint32_t, mag) + 1u;
+                        if (k < key[i]) {
+                            key[i] = k;
+                            pick[i] = c;
+                            pm[i] = m;
+                        }
+                    }
+                    if constexpr (DEBUG) {
+                        if (tile0 && i < nitems && a.margins != nullptr)
+                            a.margins[(static_cast<size_t>(item0 + i) * a.tables + t) * C + c] = m;
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                if (i < nitems) {
+                    cw[i * a.codes_pitch + cpos] = static_cast<uint8_t>(code[i]);
+                    const size_t bt = static_cast<size_t>(item0 + i) * a.tables + t;
+                    if constexpr (TRAIN) {
+                        if (tile0)
+                            a.rec[static_cast<size_t>(t) * a.items + item0 + i] =
+                                static_cast<uint64_t>(__builtin_bit_cast(uint32_t, pm[i])) |
+                                (static_cast<uint64_t>(code[i]) << 32) | (static_cast<uint64_t>(pick[i]) << 48);
+                    }
+                    if constexpr (DEBUG) {
+                        if (tile0) {
+                            if (a.indices != nullptr) a.indices[bt] = code[i];
+                            if (a.codes != nullptr) a.codes[bt] = static_cast<uint8_t>(code[i]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    // LDS operations of one wave complete in order: its code lists are ready
+
+    // 3. gather
+    const int g = lane >> lpr_log2, j = lane & ((1 << lpr_log2) - 1);
+    const int item = item0 + g;
+    const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(a.lut, a.lut_bytes);
+    const uint32_t lane_off =
+        (static_cast<uint32_t>(blockIdx.y) * static_cast<uint32_t>(a.wave_tile_bytes) + 16u * static_cast<uint32_t>(j)) |
+        (g < nitems ? 0u : kOutOfRange);
+    const uint8_t *cg = cw + (g < nitems ? g : 0) * a.codes_pitch;
+    const int nblk = (a.tables + a.per_wave - 1) / a.per_wave;
+
+    // block b's rows: codes of its tables (16 at a time from LDS), one load
+    // per table; a block past the last loads zeros (every offset out of range)
+    auto issue = [&](int b, u32x4 (&w)[kWaveBlock]) {
+        const int tb = b * a.per_wave, n = max(0, min(a.per_wave, a.tables - tb));
+        const u32x4 cv = *reinterpret_cast<const u32x4 *>(cg + min(b, nblk - 1) * kWaveBlock);
+#pragma unroll
+        for (int u = 0; u < kWaveBlock; ++u) {
+            const uint32_t code = (cv[u >> 2] >> (8 * (u & 3))) & 0xFFu;
+            const uint32_t voff = u < n ? lane_off + code * static_cast<uint32_t>(a.row_bytes) : kOutOfRange;
+            const int soff = u < n ? (tb + u) * a.table_bytes : 0;
+            w[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, 0));
+        }
+        // the block's loads stay together, ahead of the sums that follow
+        // (the scheduler would otherwise sink each load to its add)
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Every slot of a block is summed: a slot past the block's tables loaded
+    // zeros (out of range), and adding +0 changes no partial sum, none being
+    // -0 (the sum starts at +0; an exact cancellation rounds to +0 and a sum
+    // of floats cannot underflow), so the bits equal the other kernels'
+    // sums over the live rows alone.
+    float tot[E];
+    auto consume = [&](int b, const u32x4 (&w)[kWaveBlock]) {
+        float acc[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[e] = 0.f;
+#pragma unroll
+        for (int u = 0; u < kWaveBlock; ++u) {
+            {
+                if constexpr (sizeof(T) == 4) {
+                    // the whole vector, then its elements: hipcc (ROCm 7.2)
+                    // bit-casts an element of an ext_vector_type value from
+                    // the vector's first element
+                    const vec_t<float, 4> f = __builtin_bit_cast(vec_t<float, 4>, w[u]);
+#pragma unroll
+                    for (int e = 0; e < E; ++e) acc[e] += f[e];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < E; ++e)
+                        acc[e] = (e & 1) ? add_f16_mix<true>(acc[e], w[u][e >> 1]) : add_f16_mix<false>(acc[e], w[u][e >> 1]);
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) tot[e] = b == 0 ? acc[e] : tot[e] + acc[e];  // + 0 past the last block
+    };
+    // a ring of K blocks in flight: block b + K - 1 is issued before block b
+    // is summed. Straight-line code: the blocks past the last are issued and
+    // summed too (zeros), so that every wait counts exactly the loads issued
+    // since (a conditional issue would merge two counts into the smaller).
+    u32x4 w[K][kWaveBlock];
+#pragma unroll
+    for (int q = 0; q < K - 1; ++q) issue(q, w[q]);
+    for (int b0 = 0; b0 < nblk; b0 += K) {
+#pragma unroll
+        for (int q = 0; q < K; ++q) {
+            const int b = b0 + q;
+            issue(b + K - 1, w[(q + K - 1) % K]);
+            consume(b, w[q]);
+        }
+    }
+    if (g < nitems) {
+        float y[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) y[e] = tot[e] * a.scale;
+        const int col = blockIdx.y * (a.wave_tile_bytes / static_cast<int>(sizeof(T))) + j * E;
+        store_f32_nt<E>(a.out + static_cast<size_t>(item) * a.out_f + col, y);
+    }
+}
+
 // Route only (no gather): one thread per (item, table) evaluates the table's
 // comparisons in order and writes any of uint8 codes, int64 codes and f32
 // margins, laid out [items][tables] and [items][tables][comparisons]. The
@@ -674,6 +896,25 @@ __global__ __launch_bounds__(kRouteThreads) void pairwise_route_kernel(RouteArgs
     if (a.indices != nullptr) a.indices[k] = code;
 }
 
+template <typename T, int P>
+hipError_t launch_wave_items(const FwdArgs &args, const ForwardPlan &p, bool train, bool debug, hipStream_t stream) {
+    constexpr int K = kWaveRing;
+    auto kernel = train ? (debug ? pairwise_forward_wave_kernel<T, P, K, true, true> : pairwise_forward_wave_kernel<T, P, K, true, false>)
+                        : (debug ? pairwise_forward_wave_kernel<T, P, K, false, true> : pairwise_forward_wave_kernel<T, P, K, false, false>);
+    return launch_kernel(TROPNN_KERNEL_FORWARD, kernel, dim3(p.wave_blocks, p.wave_tiles), dim3(kWaveThreads),
+                         p.wave_lds_bytes, stream, args);
+}
+
+template <typename T>
+hipError_t launch_wave(const FwdArgs &args, const ForwardPlan &p, bool train, bool debug, hipStream_t stream) {
+    switch (kWave >> p.wave_lpr_log2) {
+        case 8: return launch_wave_items<T, 8>(args, p, train, debug, stream);
+        case 4: return launch_wave_items<T, 4>(args, p, train, debug, stream);
+        case 2: return launch_wave_items<T, 2>(args, p, train, debug, stream);
+        default: return launch_wave_items<T, 1>(args, p, train, debug, stream);
+    }
+}
+
 template <typename T, int N>
 hipError_t launch_typed(const FwdArgs &args, const ForwardPlan &p, bool train, bool debug, hipStream_t stream) {
     const dim3 grid(p.blocks, p.o_tiles), block(p.threads);
@@ -773,6 +1014,45 @@ ForwardPlan plan_forward(const Dims &d) {
         }
     }
 
+    // wave-item kernel: large batches (>= kWaveMinItems items and >=
+    // kWaveMinWaves waves) whose row, or 1024-byte column tile of it, is 128
+    // to 1024 bytes (a power of two), tables summed in the multi-item
+    // kernel's blocks of at most 16; comparators, input rows and code lists
+    // within 64 KB of LDS
+    p.wave = false;
+    {
+        const int row_bytes = d.out_f * esize;
+        const int tile = row_bytes <= 1024 ? row_bytes : 1024;
+        const bool pow2 = (tile & (tile - 1)) == 0;
+        const int ipw = tile >= 128 ? kWave / (tile / 16) : 1;
+        if (d.items >= kWaveMinItems && (d.items + ipw - 1) / ipw >= kWaveMinWaves && tile >= 128 && pow2 &&
+            row_bytes % tile == 0) {
+            const int w16 = (d.tables + kWaveBlock - 1) / kWaveBlock;
+            const int per16 = (d.tables + w16 - 1) / w16;
+            const int lpr = tile / 16;
+            const int pitch = w16 * kWaveBlock;  // block b's codes at byte 16 b
+            int off = d.tables * TROPNN_MAX_COMPARISONS * 8;
+            const int x_off = off;
+            off += kWaveWaves * ipw * d.in_f * 4;
+            off = (off + 15) & ~15;
+            const int c_off = off;
+            off += kWaveWaves * ipw * pitch;
+            if (off <= 64 * 1024) {
+                p.wave = true;
+                p.per_wave = per16;
+                p.codes_pitch = pitch;
+                p.codes_off = c_off;
+                p.wave_x_off = x_off;
+                p.wave_lpr_log2 = ilog2(lpr);
+                p.wave_tile_bytes = tile;
+                p.wave_tiles = row_bytes / tile;
+                p.wave_blocks = (d.items + kWaveWaves * ipw - 1) / (kWaveWaves * ipw);
+                p.wave_lds_bytes = off;
+                p.lds_bytes = off;
+            }
+        }
+    }
+
     // streamed gather (training only: it reads the codes from the route
     // records): large batches over a LUT far beyond the L2, rows of whole
     // 64-column chunks, at most 256 rows per table
@@ -818,6 +1098,9 @@ hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, c
     a.codes_pitch = p.codes_pitch;
     a.codes_off = p.codes_off;
     a.red_off = p.red_off;
+    a.wave_lpr_log2 = p.wave_lpr_log2;
+    a.wave_tile_bytes = p.wave_tile_bytes;
+    a.wave_x_off = p.wave_x_off;
     const bool train = rec != nullptr;
     const bool debug = indices != nullptr || margins != nullptr || codes != nullptr;
     if (train && p.stream_ok) {
@@ -831,6 +1114,9 @@ hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, c
         StreamArgs g{lut, a.rec, out, scale, d.items, d.out_f, d.tables, d.rows, p.stream_nblk, p.per_wave};
         return d.lut_dtype == TROPNN_LUT_F16 ? launch_stream<_Float16>(g, p, stream) : launch_stream<float>(g, p, stream);
     }
+    if (p.wave)
+        return d.lut_dtype == TROPNN_LUT_F16 ? launch_wave<_Float16>(a, p, train, debug, stream)
+                                             : launch_wave<float>(a, p, train, debug, stream);
     if (d.lut_dtype == TROPNN_LUT_F16) {
         switch (p.vec) {
             case 8: return launch_typed<_Float16, 8>(a, p, train, debug, stream);

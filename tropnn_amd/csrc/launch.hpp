@@ -37,6 +37,15 @@ struct ForwardPlan {
     int red_off;
     int lds_bytes;
     bool multi;          // large batch: several items per workgroup (blocks = ceil(items / kMultiItems))
+    // wave-item kernel (large batch, 128..1024-byte row tiles): every wave
+    // owns 64 / (tile bytes / 16) items; replaces the multi-item kernel
+    bool wave;
+    int wave_lpr_log2;   // log2 lanes per row tile (tile bytes / 16)
+    int wave_tile_bytes;
+    int wave_tiles;      // grid.y
+    int wave_blocks;     // grid.x
+    int wave_x_off;      // LDS byte offset of the input rows (comparators at 0)
+    int wave_lds_bytes;
     // streamed gather (training, large batch and LUT): a route kernel writes
     // the records, then one workgroup per (item block, 64-column chunk)
     // walks the tables with each table's LUT chunk in LDS
