@@ -711,7 +711,7 @@ def c5_loss_curve(dev, steps: int) -> dict:
         loss_r = F.cross_entropy(h.squeeze(1), y)
         loss_r.backward()
         opt_ref.step()
-        hip_loss.append(float(loss))
+        hip_loss.append(loss.detach().item())
         ref_loss.append(float(loss_r))
         same_codes.append(all(torch.equal(a._last_indices.cpu(), b._last_indices) for a, b in zip(model.layers, ref_layers)))
     first_diff = next((k for k, s in enumerate(same_codes) if not s), None)
