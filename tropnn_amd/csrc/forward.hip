@@ -704,16 +704,18 @@ __global__ __launch_bounds__(kRouteRecThreads) void pairwise_route_records_kerne
 // Streamed gather: one workgroup per (block of 512 items, chunk of 128 bytes
 // of every LUT row: 64 f16 or 32 f32 columns), the workgroups of a chunk
 // adjacent on one XCD. The workgroup walks the tables in order with the
-// tables' LUT chunks (R rows x 128 bytes) in three LDS buffers, filled by
-// LDS-direct loads (global_load_lds_dwordx4: no registers, no LDS write
-// instructions) two tables ahead; the items' codes (from the route records)
-// follow the same pipeline through a register. Thread (slot, piece) owns
-// items 4 slot .. 4 slot + 3 and one 16-byte piece of the chunk: per table
-// four LDS row reads and the adds. The workgroups of one chunk stream the
-// same LUT chunks at about the same time, so the LUT crosses HBM about once
-// instead of once per (item, table) row gather. Tables are summed in blocks
-// of the one-item kernel's tables per wave, and the blocks in order, as that
-// kernel sums its waves: the outputs are bit-identical to it.
+// tables' LUT chunks (R rows x 128 bytes) and the items' codes in four LDS
+// buffers, filled by LDS-direct loads (global_load_lds: no registers, no LDS
+// write instructions) three tables ahead. Thread (slot, piece) owns items
+// 4 slot .. 4 slot + 3 and one 16-byte piece of the chunk: per table four LDS
+// row reads and the adds. The workgroups of one chunk stream the same LUT
+// chunks at about the same time, so the LUT crosses HBM about once instead of
+// once per (item, table) row gather. Tables are summed in blocks of the
+// one-item kernel's tables per wave, and the blocks in order, as that kernel
+// sums its waves: the outputs are bit-identical to it.
+//   The buffers are four distinct LDS arrays and the table loop is unrolled
+// by four, so that the compiler tells them apart: a read of one buffer does
+// not wait for the LDS-direct loads still filling the others.
 struct StreamArgs {
     const void *lut;
     const uint64_t *rec;
@@ -727,9 +729,13 @@ constexpr int kStreamChunkBytes = 128;                       // bytes of a LUT r
 constexpr int kStreamPieces = kStreamChunkBytes / 16;        // 16-byte pieces of a row chunk
 constexpr int kStreamIpt = 4;                                // items per thread
 constexpr int kStreamItems = kStreamThreads / kStreamPieces * kStreamIpt;  // items per workgroup
-constexpr int kStreamBufs = 3;                               // LUT chunks in LDS
-constexpr int kStreamBufBytes = 256 * kStreamChunkBytes;     // one chunk, room for R = 256 rows
-constexpr int kStreamLds = kStreamBufs * (kStreamBufBytes + kStreamItems * 2);
+constexpr int kStreamChunkLds = 256 * kStreamChunkBytes;     // one table's chunk, room for R = 256 rows
+// a buffer: the chunk, then one word per thread: the upper word of item
+// b0 + tid's route record (code | r << 16) for the first kStreamItems
+// threads, a repeat for the others (every thread issues the same loads)
+constexpr int kStreamBufBytes = kStreamChunkLds + kStreamThreads * 4;
+constexpr int kStreamAhead = 3;                              // tables in flight beside the one summed
+constexpr int kStreamLoads = kStreamChunkLds / 16 / kStreamThreads + 1;  // LDS-direct loads per thread per table
 constexpr int kStreamMinItems = 4096;
 constexpr long long kStreamMinLutBytes = 32ll << 20;
 
@@ -738,10 +744,13 @@ __global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel
     constexpr int PE = 16 / static_cast<int>(sizeof(T));  // elements per 16-byte piece
     constexpr int COLS = kStreamChunkBytes / static_cast<int>(sizeof(T));
     constexpr int M = kStreamItems;
-    constexpr int STAGE = kStreamBufBytes / 16 / kStreamThreads;  // LDS-direct loads per thread per table
-    extern __shared__ __align__(16) unsigned char lds[];
+    constexpr int STAGE = kStreamChunkLds / 16 / kStreamThreads;  // chunk loads per thread per table
+    static_assert(kStreamLoads == STAGE + 1 && kStreamAhead == 3, "the wait below counts 2 tables of loads");
+    __shared__ __align__(16) unsigned char sb0[kStreamBufBytes];
+    __shared__ __align__(16) unsigned char sb1[kStreamBufBytes];
+    __shared__ __align__(16) unsigned char sb2[kStreamBufBytes];
+    __shared__ __align__(16) unsigned char sb3[kStreamBufBytes];
     const int R = a.rows;
-    uint16_t *codes = reinterpret_cast<uint16_t *>(lds + kStreamBufs * kStreamBufBytes);  // [bufs][M]
 
     const int unit = xcd_block_unit(blockIdx.x, gridDim.x);
     const int chunk = unit / a.nblk, blk = unit - chunk * a.nblk;
@@ -750,14 +759,18 @@ __global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel
     const int wave = tid >> 6;
     const size_t row_bytes = static_cast<size_t>(a.out_f) * sizeof(T);
     const unsigned char *lut = static_cast<const unsigned char *>(a.lut) + static_cast<size_t>(chunk) * kStreamChunkBytes;
+    // upper word of the record of item b0 + (tid mod M) (past the batch: of
+    // the last item, never read), table 0
+    const uint32_t *rec_hi = reinterpret_cast<const uint32_t *>(a.rec) +
+                             2 * static_cast<size_t>(min(b0 + (tid & (M - 1)), a.items - 1)) + 1;
 
-    // table t's chunk into buffer t % 3: piece q = tid + i * 1024 (row q / 8,
-    // piece q % 8) lands at byte 16 q, i.e. row-major with a 128-byte pitch,
-    // as lane l of a wave writes 16 bytes at the wave's base + 16 l. Rows past
-    // R load row R - 1 (in bounds) into buffer rows no code reads.
-    auto issue_table = [&](int t) {
+    // table t's chunk into `buf`: piece q = tid + i * 1024 (row q / 8, piece
+    // q % 8) lands at byte 16 q, i.e. row-major with a 128-byte pitch, as
+    // lane l of a wave writes 16 bytes at the wave's base + 16 l. Rows past R
+    // load row R - 1 (in bounds) into buffer rows no code reads. Then the
+    // thread's record word.
+    auto issue_table = [&](int t, unsigned char *buf) {
         const unsigned char *base = lut + static_cast<size_t>(t) * R * row_bytes;
-        unsigned char *buf = lds + (t % kStreamBufs) * kStreamBufBytes;
 #pragma unroll
         for (int i = 0; i < STAGE; ++i) {
             const int q = tid + i * kStreamThreads, row = min(q / kStreamPieces, R - 1), pc = q % kStreamPieces;
@@ -765,30 +778,9 @@ __global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel
                                              (__attribute__((address_space(3))) void *)(buf + (i * kStreamThreads + wave * kWave) * 16),
                                              16, 0, 0);
         }
-    };
-    // the items' codes: the raw record of table t + 2 waits in a register
-    // (decoded when stored, an iteration later, so that no wait for it
-    // drains the LDS-direct loads issued after it)
-    uint64_t rec_next = 0;
-    auto load_code = [&](int t) {
-        if (tid < M) {
-            const int b = min(b0 + tid, a.items - 1);  // past the batch: any record, never read
-            rec_next = a.rec[static_cast<size_t>(t) * a.items + b];
-        }
-    };
-    auto store_code = [&](int t) {
-        if (tid < M) codes[(t % kStreamBufs) * M + tid] = static_cast<uint16_t>((rec_next >> 32) & (R - 1));
-    };
-    // all of this wave's loads but the newest `pending` have landed (LDS-direct
-    // ones included), its LDS writes are done, then the workgroup meets: a
-    // plain s_barrier, since __syncthreads()'s fence would wait for every
-    // load, the LDS-direct loads of the next table too
-    auto meet = [&](bool pending) {
-        if (pending)
-            asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)" ::: "memory");
-        else
-            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_global_load_lds(rec_hi + 2 * static_cast<size_t>(t) * a.items,
+                                         (__attribute__((address_space(3))) void *)(buf + kStreamChunkLds + wave * kWave * 4),
+                                         4, 0, 0);
     };
 
     float blk_acc[kStreamIpt][PE], tot[kStreamIpt][PE];
@@ -797,72 +789,74 @@ __global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel
 #pragma unroll
         for (int e = 0; e < PE; ++e) blk_acc[k][e] = tot[k][e] = 0.f;
     int first_block = 1;
+    int next_block_end = min(a.block_tables, a.tables);  // the table count at which the current block ends
 
-    // prologue: table 0 in LDS with its codes; table 1's chunk and record on their way
-    issue_table(0);
-    load_code(0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    store_code(0);
-    if (a.tables > 1) {
-        issue_table(1);
-        load_code(1);
-    }
-    meet(a.tables > 1);  // table 1's three loads may stay in flight
-    for (int t = 0; t < a.tables; ++t) {
-        // iteration t: table t + 1's code stored (its loads, issued an
-        // iteration ago, waited for), table t read, table t + 2's loads
-        // issued, table t summed, and the workgroup meets with table t + 2's
-        // loads in flight
-        if (t + 1 < a.tables) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            store_code(t + 1);
-        }
-        // table t's codes and row pieces are read before table t + 2's loads
-        // are issued: an LDS read after an LDS-direct load waits for it (the
-        // compiler cannot tell the buffers apart), so the loads overlap the
-        // adds and the barrier instead
-        const unsigned char *cur = lds + (t % kStreamBufs) * kStreamBufBytes;
-        const uint16_t *cc = codes + (t % kStreamBufs) * M;
-        const vec_t<uint16_t, 4> cv = *reinterpret_cast<const vec_t<uint16_t, 4> *>(cc + slot * kStreamIpt);
+    // step t: table t has landed in every wave (the loads of the two tables
+    // issued after it may still be in flight: 2 * kStreamLoads), the
+    // workgroup meets, table t's codes and rows are read, table t + 3's loads
+    // are issued into the buffer of table t - 1 (read by every thread before
+    // the meeting), and table t is summed. Past the last table the loads
+    // repeat it, so that every step waits for the same count.
+    auto step = [&](int t, const unsigned char *cur, unsigned char *nxt) {
+        asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        const bool live = t < a.tables;  // workgroup-uniform
         vec_t<uint32_t, 4> w[kStreamIpt];
-#pragma unroll
-        for (int k = 0; k < kStreamIpt; ++k)
-            w[k] = *reinterpret_cast<const vec_t<uint32_t, 4> *>(cur + cv[k] * kStreamChunkBytes + piece * 16);
-        const bool more = t + 2 < a.tables;
-        if (more) {
-            issue_table(t + 2);
-            load_code(t + 2);
-        }
-#pragma unroll
-        for (int k = 0; k < kStreamIpt; ++k) {
-            if constexpr (sizeof(T) == 2) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    blk_acc[k][2 * e] = add_f16_mix<false>(blk_acc[k][2 * e], w[k][e]);
-                    blk_acc[k][2 * e + 1] = add_f16_mix<true>(blk_acc[k][2 * e + 1], w[k][e]);
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    // element to a scalar first: a bit cast of the vector element itself
-                    // reads element 0 for every e
-                    const uint32_t bits = w[k][e];
-                    blk_acc[k][e] += __builtin_bit_cast(float, bits);
-                }
-            }
-        }
-        if ((t + 1) % a.block_tables == 0 || t + 1 == a.tables) {
+        if (live) {
+            const vec_t<uint32_t, 4> cv = *reinterpret_cast<const vec_t<uint32_t, 4> *>(cur + kStreamChunkLds + slot * 16);
 #pragma unroll
             for (int k = 0; k < kStreamIpt; ++k)
-#pragma unroll
-                for (int e = 0; e < PE; ++e) {
-                    tot[k][e] = first_block ? blk_acc[k][e] : tot[k][e] + blk_acc[k][e];
-                    blk_acc[k][e] = 0.f;
-                }
-            first_block = 0;
+                w[k] = *reinterpret_cast<const vec_t<uint32_t, 4> *>(cur + (cv[k] & static_cast<uint32_t>(R - 1)) * kStreamChunkBytes + piece * 16);
         }
-        meet(more);
+        // the reads stay ahead of the next loads
+        __builtin_amdgcn_sched_barrier(0);
+        issue_table(min(t + kStreamAhead, a.tables - 1), nxt);
+        if (live) {
+#pragma unroll
+            for (int k = 0; k < kStreamIpt; ++k) {
+                if constexpr (sizeof(T) == 2) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        blk_acc[k][2 * e] = add_f16_mix<false>(blk_acc[k][2 * e], w[k][e]);
+                        blk_acc[k][2 * e + 1] = add_f16_mix<true>(blk_acc[k][2 * e + 1], w[k][e]);
+                    }
+                } else {
+                    // the whole vector, then its elements: hipcc bit-casts an
+                    // element of an ext_vector_type value as its first element
+                    const vec_t<float, 4> f = __builtin_bit_cast(vec_t<float, 4>, w[k]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) blk_acc[k][e] += f[e];
+                }
+            }
+            if (t + 1 == next_block_end) {
+                // a branch, once per block: without the barrier the compiler
+                // turns the block sum into selects run at every table (three
+                // times the adds' own instructions)
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int k = 0; k < kStreamIpt; ++k)
+#pragma unroll
+                    for (int e = 0; e < PE; ++e) {
+                        tot[k][e] = first_block ? blk_acc[k][e] : tot[k][e] + blk_acc[k][e];
+                        blk_acc[k][e] = 0.f;
+                    }
+                first_block = 0;
+                next_block_end = min(next_block_end + a.block_tables, a.tables);
+            }
+        }
+    };
+
+    issue_table(0, sb0);
+    issue_table(min(1, a.tables - 1), sb1);
+    issue_table(min(2, a.tables - 1), sb2);
+    for (int t0 = 0; t0 < a.tables; t0 += 4) {
+        step(t0, sb0, sb3);
+        step(t0 + 1, sb1, sb0);
+        step(t0 + 2, sb2, sb1);
+        step(t0 + 3, sb3, sb2);
     }
+    // no LDS-direct load may still be writing when the workgroup ends
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     const int col = chunk * COLS + piece * PE;
 #pragma unroll
     for (int k = 0; k < kStreamIpt; ++k) {
@@ -934,11 +928,9 @@ hipError_t launch_typed(const FwdArgs &args, const ForwardPlan &p, bool train, b
 
 template <typename T>
 hipError_t launch_stream(const StreamArgs &args, const ForwardPlan &p, hipStream_t stream) {
-    auto kernel = pairwise_forward_stream_kernel<T>;
-    if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void *>(kernel), p.stream_lds); e != hipSuccess)
-        return e;
-    return launch_kernel(TROPNN_KERNEL_FORWARD, kernel, dim3(p.stream_blocks), dim3(kStreamThreads), p.stream_lds,
-                         stream, args);
+    // the LDS buffers are static (4 x 36 KB)
+    return launch_kernel(TROPNN_KERNEL_FORWARD, pairwise_forward_stream_kernel<T>, dim3(p.stream_blocks),
+                         dim3(kStreamThreads), 0, stream, args);
 }
 
 int ilog2(int v) {
@@ -1062,7 +1054,7 @@ ForwardPlan plan_forward(const Dims &d) {
     if (p.stream_ok) {
         p.stream_nblk = (d.items + kStreamItems - 1) / kStreamItems;
         p.stream_blocks = p.stream_nblk * (d.out_f * esize / kStreamChunkBytes);
-        p.stream_lds = kStreamLds;
+        p.stream_lds = 4 * kStreamBufBytes;  // static
         p.route_block_items = 16;
         while (p.route_block_items > 1 && p.route_block_items * d.in_f * 4 > 64 * 1024) p.route_block_items >>= 1;
         p.route_lds = p.route_block_items * d.in_f * 4;
