@@ -63,17 +63,20 @@ def test_workspace_size(lib):
     # c2, min-margin: the fused path's {gu, r} records [T][B] x 8 bytes
     assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_MIN_MARGIN) == 136 * 512 * 8
     # general path: {gu, r} [T][B] u64 (full STE: gu [T][C][B] f32), then
-    # the sort kernel's slot offsets [T][slots] (slots = B + R (K - 1), K = 8,
-    # rounded up to whole batches), row starts [T][R + 1], batch rows
-    # [T][slots / K], the chunk-major copy of G [chunks][B][P] (P = 64
-    # columns, or the row's width rounded up to the row kernel's lanes) and,
-    # min-margin, the row kernel's partial STE dots [T][chunks][slots] f32
+    # the sort kernel's slot offsets [T][slots] (slots = B + R (K - 1),
+    # rounded up to whole batches of K: K = 4 when the row kernel takes 8
+    # columns per lane, O >= 64 and 8 | O, else 8), row starts [T][R + 1],
+    # batch rows [T][slots / K], the chunk-major copy of G [chunks][B][P]
+    # (P = 64 columns, or the row's width rounded up to the row kernel's
+    # lanes) and, min-margin, the row kernel's partial STE dots
+    # [T][chunks][slots] f32
     def general(b, o, t, r, c, p, full):
         a16 = lambda v: (v + 15) // 16 * 16
-        slots = (b + r * 7 + 7) // 8 * 8
+        k = 4 if o >= 64 and o % 8 == 0 else 8
+        slots = (b + r * (k - 1) + k - 1) // k * k
         chunks = (o + p - 1) // p
         head = a16(a16(a16(t * b * (4 * c if full else 8)) + t * slots * 4) + t * (r + 1) * 4)
-        tail = a16(a16(head + t * (slots // 8) * 4) + chunks * b * p * 4)
+        tail = a16(a16(head + t * (slots // k) * 4) + chunks * b * p * 4)
         return tail if full else a16(tail + t * chunks * slots * 4)
 
     assert ws(64, 1024, 4096, 512, 8, ph.LUT_F16, ph.STE_MIN_MARGIN) == general(64, 4096, 512, 256, 8, 64, False)
@@ -81,6 +84,8 @@ def test_workspace_size(lib):
     assert ws(33, 20, 10, 7, 3, ph.LUT_F32, ph.STE_MIN_MARGIN) == 7 * 33 * 8  # fused, 2 columns per lane
     assert ws(33, 20, 34, 7, 3, ph.LUT_F32, ph.STE_MIN_MARGIN) == general(33, 34, 7, 8, 3, 64, False)
     assert ws(33, 20, 5, 7, 3, ph.LUT_F32, ph.STE_MIN_MARGIN) == general(33, 5, 7, 8, 3, 8, False)
+    # 8 columns per lane below 64 columns: no (batches of 8)
+    assert ws(33, 20, 40, 7, 3, ph.LUT_F32, ph.STE_FULL) == general(33, 40, 7, 8, 3, 64, True)
     assert ws(512, 128, 128, 136, 9, ph.LUT_F32, ph.STE_MIN_MARGIN) == 0
     assert ws(512, 128, 128, 136, 6, ph.LUT_F32, 7) == 0 and "ste_mode" in _err(lib)
 

@@ -76,6 +76,11 @@ namespace {
 constexpr int kSortThreads = 1024;  // items per tile of the sort kernel
 constexpr int kRowsThreads = 1024;  // threads of a row-kernel workgroup
 constexpr int kRowsBatch = 8;       // sorted slots per row-kernel batch; rows are padded to whole batches
+
+// A row-kernel batch: 32 grad-row floats per lane in flight, so 4 slots for
+// 8-column pieces, else kRowsBatch slots. The sort kernel pads rows to whole
+// batches of this size.
+constexpr int rows_batch(int vec) { return vec == 8 ? 4 : kRowsBatch; }
 constexpr int kRowsChunk = 64;     // columns of a row-kernel workgroup (at most): 2 MB of G at c4, within an L2
 constexpr uint32_t kSlotPad = 0x80000000u;  // grad-row offset of a padding slot: past any grad buffer (<= 2 GiB)
 constexpr int kEntries = 16;       // index entries a walker reads per batch
@@ -101,7 +106,7 @@ struct SortArgs {
     const float *gu;      // [T][B] (min-margin) or [T][C][B] (full STE); null: no threshold gradient
     uint32_t *slot_off;   // [T][slots] sorted grad-row byte offsets, kSlotPad in padding; null: no sort
     int32_t *row_start;   // [T][R + 1] first slot of each LUT row; [R] = the padded length
-    int32_t *batch_row;   // [T][slots / kRowsBatch] the LUT row of each batch of slots
+    int32_t *batch_row;   // [T][slots / batch] the LUT row of each batch of slots
     float *grad_thr;      // or null
     const float *grad_out;  // G [B][O]
     float *g_chunked;     // G copied chunk-major: [chunks][B][P] (P = the row kernel's chunk width)
@@ -109,6 +114,7 @@ struct SortArgs {
     int nb_pack;          // slot offsets' low bits: 1: the neighbour row nb = code ^ (1 << r); 0: r
     int items, out_f, comps, rows, slots;
     int chunk_cols, chunk_vec, chunks;  // P, the row kernel's V, ceil(O / P)
+    int batch;                          // rows_batch(V): rows are padded to whole batches
 };
 
 // Row kernel (general path), one workgroup per (table, column chunk).
@@ -127,6 +133,7 @@ struct RowsArgs {
     uint32_t lut_bytes;
     float *pdot;           // [T][chunks][slots] per sorted slot: sum over the chunk's columns of G (L[nb] - L[code]), unscaled
     int items, chunks, lut_off, rs_off;  // LDS byte offsets: LUT chunk (0 with dots), row starts
+    int ring_off;                        // LDS byte offset of the row groups' slot-offset rings
 };
 
 // Reduce kernel (general path, min-margin), one workgroup per table.
@@ -386,7 +393,7 @@ __device__ __forceinline__ int wave_code_rank(int code, bool valid, int R, int C
 // code over tiles of 1024 items (and sums the threshold gradient's partials:
 // -gu at each item's min-margin comparison, or at every comparison with the
 // full STE, a fixed tree per wave, waves in order, tiles in order); the row
-// starts are the counts rounded up to whole batches of kRowsBatch slots,
+// starts are the counts rounded up to whole batches of rows_batch(V) slots,
 // exclusively scanned. Pass 2 places every item at its row's next free slot
 // (tiles, waves and lanes in order, so item order is kept inside a row) as
 // its byte offset b * P * 4 inside a chunk of the copy, with the item's
@@ -394,7 +401,7 @@ __device__ __forceinline__ int wave_code_rank(int code, bool valid, int R, int C
 // slots get kSlotPad.
 __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArgs a) {
     constexpr int kWaves = kSortThreads / kWave;
-    constexpr int K = kRowsBatch;
+    const int K = a.batch;
     extern __shared__ __align__(16) unsigned char lds[];
     const int R = a.rows, C = a.comps;
     int *cnt = reinterpret_cast<int *>(lds);                 // [waves][R] counts -> slots
@@ -504,8 +511,9 @@ __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArg
             if (col >= a.out_f) continue;
             const float *src = a.grad_out + static_cast<size_t>(b) * a.out_f + col;
             float *dst = a.g_chunked + static_cast<size_t>(cb) * a.chunk_cols + piece * a.chunk_vec;
-            if (a.chunk_vec == 4) {
-                *reinterpret_cast<vec_t<float, 4> *>(dst) = *reinterpret_cast<const vec_t<float, 4> *>(src);
+            if (a.chunk_vec % 4 == 0) {
+                for (int e = 0; e < a.chunk_vec; e += 4)
+                    *reinterpret_cast<vec_t<float, 4> *>(dst + e) = *reinterpret_cast<const vec_t<float, 4> *>(src + e);
             } else {
                 for (int e = 0; e < a.chunk_vec; ++e) dst[e] = src[e];
             }
@@ -535,11 +543,11 @@ __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArg
 // pdot[t][chunk][slot] (a batch's dots are contiguous). So the LUT rows of
 // the STE dots are read once per (table, chunk) instead of once per (item,
 // table).
-// The sorted slots form batches of kRowsBatch, each inside one row; the
+// The sorted slots form batches of K = rows_batch(V), each inside one row; the
 // batches are dealt to row groups (S lanes x V columns) as contiguous ranges
 // of lo or lo + 1 batches, the longer ones first. Per batch a group loads its
 // slots' grad-row offsets (one broadcast vector load, prefetched a batch
-// ahead with the batch's row), issues the kRowsBatch grad-row loads (padding
+// ahead with the batch's row), issues the K grad-row loads (padding
 // slots read out of range, zeros) and adds them to the open row's sum in
 // slot order. A row lying wholly in the range is scaled and written there; a
 // row crossing the range's start (end) leaves its sum in the group's slot 0
@@ -548,7 +556,7 @@ __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArg
 template <typename T, int V, int S, bool DOTS, bool NBP>
 __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArgs a) {
     constexpr int NG = kRowsThreads / S;  // row groups
-    constexpr int K = kRowsBatch;
+    constexpr int K = rows_batch(V);
     constexpr int P = S * V;  // columns of the chunk
     constexpr int KR = K <= S ? K : S;  // dots per reduce-scatter
     // a slot offset's low bits below the item offset: nb (NBP, P * 4 >= R) or r
@@ -634,48 +642,67 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
             *reinterpret_cast<vec_t<float, V> *>(part + (g * 2 + (fb < b_begin ? 0 : 1)) * P + j * V) = w;
         }
     };
-    // a batch's slot offsets and row. Past the range: without NBP
-    // out-of-range slots; with NBP the table's last batch (its loads are
-    // masked out by the lane term, its row is not used)
-    auto meta = [&](int bt, uint32_t(&off)[K], int &row) {
-        if (NBP || bt < b_end) {
-            const int bc = NBP ? min(bt, nb_all - 1) : bt;
-            const vec_t<uint32_t, 4> *src = reinterpret_cast<const vec_t<uint32_t, 4> *>(so + static_cast<size_t>(bc) * K);
+    // Slot offsets come through the group's LDS ring of W batches (W * K =
+    // 4 S slots, one 16-byte piece per lane), refilled from a window loaded
+    // W batches ahead: a batch costs its grad-row loads only. Rows are
+    // padded to whole batches, so a batch that starts at or past the open
+    // row's end starts the next non-empty row (the row starts are in LDS);
+    // the range's first row is the sort kernel's batch row.
+    constexpr int W = S * 4 / K;
+    static_assert(W * K == S * 4 && (W & (W - 1)) == 0, "a window is one 16-byte piece per lane");
+    uint32_t *ring = reinterpret_cast<uint32_t *>(lds + a.ring_off) + g * (W * K);
+    const __amdgpu_buffer_rsrc_t so_rsrc = buffer_rsrc(so, static_cast<uint32_t>(a.slots) * 4u);
+    auto window = [&](int w) {  // lane j's piece of window w (past the table's slots: zeros)
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(
+            so_rsrc, static_cast<uint32_t>((b_begin + w * W) * K + 4 * j) * 4u, 0, 0);
+        return __builtin_bit_cast(vec_t<uint32_t, 4>, v);
+    };
+    auto ring_offsets = [&](int wi, uint32_t(&off)[K]) {  // batch wi of the ring's window
 #pragma unroll
-            for (int q = 0; q < K / 4; ++q) {
-                const vec_t<uint32_t, 4> w = src[q];
+        for (int q = 0; q < K / 4; ++q) {
+            const vec_t<uint32_t, 4> w = *reinterpret_cast<const vec_t<uint32_t, 4> *>(ring + wi * K + 4 * q);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) off[4 * q + e] = w[e];
-            }
-            row = br[bc];
-        } else {
-#pragma unroll
-            for (int u = 0; u < K; ++u) off[u] = kSlotPad;
-            row = -1;
+            for (int e = 0; e < 4; ++e) off[4 * q + e] = w[e];
         }
     };
+    vec_t<uint32_t, 4> wnext = window(0);
+    *reinterpret_cast<vec_t<uint32_t, 4> *>(ring + 4 * j) = wnext;
+    wnext = window(1);
+    const int row0 = b_begin < b_end ? br[b_begin] : 0;
+    int cur_end = 0;  // first slot past the open row
     uint32_t offn[K];
-    int rown;
-    meta(b_begin, offn, rown);
+    ring_offsets(0, offn);
     for (int i = 0; __ballot(b_begin + i < b_end) != 0; ++i) {  // wave-uniform trip count
         const int bt = b_begin + i;
-        const int k = rown;
+        const bool live = bt < b_end;
         uint32_t off[K];
 #pragma unroll
         for (int u = 0; u < K; ++u) off[u] = offn[u];
+        // a batch past the range reads zeros (its ring slots belong to
+        // other groups)
         float gv[K][V];
         if constexpr (NBP) {
-            const uint32_t lane_eff = lane_col | (bt < b_end ? 0u : kOutOfRange);
+            const uint32_t lane_eff = lane_col | (live ? 0u : kOutOfRange);
 #pragma unroll
             for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, (off[u] & ~kLow) | lane_eff, chunk_base, gv[u]);
         } else {
+            const uint32_t dead = coldead | (live ? 0u : kOutOfRange);
 #pragma unroll
-            for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, ((off[u] & ~kLow) + gcol) | coldead, 0, gv[u]);
+            for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, ((off[u] & ~kLow) + gcol) | dead, 0, gv[u]);
         }
-        meta(bt + 1, offn, rown);  // the next batch's offsets, while these rows arrive
-        if (bt < b_end && k != cur) {
+        // the next batch's offsets; at a window's end the ring first takes
+        // the next window (one wave's LDS accesses complete in order)
+        if (((i + 1) & (W - 1)) == 0) {
+            *reinterpret_cast<vec_t<uint32_t, 4> *>(ring + 4 * j) = wnext;
+            wnext = window((i + 1) / W + 1);
+        }
+        ring_offsets((i + 1) & (W - 1), offn);
+        if (live && bt * K >= cur_end) {
             if (cur >= 0) finish(cur);
+            int k = cur < 0 ? row0 : cur + 1;
+            while (rs[k + 1] <= bt * K) ++k;  // empty rows
             cur = k;
+            cur_end = rs[k + 1];
 #pragma unroll
             for (int e = 0; e < V; ++e) acc[e] = 0.f;
             if constexpr (DOTS) {
@@ -690,7 +717,7 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
             for (int e = 0; e < V; ++e) acc[e] += gv[u][e];
         if constexpr (DOTS) {
             // a group past its range has cur's row (or row 0) and reads zeros
-            const int kk = bt < b_end ? k : max(cur, 0);
+            const int kk = max(cur, 0);
             // the batch's neighbour rows, all reads issued before the dots
             vec_t<float, V> nv[K];
 #pragma unroll
@@ -1338,6 +1365,7 @@ hipError_t launch_rows_v(const RowsArgs &args, const BackwardPlan &p, int tables
 template <typename T, bool DOTS>
 hipError_t launch_rows_t(const RowsArgs &args, const BackwardPlan &p, int tables, hipStream_t stream) {
     switch (p.rows_vec) {
+        case 8: return launch_rows_v<T, 8, DOTS>(args, p, tables, stream);
         case 4: return launch_rows_v<T, 4, DOTS>(args, p, tables, stream);
         case 2: return launch_rows_v<T, 2, DOTS>(args, p, tables, stream);
         default: return launch_rows_v<T, 1, DOTS>(args, p, tables, stream);
@@ -1432,31 +1460,37 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     BackwardPlan p{};
     p.full = ste_mode == TROPNN_STE_FULL;
     const int esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
-    // row kernel: V columns per lane (a divisor of the row, at most 4), S
-    // lanes per row group: the smallest power of two from 4 whose S * V
-    // columns cover min(O, 64); 64-column chunks keep one chunk of the grad
-    // rows within an XCD's L2 while the tables of the chunk are walked
-    p.rows_vec = 4;
+    // row kernel: V columns per lane (8 for rows of 64 columns or more that
+    // 8 divides, else the largest divisor of the row up to 4), S lanes per
+    // row group: the smallest power of two from 4 whose S * V columns cover
+    // min(O, 64); 64-column chunks keep one chunk of the grad rows within an
+    // XCD's L2 while the tables of the chunk are walked. Eight columns per
+    // lane halve the per-slot addressing and reduce-scatter work per column.
+    p.rows_vec = d.out_f >= kRowsChunk && d.out_f % 8 == 0 ? 8 : 4;
     while (p.rows_vec > 1 && d.out_f % p.rows_vec != 0) p.rows_vec >>= 1;
+    p.rows_batch = rows_batch(p.rows_vec);
     p.rows_slices = 4;
     while (p.rows_slices < 64 && p.rows_slices * p.rows_vec < (d.out_f < kRowsChunk ? d.out_f : kRowsChunk)) p.rows_slices <<= 1;
     const int rows_chunk = p.rows_slices * p.rows_vec;
     p.rows_chunk = rows_chunk;
     p.rows_chunks = (d.out_f + rows_chunk - 1) / rows_chunk;
     p.rows_part_off = ((d.rows + 1) * 4 + 15) & ~15;
-    p.rows_lds_bytes = p.rows_part_off + (kRowsThreads / p.rows_slices) * 2 * rows_chunk * 4;
+    // then the row groups' slot-offset rings, 16 bytes per thread
+    p.rows_ring_off = p.rows_part_off + (kRowsThreads / p.rows_slices) * 2 * rows_chunk * 4;
+    p.rows_lds_bytes = p.rows_ring_off + kRowsThreads * 16;
     // with dots: the LUT chunk [R][P] f32 at offset 0 (its rows' addresses
     // are then byte permutes), then the row starts and the split-row slots
     p.rows_lut_off = 0;
     p.rows_dots_rs_off = d.rows * rows_chunk * 4;
     p.rows_dots_part_off = (p.rows_dots_rs_off + (d.rows + 1) * 4 + 15) & ~15;
-    p.rows_lds_dots_bytes = p.rows_dots_part_off + (kRowsThreads / p.rows_slices) * 2 * rows_chunk * 4;
+    p.rows_dots_ring_off = p.rows_dots_part_off + (kRowsThreads / p.rows_slices) * 2 * rows_chunk * 4;
+    p.rows_lds_dots_bytes = p.rows_dots_ring_off + kRowsThreads * 16;
     // the neighbour row fits below the item offset (a multiple of P * 4 bytes)
     p.rows_nb_pack = rows_chunk * 4 >= d.rows;
     p.sort_lds_bytes = ((kSortThreads / kWave) * d.rows + d.rows + kSortThreads / kWave) * 4 + (kSortThreads / kWave) * 8 * 4;
     // the sorted slots of a table: its items plus up to K - 1 padding slots
     // per row, rounded up to whole batches
-    p.sort_slots = (d.items + d.rows * (kRowsBatch - 1) + kRowsBatch - 1) / kRowsBatch * kRowsBatch;
+    p.sort_slots = (d.items + d.rows * (p.rows_batch - 1) + p.rows_batch - 1) / p.rows_batch * p.rows_batch;
 
     // item kernel: N elements per lane as in the forward (the smallest power
     // of two whose 64-lane tile spans the row, 16 bytes at most, dividing the
@@ -1535,7 +1569,7 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
         p.ws_row_start = off;
         off = align16(off + static_cast<size_t>(d.tables) * (d.rows + 1) * sizeof(int32_t));
         p.ws_batch_row = off;
-        off = align16(off + static_cast<size_t>(d.tables) * (p.sort_slots / kRowsBatch) * sizeof(int32_t));
+        off = align16(off + static_cast<size_t>(d.tables) * (p.sort_slots / p.rows_batch) * sizeof(int32_t));
         p.ws_g_chunked = off;
         off = align16(off + static_cast<size_t>(p.rows_chunks) * d.items * rows_chunk * sizeof(float));
         p.ws_pdot = off;
@@ -1650,6 +1684,7 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
     so.chunk_cols = p.rows_chunk;
     so.chunk_vec = p.rows_vec;
     so.chunks = p.rows_chunks;
+    so.batch = p.rows_batch;
     so.full = p.full ? 1 : 0;
     so.nb_pack = dots && p.rows_nb_pack ? 1 : 0;
     so.items = d.items;
@@ -1675,6 +1710,7 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
     r.tables = d.tables;
     r.slots = p.sort_slots;
     r.part_off = dots ? p.rows_dots_part_off : p.rows_part_off;
+    r.ring_off = dots ? p.rows_dots_ring_off : p.rows_ring_off;
     r.rs_off = dots ? p.rows_dots_rs_off : 0;
     r.lut = lut;
     r.lut_bytes = static_cast<uint32_t>(static_cast<size_t>(d.tables) * d.rows * d.out_f * esize);

@@ -65,14 +65,16 @@ struct ForwardPlan {
 // (threshold gradient too) and the row kernel (LUT gradient).
 struct BackwardPlan {
     // row kernel
-    int rows_vec;       // V: columns per lane (divides the row, at most 4)
+    int rows_vec;       // V: columns per lane (divides the row: 8, 4, 2 or 1)
+    int rows_batch;     // sorted slots per row-kernel batch (rows padded to whole batches)
     int rows_slices;    // S: lanes per row group (4 to 64)
     int rows_chunk;     // P = S * V columns per workgroup
     int rows_chunks;    // column chunks of P
     int rows_part_off;  // LDS byte offset of the split-row slots
+    int rows_ring_off;  // LDS byte offset of the row groups' slot-offset rings
     int rows_lds_bytes;
     int rows_lut_off;   // with partial STE dots: LDS byte offset of the LUT chunk (0)
-    int rows_dots_rs_off, rows_dots_part_off;  // with partial STE dots: row starts, split-row slots
+    int rows_dots_rs_off, rows_dots_part_off, rows_dots_ring_off;  // with partial STE dots: row starts, split-row slots, rings
     int rows_lds_dots_bytes;
     bool rows_nb_pack;       // slot offsets carry the neighbour row (min-margin dots, P * 4 >= R)
     // sort kernel
