@@ -670,14 +670,21 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
     wnext = window(1);
     const int row0 = b_begin < b_end ? br[b_begin] : 0;
     int cur_end = 0;  // first slot past the open row
-    uint32_t offn[K];
-    ring_offsets(0, offn);
-    for (int i = 0; __ballot(b_begin + i < b_end) != 0; ++i) {  // wave-uniform trip count
+    // With dots, batch b's K dots go to its ring slots once its offsets are
+    // read, and each window's 4 S dots (one 128-byte line at c4) are stored
+    // as one 16-byte piece per lane: whole lines instead of a partial line
+    // per batch.
+    auto flush = [&](int w) {  // window w's dots to pdot (live batches only)
+        if ((b_begin + w * W) * K + 4 * j < b_end * K)
+            *reinterpret_cast<vec_t<uint32_t, 4> *>(pd + (b_begin + w * W) * K + 4 * j) =
+                *reinterpret_cast<const vec_t<uint32_t, 4> *>(ring + 4 * j);
+    };
+    uint32_t off[K];
+    ring_offsets(0, off);
+    int i = 0;
+    for (; __ballot(b_begin + i < b_end) != 0; ++i) {  // wave-uniform trip count
         const int bt = b_begin + i;
         const bool live = bt < b_end;
-        uint32_t off[K];
-#pragma unroll
-        for (int u = 0; u < K; ++u) off[u] = offn[u];
         // a batch past the range reads zeros (its ring slots belong to
         // other groups)
         float gv[K][V];
@@ -690,13 +697,6 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
 #pragma unroll
             for (int u = 0; u < K; ++u) buffer_row<float, V>(g_rsrc, ((off[u] & ~kLow) + gcol) | dead, 0, gv[u]);
         }
-        // the next batch's offsets; at a window's end the ring first takes
-        // the next window (one wave's LDS accesses complete in order)
-        if (((i + 1) & (W - 1)) == 0) {
-            *reinterpret_cast<vec_t<uint32_t, 4> *>(ring + 4 * j) = wnext;
-            wnext = window((i + 1) / W + 1);
-        }
-        ring_offsets((i + 1) & (W - 1), offn);
         if (live && bt * K >= cur_end) {
             if (cur >= 0) finish(cur);
             int k = cur < 0 ? row0 : cur + 1;
@@ -750,10 +750,22 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
                 for (int q = 0; q < KR; ++q) dh[q] = d[h * KR + q];
                 const float dot = reduce_scatter<S, KR>(dh, j);
                 const int q = (j / (S / KR)) & (KR - 1);  // the slot whose dot this lane holds
-                if (j % (S / KR) == 0 && bt < b_end) pd[bt * K + h * KR + q] = dot;
+                if (j % (S / KR) == 0 && live)
+                    ring[(i & (W - 1)) * K + h * KR + q] = __builtin_bit_cast(uint32_t, dot);
             }
         }
+        // the next batch's offsets; at a window's end the ring first gives
+        // up its dots, then takes the next window (one wave's LDS accesses
+        // complete in order)
+        if (((i + 1) & (W - 1)) == 0) {
+            if constexpr (DOTS) flush(i / W);
+            *reinterpret_cast<vec_t<uint32_t, 4> *>(ring + 4 * j) = wnext;
+            wnext = window((i + 1) / W + 1);
+        }
+        ring_offsets((i + 1) & (W - 1), off);
     }
+    if constexpr (DOTS)
+        if ((i & (W - 1)) != 0) flush(i / W);  // the last, partial window
     if (cur >= 0) finish(cur);
     __syncthreads();
 
