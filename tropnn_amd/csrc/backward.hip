@@ -545,11 +545,12 @@ __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArg
 // table).
 // The sorted slots form batches of K = rows_batch(V), each inside one row; the
 // batches are dealt to row groups (S lanes x V columns) as contiguous ranges
-// of lo or lo + 1 batches, the longer ones first. Per batch a group loads its
-// slots' grad-row offsets (one broadcast vector load, prefetched a batch
-// ahead with the batch's row), issues the K grad-row loads (padding
-// slots read out of range, zeros) and adds them to the open row's sum in
-// slot order. A row lying wholly in the range is scaled and written there; a
+// of lo or lo + 1 batches, the longer ones first. Per batch a group reads its
+// slots' grad-row offsets from its LDS ring (refilled a window of batches
+// at a time), issues the K grad-row loads (padding slots read out of range,
+// zeros) and adds them to the open row's sum in slot order; the batch's
+// dots go back into the ring and leave a window at a time. A row lying
+// wholly in the range is scaled and written there; a
 // row crossing the range's start (end) leaves its sum in the group's slot 0
 // (1), and a combine step adds the pieces in range order and writes the
 // row. Empty rows are written as zeros, so grad_lut is fully overwritten.
