@@ -65,6 +65,7 @@
 //  A third, tiny kernel builds the inverse anchor index; callers rebuild it
 //  only when the anchors change.
 #include <mutex>
+#include <type_traits>
 #include <unordered_map>
 
 #include "device.hpp"
@@ -74,13 +75,19 @@ namespace tropnn {
 namespace {
 
 constexpr int kSortThreads = 1024;  // items per tile of the sort kernel
-constexpr int kRowsThreads = 1024;  // threads of a row-kernel workgroup
+constexpr int kRowsThreads = 1024;  // threads of a row-kernel workgroup (but see rows_threads)
 constexpr int kRowsBatch = 8;       // sorted slots per row-kernel batch; rows are padded to whole batches
 
 // A row-kernel batch: 32 grad-row floats per lane in flight, so 4 slots for
 // 8-column pieces, else kRowsBatch slots. The sort kernel pads rows to whole
 // batches of this size.
 constexpr int rows_batch(int vec) { return vec == 8 ? 4 : kRowsBatch; }
+
+// Threads of a row-kernel workgroup. With partial dots over an f16 LUT the
+// LUT chunk stays f16 in LDS (32 KB at 64 columns), so that a 512-thread
+// workgroup needs under 80 KB and two share a CU: one's staging and combine
+// overlap the other's walk. Otherwise 1024.
+constexpr int rows_threads(bool dots, int lut_esize) { return dots && lut_esize == 2 ? 512 : kRowsThreads; }
 constexpr int kRowsChunk = 64;     // columns of a row-kernel workgroup (at most): 2 MB of G at c4, within an L2
 constexpr uint32_t kSlotPad = 0x80000000u;  // grad-row offset of a padding slot: past any grad buffer (<= 2 GiB)
 constexpr int kEntries = 16;       // index entries a walker reads per batch
@@ -555,22 +562,26 @@ __global__ __launch_bounds__(kSortThreads) void pairwise_bwd_sort_kernel(SortArg
 // (1), and a combine step adds the pieces in range order and writes the
 // row. Empty rows are written as zeros, so grad_lut is fully overwritten.
 template <typename T, int V, int S, bool DOTS, bool NBP>
-__global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArgs a) {
-    constexpr int NG = kRowsThreads / S;  // row groups
+__global__ __launch_bounds__(rows_threads(DOTS, sizeof(T))) void pairwise_bwd_rows_kernel(RowsArgs a) {
+    constexpr int NT = rows_threads(DOTS, sizeof(T));
+    constexpr int NG = NT / S;  // row groups
     constexpr int K = rows_batch(V);
     constexpr int P = S * V;  // columns of the chunk
     constexpr int KR = K <= S ? K : S;  // dots per reduce-scatter
     // a slot offset's low bits below the item offset: nb (NBP, P * 4 >= R) or r
     constexpr uint32_t kLow = NBP ? static_cast<uint32_t>(P * 4 - 1) : 7u;
     static_assert(!NBP || DOTS, "nb in the slot offsets serves the STE dots");
+    // DOTS: the table's LUT chunk [R][P] in LDS, f32, or f16 for an f16 LUT
+    // (the 512-thread workgroups of rows_threads)
+    using LT = std::conditional_t<NT == kRowsThreads, float, _Float16>;
     // the neighbour row's LDS address from one byte permute: the LUT chunk at
     // LDS offset 0 with 256-byte rows, nb (< 256) in the slot offset's low
     // byte, the lane's column offset (< 256) in the address's low byte
-    constexpr bool kNbPerm = NBP && P * 4 == 256;
+    constexpr bool kNbPerm = NBP && P * sizeof(LT) == 256;
     extern __shared__ __align__(16) unsigned char lds[];
     int *rs = reinterpret_cast<int *>(lds + a.rs_off);            // [R + 1] row starts (slots)
     float *part = reinterpret_cast<float *>(lds + a.part_off);    // [groups][2][P] split rows
-    float *lut_s = reinterpret_cast<float *>(lds + a.lut_off);    // DOTS: [R][P] the table's LUT chunk
+    LT *lut_s = reinterpret_cast<LT *>(lds + a.lut_off);
     // unit = chunk * T + table, each XCD taking one contiguous block of units:
     // an XCD walks its chunks one at a time over every table, so the chunk's
     // slice of G is read into its L2 once
@@ -591,28 +602,28 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
     const uint32_t coldead = col_ok ? 0u : kOutOfRange;
     const uint32_t lane_col = static_cast<uint32_t>(j * V) * 4u | coldead;
     const int chunk_base = static_cast<int>(static_cast<uint32_t>(chunk) * a.chunk_bytes);
-    const uint32_t lane_lds = static_cast<uint32_t>(j * V) * 4u;
+    const uint32_t lane_lds = static_cast<uint32_t>(j * V) * static_cast<uint32_t>(sizeof(LT));
     const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.g_chunked, a.gc_bytes);
     const uint32_t *so = a.slot_off + static_cast<size_t>(t) * a.slots;
     const int32_t *br = a.batch_row + static_cast<size_t>(t) * (a.slots / K);
     float *gl = a.grad_lut != nullptr ? a.grad_lut + static_cast<size_t>(t) * R * O : nullptr;
-    for (int k = tid; k <= R; k += kRowsThreads) rs[k] = a.row_start[static_cast<size_t>(t) * (R + 1) + k];
+    for (int k = tid; k <= R; k += NT) rs[k] = a.row_start[static_cast<size_t>(t) * (R + 1) + k];
     if constexpr (DOTS) {
         // the LUT chunk: R rows of P columns (pieces of V, columns past O zero)
         const __amdgpu_buffer_rsrc_t lut_rsrc = buffer_rsrc(a.lut, a.lut_bytes);
-        for (int q = tid; q < R * S; q += kRowsThreads) {
+        for (int q = tid; q < R * S; q += NT) {
             const int row = q / S, pc = q - row * S, c0 = chunk * P + pc * V;
             float w[V];
             buffer_row<T, V>(lut_rsrc,
                              c0 < O ? static_cast<uint32_t>((static_cast<size_t>(t) * R + row) * O + c0) * sizeof(T)
                                     : kOutOfRange,
                              0, w);
-            vec_t<float, V> wv;
+            vec_t<LT, V> wv;
 #pragma unroll
-            for (int e = 0; e < V; ++e) wv[e] = w[e];
-            // whole-vector LDS accesses: element by element the lanes' 4-byte
-            // accesses stride by V * 4 bytes and collide in the banks
-            *reinterpret_cast<vec_t<float, V> *>(lut_s + row * P + pc * V) = wv;
+            for (int e = 0; e < V; ++e) wv[e] = static_cast<LT>(w[e]);  // exact: w came from T
+            // whole-vector LDS accesses: element by element the lanes'
+            // accesses stride by V elements and collide in the banks
+            *reinterpret_cast<vec_t<LT, V> *>(lut_s + row * P + pc * V) = wv;
         }
     }
     __syncthreads();
@@ -707,9 +718,9 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
 #pragma unroll
             for (int e = 0; e < V; ++e) acc[e] = 0.f;
             if constexpr (DOTS) {
-                const vec_t<float, V> lv = *reinterpret_cast<const vec_t<float, V> *>(lut_s + k * P + j * V);
+                const vec_t<LT, V> lv = *reinterpret_cast<const vec_t<LT, V> *>(lut_s + k * P + j * V);
 #pragma unroll
-                for (int e = 0; e < V; ++e) lkv[e] = lv[e];
+                for (int e = 0; e < V; ++e) lkv[e] = static_cast<float>(lv[e]);
             }
         }
 #pragma unroll
@@ -720,7 +731,7 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
             // a group past its range has cur's row (or row 0) and reads zeros
             const int kk = max(cur, 0);
             // the batch's neighbour rows, all reads issued before the dots
-            vec_t<float, V> nv[K];
+            vec_t<LT, V> nv[K];
 #pragma unroll
             for (int u = 0; u < K; ++u) {
                 if constexpr (kNbPerm) {
@@ -729,19 +740,30 @@ __global__ __launch_bounds__(kRowsThreads) void pairwise_bwd_rows_kernel(RowsArg
                     // first, 0x0c gives zero); the LUT chunk starts at LDS
                     // address 0, so this is the LDS address itself
                     const uint32_t addr = __builtin_amdgcn_perm(off[u], lane_lds, 0x0c0c0400u);
-                    nv[u] = *reinterpret_cast<const __attribute__((address_space(3))) vec_t<float, V> *>(addr);
+                    nv[u] = *reinterpret_cast<const __attribute__((address_space(3))) vec_t<LT, V> *>(addr);
                 } else {
                     // NBP: the sort kernel left nb in the offset's low bits (< R)
                     const int nb = NBP ? static_cast<int>(off[u] & kLow) : (kk ^ (1 << (off[u] & 7u))) & (R - 1);
-                    nv[u] = *reinterpret_cast<const vec_t<float, V> *>(lut_s + nb * P + j * V);
+                    nv[u] = *reinterpret_cast<const vec_t<LT, V> *>(lut_s + nb * P + j * V);
                 }
             }
+            // L[nb] - L[code] in f32: from f16, one mixed-precision fma
+            // (v_fma_mix_f32) of the widened element (exact) with 1 and
+            // -L[code], rounded once like the f32 subtraction; the 1 is
+            // opaque, or the compiler folds the fma into a conversion and a
+            // subtraction
+            float one = 1.0f;
+            if constexpr (sizeof(LT) == 2) __asm__("" : "+v"(one));
             float d[K];
 #pragma unroll
             for (int u = 0; u < K; ++u) {
                 float sd = 0.f;
 #pragma unroll
-                for (int e = 0; e < V; ++e) sd += gv[u][e] * (nv[u][e] - lkv[e]);
+                for (int e = 0; e < V; ++e) {
+                    const float diff = sizeof(LT) == 2 ? __builtin_fmaf(static_cast<float>(nv[u][e]), one, -lkv[e])
+                                                       : static_cast<float>(nv[u][e]) - lkv[e];
+                    sd += gv[u][e] * diff;
+                }
                 d[u] = sd;
             }
 #pragma unroll
@@ -1359,8 +1381,10 @@ hipError_t launch_rows_vs(const RowsArgs &args, const BackwardPlan &p, int table
     auto kernel = DOTS && p.rows_nb_pack ? pairwise_bwd_rows_kernel<T, V, S, DOTS, DOTS>
                                          : pairwise_bwd_rows_kernel<T, V, S, DOTS, false>;
     const int lds = DOTS ? p.rows_lds_dots_bytes : p.rows_lds_bytes;
+    constexpr int threads = rows_threads(DOTS, sizeof(T));
+    if (threads != (DOTS ? p.rows_dots_threads : kRowsThreads)) return hipErrorInvalidConfiguration;  // plan mismatch
     if (hipError_t e = allow_lds(kernel, lds); e != hipSuccess) return e;
-    return launch_kernel(TROPNN_KERNEL_BACKWARD_TABLE, kernel, dim3(tables * p.rows_chunks), dim3(kRowsThreads), lds,
+    return launch_kernel(TROPNN_KERNEL_BACKWARD_TABLE, kernel, dim3(tables * p.rows_chunks), dim3(threads), lds,
                          stream, args);
 }
 
@@ -1494,10 +1518,13 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     // with dots: the LUT chunk [R][P] f32 at offset 0 (its rows' addresses
     // are then byte permutes), then the row starts and the split-row slots
     p.rows_lut_off = 0;
-    p.rows_dots_rs_off = d.rows * rows_chunk * 4;
+    // (in the LUT's element type for an f16 LUT, with rows_threads' 512-thread
+    // workgroups)
+    p.rows_dots_threads = rows_threads(true, esize);
+    p.rows_dots_rs_off = (d.rows * rows_chunk * esize + 15) & ~15;
     p.rows_dots_part_off = (p.rows_dots_rs_off + (d.rows + 1) * 4 + 15) & ~15;
-    p.rows_dots_ring_off = p.rows_dots_part_off + (kRowsThreads / p.rows_slices) * 2 * rows_chunk * 4;
-    p.rows_lds_dots_bytes = p.rows_dots_ring_off + kRowsThreads * 16;
+    p.rows_dots_ring_off = p.rows_dots_part_off + (p.rows_dots_threads / p.rows_slices) * 2 * rows_chunk * 4;
+    p.rows_lds_dots_bytes = p.rows_dots_ring_off + p.rows_dots_threads * 16;
     // the neighbour row fits below the item offset (a multiple of P * 4 bytes)
     p.rows_nb_pack = rows_chunk * 4 >= d.rows;
     p.sort_lds_bytes = ((kSortThreads / kWave) * d.rows + d.rows + kSortThreads / kWave) * 4 + (kSortThreads / kWave) * 8 * 4;

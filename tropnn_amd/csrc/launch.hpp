@@ -76,6 +76,7 @@ struct BackwardPlan {
     int rows_lut_off;   // with partial STE dots: LDS byte offset of the LUT chunk (0)
     int rows_dots_rs_off, rows_dots_part_off, rows_dots_ring_off;  // with partial STE dots: row starts, split-row slots, rings
     int rows_lds_dots_bytes;
+    int rows_dots_threads;  // threads of the row kernel's workgroup with dots (512 for an f16 LUT, else 1024)
     bool rows_nb_pack;       // slot offsets carry the neighbour row (min-margin dots, P * 4 >= R)
     // sort kernel
     int sort_lds_bytes;
