@@ -276,6 +276,11 @@ def test_train_parity(i, o, t, c, b, thr_std):
         (64, 300, 20, 8, 2100, True, "izhikevich", "f32"),  # general path, 5 chunks, 3 sort tiles
         (40, 3, 50, 3, 500, True, "izhikevich", "f32"),  # general path, 4-lane row groups
         (40, 6, 50, 3, 500, True, "izhikevich", "f32"),  # fused path, 2 columns per lane
+        # general path, rows of whole 64-column chunks: 8 columns per lane in
+        # 4-slot batches; f16: the LUT chunk as f16 in LDS in
+        # 512-thread workgroups; f32: neighbour rows by byte permute
+        (48, 320, 20, 6, 700, True, "izhikevich", "f16"),
+        (48, 320, 20, 6, 700, True, "fast_sigmoid_odd", "f32"),
     ],
 )
 def test_train_parity_ste_variants(i, o, t, c, b, min_margin, surrogate, lut_dtype):
