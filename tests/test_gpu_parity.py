@@ -365,6 +365,38 @@ def test_f16_lut_training():
     assert_train_parity(ref, hip, *train_step(ref, hip, x, g), tol=F16_TOL)
 
 
+@pytest.mark.parametrize(
+    "i,o,t,c,b,mode",
+    [
+        (128, 128, 136, 6, 512, "train"),  # fused path (the c2 layer)
+        (48, 320, 20, 6, 700, "train"),  # general path, 8 columns per lane, the LUT chunk f16 in LDS
+        (100, 1000, 12, 7, 300, "train"),  # general path, a partial last column chunk
+        (128, 128, 136, 6, 4100, "eval"),  # wave-item forward
+        (256, 512, 16, 6, 8, "eval"),  # one-item forward (the c1 layer)
+    ],
+)
+def test_f16_reads_match_the_oracle_on_the_f16_lut(i, o, t, c, b, mode):
+    """The f16-LUT paths widen each f16 element exactly and compute in f32, so
+    against the oracle run on the same RNE f16 copy of the LUT they agree to
+    the f32 tolerance (against the f32 oracle only to the LUT's own rounding,
+    F16_TOL): a kernel error of a few 1e-4 would pass the F16_TOL tests but
+    not this one."""
+    ref, hip = make_pair(i, o, t, c, seed=i + o, thr_std=0.3, lut_dtype="f16")
+    with torch.no_grad():
+        ref.lut.copy_(ref.lut.half().float())  # the values the kernels read
+    x = seeded((b, i), seed=b + 3)
+    if mode == "train":
+        g = seeded((b, 1, o), seed=b + 4)
+        assert_train_parity(ref, hip, *train_step(ref, hip, x, g), tol=F32_TOL)
+    else:
+        hip.eval()
+        with torch.no_grad():
+            y = hip(x.to(DEV))
+            y_ref = ref.eval()(x)
+        assert torch.equal(hip._last_indices.cpu().reshape(b, t), ref._last_indices.reshape(b, t))
+        assert rel_err(y, y_ref) <= F32_TOL
+
+
 def test_f16_cache_follows_lut_updates():
     _, hip = make_pair(16, 8, 4, 3, seed=0, lut_dtype="f16")
     first = hip._lut_for_reading()
