@@ -1,0 +1,62 @@
+"""Seeded random shapes over every forward kernel (one-item, multi-item,
+wave-item) and both backward paths (fused, general; min-margin and full STE,
+both surrogates), f32 and f16 LUTs, against the CPU oracle: route codes
+exact, outputs and every gradient within the f32 tolerance (f16 LUT reads
+against the oracle run on the same RNE f16 copy of the LUT). A regression
+guard beside the hand-picked cases of test_gpu_parity."""
+from __future__ import annotations
+
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import routing_np
+from test_gpu_parity import DEV, F32_TOL, assert_train_parity, make_pair, rel_err, seeded, train_step
+
+pytestmark = pytest.mark.gpu
+
+
+def _cases(seed: int, n: int):
+    rng = random.Random(seed)
+    out = []
+    while len(out) < n:
+        kind = rng.choice(["eval", "train", "train"])
+        c = rng.choice([1, 2, 3, 4, 5, 6, 7, 8])
+        t = rng.choice([1, 3, 9, 17, 40, 136])
+        i = rng.choice([4, 16, 33, 64, 128, 300])
+        o = rng.choice([2, 6, 10, 32, 64, 96, 128, 136, 256, 320, 512, 1000])
+        b = rng.choice([1, 7, 64, 513, 2100, 4100] if kind == "eval" else [1, 5, 33, 512, 1100, 2100])
+        if t * (2**c) * o * 4 > (256 << 20) or b * t * o > 60_000_000:
+            continue  # keep the CPU oracle within seconds
+        out.append(
+            (kind, i, o, t, c, b, rng.choice(["f32", "f16"]), rng.random() < 0.7,
+             rng.choice(["fast_sigmoid_odd", "izhikevich"]), rng.choice([0.0, 0.3]))
+        )
+    return out
+
+
+@pytest.mark.parametrize("case", _cases(2024, 36), ids=lambda c: "-".join(str(v) for v in c))
+def test_random_shape(case):
+    kind, i, o, t, c, b, lut_dtype, min_margin, surrogate, thr = case
+    ref, hip = make_pair(
+        i, o, t, c, seed=i + o + t, thr_std=thr, lut_dtype=lut_dtype, use_min_margin_ste=min_margin,
+        surrogate=surrogate,
+    )
+    if lut_dtype == "f16":
+        with torch.no_grad():
+            ref.lut.copy_(ref.lut.half().float())  # the values the kernels read
+    x = seeded((b, i), seed=b + c)
+    if kind == "train":
+        g = seeded((b, 1, o), seed=b + c + 1)
+        assert_train_parity(ref, hip, *train_step(ref, hip, x, g), tol=F32_TOL)
+        return
+    hip.eval()
+    with torch.no_grad():
+        y = hip(x.to(DEV))
+        idx = hip._last_indices
+        y_ref = ref.eval()(x)
+    codes = routing_np.route_codes(x.numpy(), ref.anchors.numpy(), ref.thresholds.detach().numpy())
+    np.testing.assert_array_equal(idx.cpu().reshape(b, t).numpy(), codes)
+    assert rel_err(y, y_ref) <= F32_TOL
