@@ -688,8 +688,8 @@ __global__ __launch_bounds__(rows_threads(DOTS, sizeof(T))) void pairwise_bwd_ro
     // per batch.
     auto flush = [&](int w) {  // window w's dots to pdot (live batches only)
         if ((b_begin + w * W) * K + 4 * j < b_end * K)
-            *reinterpret_cast<vec_t<uint32_t, 4> *>(pd + (b_begin + w * W) * K + 4 * j) =
-                *reinterpret_cast<const vec_t<uint32_t, 4> *>(ring + 4 * j);
+            __builtin_nontemporal_store(*reinterpret_cast<const vec_t<uint32_t, 4> *>(ring + 4 * j),
+                                        reinterpret_cast<vec_t<uint32_t, 4> *>(pd + (b_begin + w * W) * K + 4 * j));
     };
     uint32_t off[K];
     ring_offsets(0, off);
