@@ -5,7 +5,8 @@ Bars:
   * route codes and margins: bit-exact (torch.equal on int64 codes and on the
     f32 margin bit patterns);
   * f32 LUT: forward output and every gradient within 1e-5 relative error,
-    measured norm-wise as max|hip - oracle| / max|oracle|;
+    measured norm-wise as max|hip - oracle| / max|oracle|, and in training
+    also element by element within 2e-4 of |oracle| + 1e-3 max|oracle|;
   * f16 LUT reads: within 1e-3 relative of the f32-LUT oracle.
 The reference's own parity tests (test_backend_parity.py:348-369) use
 allclose(atol=1e-6); test_reference_case repeats that case and bar.
@@ -32,6 +33,22 @@ def _need_gpu():
         pytest.skip("needs a GPU")
     yield
     torch.cuda.synchronize()
+
+
+ELEM_RTOL = 2e-4
+ELEM_FLOOR = 1e-3
+
+
+def elem_err(a: torch.Tensor, b: torch.Tensor) -> float:
+    """max over elements of |a - b| / (|b| + ELEM_FLOOR max|b|), in float64."""
+    a = a.detach().double().cpu()
+    b = b.detach().double().cpu()
+    if b.numel() == 0:
+        return 0.0
+    scale = b.abs().max()
+    if scale == 0:
+        return (a - b).abs().max().item()
+    return ((a - b).abs() / (b.abs() + ELEM_FLOOR * scale)).max().item()
 
 
 def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
@@ -89,6 +106,18 @@ def assert_train_parity(ref, hip, yx_ref, yx_hip, tol=F32_TOL, x_grad=True):
         assert x_hip.grad is None and x_ref.grad is None
     bad = {k: v for k, v in errs.items() if not v <= tol}
     assert not bad, f"beyond {tol}: {bad} (all: {errs})"
+    if tol == F32_TOL:
+        # and element by element: |hip - ref| <= ELEM_RTOL (|ref| + ELEM_FLOOR
+        # max|ref|). Far stricter than the norm-wise bar on small elements;
+        # the floor covers sums that cancel, where any change of summation
+        # order in f32 moves the result (seen: 9.4e-5 at most)
+        pairs = {"output": (y_hip, y_ref), "grad_thresholds": (hip.thresholds.grad, ref.thresholds.grad),
+                 "grad_lut": (hip.lut.grad, ref.lut.grad)}
+        if x_grad:
+            pairs["grad_x"] = (x_hip.grad, x_ref.grad)
+        elem = {k: elem_err(h, r) for k, (h, r) in pairs.items()}
+        bad = {k: v for k, v in elem.items() if not v <= ELEM_RTOL}
+        assert not bad, f"element-wise beyond {ELEM_RTOL}: {bad} (all: {elem})"
     return errs
 
 
