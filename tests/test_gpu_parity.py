@@ -310,6 +310,7 @@ def test_train_parity(i, o, t, c, b, thr_std):
         # 512-thread workgroups; f32: neighbour rows by byte permute
         (48, 320, 20, 6, 700, True, "izhikevich", "f16"),
         (48, 320, 20, 6, 700, True, "fast_sigmoid_odd", "f32"),
+        (32, 320, 4, 6, 6000, True, "izhikevich", "f32"),  # ~12 batches of 4 slots per row group: two slot-offset windows, the second partial
     ],
 )
 def test_train_parity_ste_variants(i, o, t, c, b, min_margin, surrogate, lut_dtype):
@@ -400,6 +401,7 @@ def test_f16_lut_training():
         (128, 128, 136, 6, 512, "train"),  # fused path (the c2 layer)
         (48, 320, 20, 6, 700, "train"),  # general path, 8 columns per lane, the LUT chunk f16 in LDS
         (100, 1000, 12, 7, 300, "train"),  # general path, a partial last column chunk
+        (32, 320, 4, 6, 6000, "train"),  # general path, f16: ~24 batches per row group, three slot-offset windows
         (128, 128, 136, 6, 4100, "eval"),  # wave-item forward
         (256, 512, 16, 6, 8, "eval"),  # one-item forward (the c1 layer)
     ],
