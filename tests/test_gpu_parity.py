@@ -325,6 +325,49 @@ def test_train_parity_ste_variants(i, o, t, c, b, min_margin, surrogate, lut_dty
     assert_train_parity(ref, hip, *train_step(ref, hip, x, g), tol=tol)
 
 
+@pytest.mark.parametrize("i,o,t,c,b", [(128, 128, 136, 6, 64), (48, 320, 20, 6, 300)])
+@pytest.mark.parametrize("case", ["transposed_x_sum", "strided_grad", "sliced_3d_x"])
+def test_noncontiguous_inputs_and_grads(i, o, t, c, b, case):
+    """Views as inputs and upstream gradients (fused and general backward):
+    a transposed x with y.sum().backward() (the upstream gradient is an
+    expanded ones tensor with zero strides), a step-2 slice as the upstream
+    gradient, and a [B, S, I] slice with S = 2. Codes bit-exact, output and
+    gradients at the f32 bars, against the oracle fed the same views."""
+    ref, hip = make_pair(i, o, t, c, seed=7, thr_std=0.3)
+
+    def run(mod, dev):
+        mod.train()
+        if case == "transposed_x_sum":
+            leaf = seeded((i, b), seed=5).to(dev).requires_grad_(True)
+            x = leaf.t()
+            y = mod(x)
+            y.sum().backward()
+        elif case == "strided_grad":
+            leaf = seeded((b, i), seed=5).to(dev).requires_grad_(True)
+            x = leaf
+            y = mod(x)
+            g = seeded((b, 1, 2 * o), seed=6).to(dev)[..., ::2]
+            y.backward(g)
+        else:
+            leaf = seeded((b, 4, i), seed=5).to(dev).requires_grad_(True)
+            x = leaf[:, ::2, :]
+            y = mod(x)
+            y.backward(seeded(tuple(y.shape), seed=6).to(dev))
+        assert not x.is_contiguous() or case == "strided_grad"
+        return y, leaf
+
+    y_ref, leaf_ref = run(ref, torch.device("cpu"))
+    y_hip, leaf_hip = run(hip, DEV)
+    torch.cuda.synchronize()
+    assert y_hip.shape == y_ref.shape
+    assert torch.equal(hip._last_indices.cpu(), ref._last_indices), "route codes differ"
+    pairs = {"output": (y_hip, y_ref), "grad_x": (leaf_hip.grad, leaf_ref.grad),
+             "grad_thresholds": (hip.thresholds.grad, ref.thresholds.grad), "grad_lut": (hip.lut.grad, ref.lut.grad)}
+    errs = {k: (rel_err(h, r), elem_err(h, r)) for k, (h, r) in pairs.items()}
+    bad = {k: v for k, v in errs.items() if not (v[0] <= F32_TOL and v[1] <= ELEM_RTOL)}
+    assert not bad, f"beyond the f32 bars: {bad} (all: {errs})"
+
+
 def test_full_ste_without_route_debug():
     """With the route debug cache off the forward still keeps the margins the
     full STE needs."""
