@@ -230,20 +230,30 @@ __device__ __forceinline__ int index_word(const int32_t *offs, const int32_t *en
     return k <= in_f ? offs[k] : (k - in_f - 1 < n_ent ? ents[k - in_f - 1] : 0);
 }
 
-// grad_x row of one item: thread f sums the item's signed gu slots gud[(t * C
-// + c)] named by feature f's entries of the inverse anchor index (staged in
-// LDS as index_word lays it out), in entry order; side 1 subtracts. A batch
+// grad_x row of one item: the item's signed gu slots gud[(t * C + c)] named
+// by feature f's entries of the inverse anchor index (staged in LDS as
+// index_word lays it out), summed in entry order; side 1 subtracts. A batch
 // reads its kEntries entries and slots unconditionally (entries past the
 // feature's last belong to later features or are the zero padding, so every
 // slot index is in range) and drops the extra ones with a select: straight-
 // line code instead of a branch around every load.
+// When all the features fit half the threads, two adjacent lanes walk a
+// feature: lane h of the pair takes the entry batches h, h + 2, ... and the
+// feature's value is (lane 0's sum) + (lane 1's sum), so a feature of up to
+// 2 kEntries entries takes one batch per lane (c2: 128 features of ~13
+// entries, one in six above kEntries, on 256 threads). Otherwise one lane
+// walks a feature's batches in order. nthr is even.
 __device__ __forceinline__ void feature_walk(const float *gud, const int *idx_s, int in_f, float *grad_x_row, int tid,
                                              int nthr) {
     const int *off_s = idx_s, *ent_s = idx_s + in_f + 1;
-    for (int f = tid; f < in_f; f += nthr) {
+    const bool pair = in_f * 2 <= nthr;  // uniform
+    const int h = pair ? tid & 1 : 0;
+    const int fstep = pair ? nthr >> 1 : nthr, estep = pair ? 2 * kEntries : kEntries;
+    // both lanes of a pair see the same f, so they leave the loop together
+    for (int f = pair ? tid >> 1 : tid; f < in_f; f += fstep) {
         const int f0 = off_s[f], f1 = off_s[f + 1];
         float gx = 0.f;
-        for (int eb = f0; eb < f1; eb += kEntries) {
+        for (int eb = f0 + h * kEntries; eb < f1; eb += estep) {
             int en[kEntries];
 #pragma unroll
             for (int q = 0; q < kEntries; ++q) en[q] = ent_s[eb + q];
@@ -256,7 +266,14 @@ __device__ __forceinline__ void feature_walk(const float *gud, const int *idx_s,
                 gx = eb + q < f1 ? gx + sv : gx;
             }
         }
-        __builtin_nontemporal_store(gx, grad_x_row + f);
+        if (pair) {
+            // the partner lane's sum (DPP quad_perm [1,0,3,2]: lane ^ 1)
+            const float other = __builtin_bit_cast(
+                float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, gx), 0xB1, 0xF, 0xF, false));
+            if (h == 0) __builtin_nontemporal_store(gx + other, grad_x_row + f);
+        } else {
+            __builtin_nontemporal_store(gx, grad_x_row + f);
+        }
     }
 }
 
