@@ -644,7 +644,9 @@ def test_c4_large_layer_properties():
         (an item placed in the wrong row of a later sort tile, or a wrong
         sign or comparison in the threshold gradient, fails these);
       * forward and input gradient of a row depend on that row only: a random
-        subset of rows is compared with the oracle run on those rows alone;
+        subset of rows is compared with the oracle run on those rows alone
+        (at the f16 bar with the f32 LUT, and at the f32 bars with the LUT
+        rounded to f16 as the kernels read it);
       * every item adds its scaled grad row to exactly one row per table, so
         sum_r grad_lut[t, r, :] = s * sum_b G[b, :] for every table t;
       * gradients are linear in G: grad(G1 + G2) = grad(G1) + grad(G2).
@@ -695,6 +697,16 @@ def test_c4_large_layer_properties():
     y_sub.backward(gfull[sub.to(DEV)].cpu())
     assert rel_err(y[sub.to(DEV)], y_sub) <= F16_TOL
     assert rel_err(gx[sub.to(DEV)], x_sub.grad) <= F16_TOL
+    # and at the f32 bar (norm-wise and element-wise) against the oracle
+    # reading the same f16-rounded LUT: what is left is summation order
+    with torch.no_grad():
+        ref.lut.copy_(ref.lut.half().float())
+    ref.zero_grad(set_to_none=True)
+    x_sub = x[sub.to(DEV)].cpu().requires_grad_(True)
+    y_sub = ref.train()(x_sub)
+    y_sub.backward(gfull[sub.to(DEV)].cpu())
+    for name, (h, r) in {"output": (y[sub.to(DEV)], y_sub), "grad_x": (gx[sub.to(DEV)], x_sub.grad)}.items():
+        assert rel_err(h, r) <= F32_TOL and elem_err(h, r) <= ELEM_RTOL, (name, rel_err(h, r), elem_err(h, r))
 
     row_sums = glut.sum(dim=1)  # [T, O]
     want = (gfull.view(b, o).double().sum(0) * s).float()
