@@ -5,8 +5,9 @@ Bars:
   * route codes and margins: bit-exact (torch.equal on int64 codes and on the
     f32 margin bit patterns);
   * f32 LUT: forward output and every gradient within 1e-5 relative error,
-    measured norm-wise as max|hip - oracle| / max|oracle|, and in training
-    also element by element within 2e-4 of |oracle| + 1e-3 max|oracle|;
+    measured norm-wise as max|hip - oracle| / max|oracle|, and (training,
+    f32 eval forward, views, c4's sampled rows) also element by element
+    within 2e-4 of |oracle| + 1e-3 max|oracle|;
   * f16 LUT reads: within 1e-3 relative of the f32-LUT oracle.
 The reference's own parity tests (test_backend_parity.py:348-369) use
 allclose(atol=1e-6); test_reference_case repeats that case and bar.
@@ -181,6 +182,7 @@ def test_eval_forward_f32(i, o, t, c, b):
         y_hip = hip.eval()(x.to(DEV))
     assert torch.equal(hip._last_indices.cpu(), ref._last_indices)
     assert rel_err(y_hip, y_ref) <= F32_TOL
+    assert elem_err(y_hip, y_ref) <= ELEM_RTOL
 
 
 @pytest.mark.parametrize(
