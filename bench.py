@@ -16,8 +16,12 @@ Timed regions (both full fwd+bwd of the module API, no work skipped):
             the launch-bound loop four steps at a time keeps the GPU busy. The
             rate with one step per graph is reported beside it.
   eager  -- plain autograd steps back to back (as the reference harness
-            times its train step, tools/benchmarking/benchmark.py:105-118);
-            the kernels of each step carry HIP events that their own dispatch
+            times its train step, tools/benchmarking/benchmark.py:105-118),
+            and again under torch.autograd.set_multithreading_enabled(False),
+            torch's switch that runs the backward on the calling thread
+            instead of handing it to the device's autograd thread and back
+            (`eager_us_per_step_calling_thread_engine`); in a third run the
+            kernels of each step carry HIP events that their own dispatch
             stamps (library hook tropnn_hip_arm_kernel_events, via
             hipExtLaunchKernel), giving the per-kernel durations `roofline`
             uses.
@@ -977,6 +981,18 @@ def bench_c2(args, dev) -> dict:
     torch.cuda.synchronize()
     eager_us = (time.perf_counter() - t0) * 1e6 / esteps
     log(f"eager {eager_us:.1f} us/step")
+    # the same steps with torch's calling-thread autograd engine: the default
+    # engine hands every backward to its device thread and back
+    with torch.autograd.set_multithreading_enabled(False):
+        for w in range(nb):
+            step(w)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(esteps):
+            step(k % nb)
+        torch.cuda.synchronize()
+        eager_ct_us = (time.perf_counter() - t0) * 1e6 / esteps
+    log(f"eager {eager_ct_us:.1f} us/step (torch.autograd.set_multithreading_enabled(False))")
     fused = fused_backward()
     algo = algorithmic_bytes(fused)
     comp = compulsory_bytes(fused)
@@ -1052,6 +1068,7 @@ def bench_c2(args, dev) -> dict:
         },
         "us_per_step_one_step_per_graph": round(graph1_us, 3),
         "eager_us_per_step": round(eager_us, 3),
+        "eager_us_per_step_calling_thread_engine": round(eager_ct_us, 3),
         "kernels": kernels,
     }
     if cpu:
