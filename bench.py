@@ -127,8 +127,8 @@ def compulsory_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = T
       backward_reduce: grad_thr;
       backward_scatter: grad_x and the anchors;
       backward_sort: nothing.
-    The step total at c2 is 14,589,824 B: SURVEY's 9,981,056 B (every
-    tensor once), plus the code bytes and the backward's second LUT read."""
+    The step total at c2 is 14,589,824 B: 9,981,056 B for every tensor of the
+    step once, plus the code bytes and the backward's second LUT read."""
     r = 1 << c
     lut = e * t * min(b, r) * o
     grad_lut = 4 * t * r * o
