@@ -105,6 +105,53 @@ Dims validate(const Tensor &latent, const Tensor &anchors, const Tensor &thresho
 
 constexpr int64_t kRouteNone = 0, kRouteFull = 1, kRouteCodes = 2;
 
+// One forward launch and the tensors it writes.
+struct Forward {
+    Tensor out, indices, margins, record, saved_margins;
+    Tensor lut_read;  // the contiguous LUT the kernels read
+};
+
+// Validation, allocation and the forward launch. want_record: the backward
+// will read the route record; want_margins: the full-STE backward will read
+// every comparison's margin.
+Forward run_forward(const Dims &d, const Tensor &latent, const Tensor &anchors, const Tensor &thresholds,
+                    const Tensor &lut_read, double output_scale, int64_t route_mode, bool want_record,
+                    bool want_margins) {
+    const int64_t items = d.batch * d.steps;
+    const bool full_route = route_mode == kRouteFull;
+    const Tensor x = latent.contiguous();  // [B,S,I] is [items, I] row-major
+    const Tensor anc = anchors.contiguous(), thr = thresholds.contiguous(), lut_c = lut_read.contiguous();
+    const auto f32 = latent.options();
+    Forward f;
+    f.lut_read = lut_c;
+    f.out = at::empty({d.batch, d.steps, d.out_f}, f32);
+    if (want_record) f.record = at::empty({d.tables, items}, f32.dtype(at::kLong));
+    if (full_route) {
+        f.indices = at::empty({d.batch, d.steps, d.tables}, f32.dtype(at::kLong));
+        f.margins = at::empty({d.batch, d.steps, d.tables, d.comps}, f32);
+    } else {
+        f.indices = at::empty({d.batch, d.steps, route_mode == kRouteCodes ? d.tables : 0},
+                              f32.dtype(route_mode == kRouteCodes ? at::kByte : at::kLong));
+        f.margins = at::empty({d.batch, d.steps, 0}, f32);
+    }
+    // the margins the full-STE backward reads
+    if (want_margins) f.saved_margins = full_route ? f.margins : at::empty({items, d.tables, d.comps}, f32);
+
+    TORCH_CHECK(g_bound.load(std::memory_order_acquire), "tropnn_hip.pairwise: the C ABI is not bound");
+    const int lut_dtype = lut_c.scalar_type() == at::kHalf ? TROPNN_LUT_F16 : TROPNN_LUT_F32;
+    const int rc = g_abi.forward(
+        items, d.in_f, d.out_f, d.tables, d.comps, x.const_data_ptr<float>(), anc.const_data_ptr<int64_t>(),
+        thr.const_data_ptr<float>(), lut_c.const_data_ptr(), lut_dtype, static_cast<float>(output_scale),
+        f.out.mutable_data_ptr<float>(),
+        want_record ? reinterpret_cast<tropnn_route_record *>(f.record.mutable_data_ptr()) : nullptr,
+        full_route ? f.indices.mutable_data_ptr<int64_t>() : nullptr,
+        full_route ? f.margins.mutable_data_ptr<float>()
+                   : (want_margins ? f.saved_margins.mutable_data_ptr<float>() : nullptr),
+        route_mode == kRouteCodes ? f.indices.mutable_data_ptr<uint8_t>() : nullptr, current_stream(x));
+    check_rc(rc, "tropnn_hip_pairwise_forward");
+    return f;
+}
+
 struct PairwiseFunction : public torch::autograd::Function<PairwiseFunction> {
     // Argument order fixes the input-edge numbering of needs_input_grad:
     // tensors latent 0, anchors 1, thresholds 2, lut 3, lut_read 4 (the
@@ -115,7 +162,6 @@ struct PairwiseFunction : public torch::autograd::Function<PairwiseFunction> {
                                  const std::optional<Tensor> &index_entries, bool ste, bool min_margin,
                                  int64_t surrogate, double output_scale, int64_t route_mode, bool recorded) {
         const Dims d = validate(latent, anchors, thresholds, lut_read);
-        const int64_t items = d.batch * d.steps;
         // What the backward may be asked for: every input that requires a
         // gradient, when autograd records this call. (needs_input_grad is
         // narrower inside a backward pass, e.g. a checkpoint recompute under
@@ -127,41 +173,13 @@ struct PairwiseFunction : public torch::autograd::Function<PairwiseFunction> {
         const bool needs_route = ste && (g_x || g_thr);
         const bool want_record = g_lut || needs_route;
         const bool want_margins = needs_route && !min_margin;
-        const bool full_route = route_mode == kRouteFull;
         if (ste && g_x)
             TORCH_CHECK(index_offsets.has_value() && index_entries.has_value(),
                         "the latent gradient needs the inverse anchor index");
-
-        const Tensor x = latent.contiguous();  // [B,S,I] is [items, I] row-major
-        const Tensor anc = anchors.contiguous(), thr = thresholds.contiguous(), lut_c = lut_read.contiguous();
-        const auto f32 = latent.options();
-        Tensor out = at::empty({d.batch, d.steps, d.out_f}, f32);
-        Tensor record = want_record ? at::empty({d.tables, items}, f32.dtype(at::kLong)) : Tensor();
-        Tensor indices, margins;
-        if (full_route) {
-            indices = at::empty({d.batch, d.steps, d.tables}, f32.dtype(at::kLong));
-            margins = at::empty({d.batch, d.steps, d.tables, d.comps}, f32);
-        } else {
-            indices = at::empty({d.batch, d.steps, route_mode == kRouteCodes ? d.tables : 0},
-                                f32.dtype(route_mode == kRouteCodes ? at::kByte : at::kLong));
-            margins = at::empty({d.batch, d.steps, 0}, f32);
-        }
-        // the margins the full-STE backward reads
-        Tensor saved_margins;
-        if (want_margins) saved_margins = full_route ? margins : at::empty({items, d.tables, d.comps}, f32);
-
-        TORCH_CHECK(g_bound.load(std::memory_order_acquire), "tropnn_hip.pairwise: the C ABI is not bound");
-        const int lut_dtype = lut_c.scalar_type() == at::kHalf ? TROPNN_LUT_F16 : TROPNN_LUT_F32;
-        const int rc = g_abi.forward(
-            items, d.in_f, d.out_f, d.tables, d.comps, x.const_data_ptr<float>(), anc.const_data_ptr<int64_t>(),
-            thr.const_data_ptr<float>(), lut_c.const_data_ptr(), lut_dtype, static_cast<float>(output_scale),
-            out.mutable_data_ptr<float>(),
-            want_record ? reinterpret_cast<tropnn_route_record *>(record.mutable_data_ptr()) : nullptr,
-            full_route ? indices.mutable_data_ptr<int64_t>() : nullptr,
-            full_route ? margins.mutable_data_ptr<float>()
-                       : (want_margins ? saved_margins.mutable_data_ptr<float>() : nullptr),
-            route_mode == kRouteCodes ? indices.mutable_data_ptr<uint8_t>() : nullptr, current_stream(x));
-        check_rc(rc, "tropnn_hip_pairwise_forward");
+        Forward f = run_forward(d, latent, anchors, thresholds, lut_read, output_scale, route_mode, want_record,
+                                want_margins);
+        Tensor &out = f.out, &indices = f.indices, &margins = f.margins, &record = f.record,
+               &saved_margins = f.saved_margins, &lut_c = f.lut_read;
 
         ctx->set_materialize_grads(false);
         ctx->mark_non_differentiable({indices, margins});
@@ -240,6 +258,12 @@ std::tuple<Tensor, Tensor, Tensor> pairwise(const Tensor &latent, const Tensor &
                       "unknown route mode ", route_mode);
     const bool recorded =
         at::GradMode::is_enabled() && (latent.requires_grad() || thresholds.requires_grad() || lut.requires_grad());
+    if (!recorded) {
+        // no backward node: the launch alone (inference, torch.no_grad)
+        const Dims d = validate(latent, anchors, thresholds, lut_read);
+        Forward f = run_forward(d, latent, anchors, thresholds, lut_read, output_scale, route_mode, false, false);
+        return {f.out, f.indices, f.margins};
+    }
     auto outs = PairwiseFunction::apply(latent, anchors, thresholds, lut, lut_read.detach(), index_offsets,
                                         index_entries, ste, min_margin, surrogate, output_scale, route_mode,
                                         recorded);
