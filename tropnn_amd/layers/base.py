@@ -143,6 +143,6 @@ class RoutedLinearBase(nn.Module, ABC):
             self._route_debug = RouteDebug(codes=indices.detach(), recompute_margins=self._recompute_margins(latent))
         elif mode:
             self._route_debug = RouteDebug(indices=indices.detach(), margins=margins.detach())
-        else:
+        elif self._route_debug is not None:  # nn.Module.__setattr__ only when it changes
             self._route_debug = None
         return output if output.dtype == input_dtype else output.to(dtype=input_dtype)
