@@ -267,9 +267,7 @@ __device__ __forceinline__ void feature_walk(const float *gud, const int *idx_s,
             }
         }
         if (pair) {
-            // the partner lane's sum (DPP quad_perm [1,0,3,2]: lane ^ 1)
-            const float other = __builtin_bit_cast(
-                float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, gx), 0xB1, 0xF, 0xF, false));
+            const float other = dpp<kXor1>(gx);  // the partner lane's sum
             if (h == 0) __builtin_nontemporal_store(gx + other, grad_x_row + f);
         } else {
             __builtin_nontemporal_store(gx, grad_x_row + f);

@@ -437,7 +437,7 @@ __global__ __launch_bounds__(kWaveThreads) void pairwise_forward_wave_kernel(Fwd
     static_assert(P == 1 || P == 2 || P == 4 || P == 8, "1, 2, 4 or 8 items per wave");
     using u32x4 = vec_t<uint32_t, 4>;
     extern __shared__ __align__(16) unsigned char lds[];
-    WaveComparator *cmp = reinterpret_cast<WaveComparator *>(lds);  // [T][kC]
+    WaveComparator *cmp = reinterpret_cast<WaveComparator *>(lds);  // [kC][T]
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     float *xs = reinterpret_cast<float *>(lds + a.wave_x_off) + wave * P * a.in_f;  // [in_f][P]: items interleaved
@@ -447,7 +447,8 @@ __global__ __launch_bounds__(kWaveThreads) void pairwise_forward_wave_kernel(Fwd
     const int C = a.comps;
 
     // 1. comparators (kC slots per table; the unused ones compare x[0] with
-    // itself); this wave's input rows
+    // itself), slot-major so that the route's lanes (consecutive tables) read
+    // consecutive 8-byte words; this wave's input rows
 #pragma unroll 4
     for (int k = tid; k < a.tables * kC; k += kWaveThreads) {
         const int t = k / kC, c = k - t * kC;
@@ -455,7 +456,7 @@ __global__ __launch_bounds__(kWaveThreads) void pairwise_forward_wave_kernel(Fwd
         const uint32_t ia = static_cast<uint32_t>(clamp_index(a.anchors[2 * tc], a.in_f));
         const uint32_t ib = static_cast<uint32_t>(clamp_index(a.anchors[2 * tc + 1], a.in_f));
         const float th = a.thr[tc];
-        cmp[k] = c < C ? WaveComparator{ia | (ib << 16), th} : WaveComparator{0u, 0.f};
+        cmp[c * a.tables + t] = c < C ? WaveComparator{ia | (ib << 16), th} : WaveComparator{0u, 0.f};
     }
     {
         // element f of item i at xs[f * P + i], so that one vector read gets
@@ -498,7 +499,7 @@ __global__ __launch_bounds__(kWaveThreads) void pairwise_forward_wave_kernel(Fwd
                 pm[i] = 0.f;
             }
             for (int c = 0; c < C; ++c) {
-                const WaveComparator q = cmp[t * kC + c];
+                const WaveComparator q = cmp[c * a.tables + t];
                 const vec_t<float, P> xa = *reinterpret_cast<const vec_t<float, P> *>(xs + (q.ab & 0xFFFFu) * P);
                 const vec_t<float, P> xb = *reinterpret_cast<const vec_t<float, P> *>(xs + (q.ab >> 16) * P);
 #pragma unroll
