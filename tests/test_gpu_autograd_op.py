@@ -55,6 +55,16 @@ def test_forward_under_no_grad_and_with_grad_agree():
     assert out0.grad_fn is None and out1.grad_fn is not None
     assert not idx1.requires_grad and not mar1.requires_grad
     assert torch.equal(out0, out1) and torch.equal(idx0, idx1) and torch.equal(mar0, mar1)
+    # a call that records nothing because no input needs a gradient (the
+    # operator then launches without its autograd function), in every route
+    # mode, against the recorded call
+    frozen = (latent.detach(), anchors, thr.detach(), lut.detach())
+    for mode in (True, "codes", False):
+        out2, idx2, mar2 = pairwise_hip(*frozen, output_scale=0.25, return_route=mode)
+        out3, idx3, mar3 = pairwise_hip(latent, anchors, thr, lut, output_scale=0.25, return_route=mode)
+        assert out2.grad_fn is None and not out2.requires_grad and out3.grad_fn is not None
+        assert torch.equal(out2, out3) and torch.equal(idx2, idx3) and torch.equal(mar2, mar3)
+        assert idx2.dtype == idx3.dtype and idx2.shape == idx3.shape and mar2.shape == mar3.shape
 
 
 def test_only_lut_gradient_when_latent_and_thresholds_are_frozen():
