@@ -6,25 +6,34 @@ G ~ N(0,1); one step = forward + fast_sigmoid_odd min-margin STE backward
 (y = layer(x); y.backward(G)) with x, thresholds and LUT gradients. Params are
 the module's seeded init (seed 0); inputs are synthetic and already in HBM.
 
-Timed regions (both full fwd+bwd of the module API, no work skipped):
+Timed regions (both full fwd+bwd of the module API, no work skipped), each
+measured by time_windows(): windows of exactly K = --steps steps are issued
+back to back with a HIP event between consecutive windows, after >= 0.3 s of
+warmup (the GPU clocks ramp up under sustained load); at least 25 windows,
+100 steps and 0.2 s are timed and the MEDIAN window per step is reported,
+with the fastest and slowest windows and the wall-clock mean beside it:
   graph  -- the steps captured in HIP graphs (torch.cuda.CUDAGraph), four
             steps per graph, one on each of 4 distinct resident (x, G)
-            batches: exactly K steps are timed (K // 4 four-step replays, then
-            K % 4 one-step replays), after >= 0.3 s of replays (the GPU clocks
-            ramp up under sustained load). This is `value`. One graph launch
-            costs 14-19 us of host time and ~5 us on the device, so capturing
-            the launch-bound loop four steps at a time keeps the GPU busy. The
-            rate with one step per graph is reported beside it.
+            batches (a window is K // 4 four-step replays, then K % 4
+            one-step replays). This is `value` / `ms_per_step`. One graph
+            launch costs 14-19 us of host time and ~5 us on the device, so
+            capturing the launch-bound loop four steps at a time keeps the GPU
+            busy. The rate with one step per graph, and with the reference
+            shell's route debug tensors written (cache_route_debug=True), are
+            reported beside it.
   eager  -- plain autograd steps back to back (as the reference harness
             times its train step, tools/benchmarking/benchmark.py:105-118),
             and again under torch.autograd.set_multithreading_enabled(False),
             torch's switch that runs the backward on the calling thread
             instead of handing it to the device's autograd thread and back
-            (`eager_us_per_step_calling_thread_engine`); in a third run the
-            kernels of each step carry HIP events that their own dispatch
-            stamps (library hook tropnn_hip_arm_kernel_events, via
-            hipExtLaunchKernel), giving the per-kernel durations `roofline`
-            uses.
+            (`eager_us_per_step_calling_thread_engine`); in a further 200
+            steps the kernels of each step carry HIP events that their own
+            dispatch stamps (library hook tropnn_hip_arm_kernel_events, via
+            hipExtLaunchKernel), giving the per-kernel durations (mean,
+            median, min, max) that `roofline` uses.
+peak_bytes: device bytes allocated above the resident state by one eval
+forward and by one fwd+bwd step, measured as the reference harness measures
+them (tools/benchmarking/benchmark.py:57-88), and the backward's workspace.
 
 roofline (the dominant kernel, the longest average duration):
   achieved / frac -- HBM bytes per launch as rocprofv3 counts them
@@ -46,7 +55,9 @@ inference only) on the same cores.
 Other BASELINE.json configs, each its own JSON line (--workload): c1, the
 small f32 eval forward at batch 8 (latency); c3, the f16 eval forward sweep
 at batch 1 / 64 / 8192; c4, the large f16-LUT layer fwd+bwd at batch 8192;
-c5, the EMNIST classifier training step and its 100-step loss curve.
+c5, the EMNIST classifier training step and its 100-step loss curve. The
+default run also measures all four after the headline and adds compact
+records of them under `other_configs` (--other-configs off skips them).
 
 Prints ONE JSON line.
 """
@@ -389,22 +400,124 @@ def _kernel_events(names, n):
     return evs
 
 
-def _graph_per_call_us(graphs, steps: int, warmup: int) -> float:
-    """us per replay over `steps` replays of `graphs` round robin, after
-    >= 0.3 s (and >= warmup replays) of warmup."""
+def _spread(values) -> dict:
+    """mean, median, min and max of a list of per-launch (or per-step) times."""
+    v = sorted(values)
+    return {"mean": sum(v) / len(v), "median": v[len(v) // 2], "min": v[0], "max": v[-1], "n": len(v)}
+
+
+def time_windows(window, steps: int, warmup: int, min_windows: int = 25, min_steps: int = 100,
+                 min_seconds: float = 0.2) -> dict:
+    """Device time per step, measured the way BASELINE.md plans it (the median
+    over >= 100 steps). window() issues one window of `steps` steps without
+    waiting for them. After >= `warmup` warmup windows and >= 0.3 s of them
+    (the GPU clocks ramp up under sustained load), n windows are issued back
+    to back with no host synchronisation between them and a HIP event
+    recorded on the current stream between consecutive windows, n =
+    max(min_windows, ceil(min_steps / steps), the windows that fill
+    min_seconds). Each window's time is the interval between its two events;
+    the figure is the median window per step, with the fastest and slowest
+    windows and the wall-clock mean over the whole timed region beside it, so
+    one host stall moves one window, not the figure."""
+    import math
+
     import torch
 
+    stream = torch.cuda.current_stream()
     torch.cuda.synchronize()
     t0, w = time.perf_counter(), 0
-    while w < warmup or time.perf_counter() - t0 < 0.3:
-        graphs[w % len(graphs)].replay()
+    while w < max(warmup, 2) or time.perf_counter() - t0 < 0.3:
+        window()
         w += 1
     torch.cuda.synchronize()
+    est_s = (time.perf_counter() - t0) / w
+    n = max(min_windows, math.ceil(min_steps / steps), math.ceil(min_seconds / max(est_s, 1e-9)))
+    n = min(n, 20000)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    window()  # queue work ahead of the first event so it marks a busy device
     t0 = time.perf_counter()
-    for k in range(steps):
-        graphs[k % len(graphs)].replay()
+    evs[0].record(stream)
+    for k in range(n):
+        window()
+        evs[k + 1].record(stream)
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e6 / steps
+    wall = time.perf_counter() - t0
+    per_step = sorted(1e3 * evs[k].elapsed_time(evs[k + 1]) / steps for k in range(n))
+    return {
+        "us_per_step": per_step[n // 2],
+        "min": per_step[0],
+        "max": per_step[-1],
+        "windows": n,
+        "steps_per_window": steps,
+        "wall_mean": wall * 1e6 / (n * steps),
+    }
+
+
+def window_fields(t: dict, prefix: str = "") -> dict:
+    """The spread of a time_windows() result as JSON fields (us per step)."""
+    return {
+        f"{prefix}windows": t["windows"],
+        f"{prefix}window_min_us": round(t["min"], 3),
+        f"{prefix}window_max_us": round(t["max"], 3),
+        f"{prefix}wall_mean_us": round(t["wall_mean"], 3),
+    }
+
+
+def peak_bytes(fn, dev) -> int:
+    """Peak device bytes allocated by one fn() call above what was allocated
+    before it, measured as the reference harness measures its forward and
+    train peaks (tools/benchmarking/benchmark.py:57-88): memory_allocated
+    before, reset_peak_memory_stats, the call and a synchronize,
+    max_memory_allocated after."""
+    import torch
+
+    torch.cuda.synchronize(dev)
+    base = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    out = fn()
+    torch.cuda.synchronize(dev)
+    peak = torch.cuda.max_memory_allocated(dev)
+    del out
+    torch.cuda.synchronize(dev)
+    return max(0, int(peak - base))
+
+
+def eval_peak_bytes(layer, x, dev) -> int:
+    """Peak bytes of one eval forward under torch.no_grad (benchmark.py:57-70)."""
+    import torch
+
+    def fn():
+        with torch.no_grad():
+            return layer(x)
+
+    layer.eval()
+    return peak_bytes(fn, dev)
+
+
+def train_peak_bytes(layer, x, g, dev) -> int:
+    """Peak bytes of one fwd+bwd step (y = layer(x); y.backward(G)) with the
+    gradients set to None before the baseline is read, as benchmark.py:73-88
+    measures its train step; the gradients the step leaves are part of the
+    peak."""
+    def fn():
+        layer(x).backward(g)
+
+    layer.train()
+    layer.zero_grad(set_to_none=True)
+    x.grad = None
+    out = peak_bytes(fn, dev)
+    layer.zero_grad(set_to_none=True)
+    x.grad = None
+    return out
+
+
+def backward_workspace_bytes(b: int, i: int, o: int, t: int, c: int, lut_f16: bool) -> int:
+    """The device workspace one min-margin STE backward allocates
+    (tropnn_hip_pairwise_backward_workspace_size)."""
+    from tropnn_amd.backends.pairwise_hip import LUT_F16, LUT_F32, STE_MIN_MARGIN, load_library
+
+    return int(load_library().tropnn_hip_pairwise_backward_workspace_size(
+        b, i, o, t, c, LUT_F16 if lut_f16 else LUT_F32, STE_MIN_MARGIN))
 
 
 def _eval_forward_gpu(layer, xs, steps: int, warmup: int) -> dict:
@@ -412,28 +525,28 @@ def _eval_forward_gpu(layer, xs, steps: int, warmup: int) -> dict:
     eager calls (benchmark.py:91-102's loop), the median latency of one call
     to its result (call, then synchronize), one HIP graph per call replayed
     back to back, and the forward kernel's own duration (events stamped by
-    its dispatch)."""
+    its dispatch). Back-to-back figures are time_windows() medians of windows
+    of `steps` calls."""
     import torch
 
     from tropnn_amd.backends.pairwise_hip import arm_kernel_events
 
     nb = len(xs)
+    ctr = [0]
+
+    def eager_window() -> None:
+        with torch.no_grad():
+            for _ in range(steps):
+                layer(xs[ctr[0] % nb])
+                ctr[0] += 1
+
     with torch.no_grad():
         for x in xs:
             layer(x)
-        torch.cuda.synchronize()
-        t0, w = time.perf_counter(), 0
-        while w < warmup or time.perf_counter() - t0 < 0.3:
-            layer(xs[w % nb])
-            w += 1
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for k in range(steps):
-            layer(xs[k % nb])
-        torch.cuda.synchronize()
-        eager_us = (time.perf_counter() - t0) * 1e6 / steps
+    eager = time_windows(eager_window, steps, warmup)
+    with torch.no_grad():
         lat = []
-        for k in range(min(steps, 200)):
+        for k in range(min(steps * 10, 200)):
             t0 = time.perf_counter()
             layer(xs[k % nb])
             torch.cuda.synchronize()
@@ -446,15 +559,23 @@ def _eval_forward_gpu(layer, xs, steps: int, warmup: int) -> dict:
             with torch.cuda.graph(gph):
                 layer(x)
             graphs.append(gph)
-    graph_us = _graph_per_call_us(graphs, steps, warmup)
+
+    def graph_window() -> None:
+        for _ in range(steps):
+            graphs[ctr[0] % nb].replay()
+            ctr[0] += 1
+
+    graph = time_windows(graph_window, steps, warmup)
     evs = _kernel_events(("forward",), 100)["forward"]
     with torch.no_grad():
         for k, (e0, e1) in enumerate(evs):
             arm_kernel_events("forward", e0, e1)
             layer(xs[k % nb])
     torch.cuda.synchronize()
-    kus = sorted(1e3 * e0.elapsed_time(e1) for e0, e1 in evs)[len(evs) // 2]
-    return {"eager_us_per_call": eager_us, "sync_latency_us": sync_us, "graph_us_per_call": graph_us, "kernel_us": kus}
+    kern = _spread([1e3 * e0.elapsed_time(e1) for e0, e1 in evs])
+    return {"eager_us_per_call": eager["us_per_step"], "sync_latency_us": sync_us,
+            "graph_us_per_call": graph["us_per_step"], "kernel_us": kern["median"], "kernel_us_mean": kern["mean"],
+            "kernel_spread": kern, "eager_windows": eager, "graph_windows": graph}
 
 
 # ---------------------------------------------------------------- workloads
@@ -475,7 +596,8 @@ def bench_c1(args, dev) -> dict:
     gen = torch.Generator().manual_seed(0)
     xs = [torch.randn(b, C1["i"], generator=gen).to(dev) for _ in range(4)]
     gpu = _eval_forward_gpu(layer, xs, args.steps, args.warmup)
-    log("c1: " + ", ".join(f"{k}={v:.2f}" for k, v in gpu.items()))
+    log("c1: " + ", ".join(f"{k}={v:.2f}" for k, v in gpu.items() if isinstance(v, float)))
+    fwd_peak = eval_peak_bytes(layer, xs[0], dev)
     algo = 4 * b * C1["i"] + 20 * C1["t"] * C1["c"] + 4 * b * C1["t"] * C1["o"] + 4 * b * C1["o"]
     cpus = []
     if args.cpu_budget > 0:
@@ -503,9 +625,11 @@ def bench_c1(args, dev) -> dict:
         "sync_latency_us": round(gpu["sync_latency_us"], 3),
         "graph_us_per_call": round(gpu["graph_us_per_call"], 3),
         "kernel_us": round(gpu["kernel_us"], 3),
-        "roofline": roofline("forward", gpu["kernel_us"], algo,
+        **window_fields(gpu["eager_windows"]),
+        "roofline": roofline("forward", gpu["kernel_us_mean"], algo,
                              compulsory_bytes(True, b=b, i=C1["i"], o=C1["o"], t=C1["t"], c=C1["c"])["forward"] - b * C1["t"],
                              "c1"),
+        "peak_bytes": {"forward": fwd_peak},
         "cpu_baseline": cpus[0] if cpus else None,
         "cpu_baselines": cpus,
     }
@@ -540,16 +664,20 @@ def bench_c3(args, dev) -> dict:
         # skips the Python path, at large ones eager calls pipeline behind the
         # kernels while each graph launch adds its own host and device cost
         us = min(gpu["eager_us_per_call"], gpu["graph_us_per_call"])
+        mode = "eager" if us == gpu["eager_us_per_call"] else "graph"
         res = {
             "kernel_us": round(gpu["kernel_us"], 3),
+            "kernel_us_mean": round(gpu["kernel_us_mean"], 3),
             "us_per_call": round(us, 3),
-            "mode": "eager" if us == gpu["eager_us_per_call"] else "graph",
+            "mode": mode,
             "eager_us_per_call": round(gpu["eager_us_per_call"], 3),
             "graph_us_per_call": round(gpu["graph_us_per_call"], 3),
             "sync_latency_us": round(gpu["sync_latency_us"], 3),
+            **window_fields(gpu[f"{mode}_windows"]),
             "samples_per_s": round(b / (us * 1e-6), 1),
             "algorithmic_bytes": algo,
             "algorithmic_GBs": round(algo / (us * 1e-6) / 1e9, 1),
+            "forward_peak_bytes": eval_peak_bytes(layer, xs[0], dev),
         }
         log(f"c3 batch {b}: graph {gpu['graph_us_per_call']:.2f} us/call, eager {gpu['eager_us_per_call']:.2f}, "
             f"kernel {gpu['kernel_us']:.2f} us")
@@ -581,7 +709,7 @@ def bench_c3(args, dev) -> dict:
                    "mode": "module eval calls back to back under torch.no_grad: eager or one HIP graph per call, "
                    "the faster (per_batch.mode)"},
         "per_batch": results,
-        "roofline": roofline("forward", big["kernel_us"], big["algorithmic_bytes"], comp, "c3"),
+        "roofline": roofline("forward", big["kernel_us_mean"], big["algorithmic_bytes"], comp, "c3"),
         "cpu_baseline": results["8192"].get("cpu_baselines", [None])[0],
     }
     return out
@@ -622,6 +750,11 @@ def bench_c5(args, dev) -> dict:
             step(w % nb)
     torch.cuda.current_stream(dev).wait_stream(side)
     torch.cuda.synchronize()
+    # peak bytes of one eager training step (forward, loss, backward,
+    # optimizer step) after the optimizer state exists, the gradients set to
+    # None before the baseline is read (benchmark.py:73-88)
+    opt.zero_grad(set_to_none=True)
+    train_peak = peak_bytes(lambda: step(0), dev)
     graphs = []
     for k in range(nb):
         opt.zero_grad(set_to_none=True)
@@ -630,17 +763,16 @@ def bench_c5(args, dev) -> dict:
             step(k)
         graphs.append(gph)
     torch.cuda.synchronize()
-    t0, w = time.perf_counter(), 0
-    while w < args.warmup or time.perf_counter() - t0 < 0.3:
-        graphs[w % nb].replay()
-        w += 1
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(args.steps):
-        graphs[k % nb].replay()
-    torch.cuda.synchronize()
-    us = (time.perf_counter() - t0) * 1e6 / args.steps
-    log(f"c5 graph {us:.1f} us/step")
+    ctr = [0]
+
+    def window() -> None:
+        for _ in range(args.steps):
+            graphs[ctr[0] % nb].replay()
+            ctr[0] += 1
+
+    tw = time_windows(window, args.steps, args.warmup)
+    us = tw["us_per_step"]
+    log(f"c5 graph {us:.1f} us/step (median of {tw['windows']} windows, {tw['min']:.1f}-{tw['max']:.1f})")
     curve = c5_loss_curve(dev, args.curve_steps) if args.curve_steps > 0 else None
     cpu = cpu_baseline_c5(args.cpu_budget) if args.cpu_budget > 0 else None
     value = 512 / (us * 1e-6)
@@ -664,8 +796,10 @@ def bench_c5(args, dev) -> dict:
             "one HIP graph per training step",
             "batch": 512,
         },
+        **window_fields(tw),
         "layer_algorithmic_bytes_per_step": C5_LAYER_BYTES,
         "layer_algorithmic_GBs": round(C5_LAYER_BYTES / (us * 1e-6) / 1e9, 1),
+        "peak_bytes": {"train_step": train_peak},
         "cpu_baseline": cpu,
         "loss_curve": curve,
     }
@@ -716,7 +850,7 @@ def c5_loss_curve(dev, steps: int) -> dict:
         loss_r.backward()
         opt_ref.step()
         hip_loss.append(loss.detach().item())
-        ref_loss.append(float(loss_r))
+        ref_loss.append(loss_r.item())
         same_codes.append(all(torch.equal(a._last_indices.cpu(), b._last_indices) for a, b in zip(model.layers, ref_layers)))
     first_diff = next((k for k, s in enumerate(same_codes) if not s), None)
     rel = [abs(a - b) / abs(b) for a, b in zip(hip_loss, ref_loss)]
@@ -812,20 +946,35 @@ def bench_c4(args, dev) -> dict:
     for w in range(args.warmup):
         step(w % nb)
     torch.cuda.synchronize()
+    train_peak = train_peak_bytes(layer, xs[0], gs[0], dev)
+    workspace = backward_workspace_bytes(b, C4["i"], C4["o"], C4["t"], C4["c"], True)
     algo = algorithmic_bytes(False, e=2, streamed=True, **C4)
     comp = compulsory_bytes(False, e=2, streamed=True, **C4)
     names = tuple(algo)
+    ctr = [0]
+
+    def window() -> None:
+        for _ in range(args.steps):
+            step(ctr[0] % nb)
+            ctr[0] += 1
+
+    # steps take milliseconds: at least 5 windows and 10 steps (BASELINE.md's
+    # >= 10 for c4), no time floor
+    tw = time_windows(window, args.steps, 0, min_windows=5, min_steps=10, min_seconds=0.0)
+    step_ms = tw["us_per_step"] * 1e-3
+    # per-kernel durations over further steps, from events each kernel's own
+    # dispatch stamps (kept out of the timed windows above)
     evs = _kernel_events(names, args.steps)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for k in range(args.steps):
         for n in names:
             arm_kernel_events(n, *evs[n][k])
         step(k % nb)
     torch.cuda.synchronize()
-    step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    kern_us = {n: 1e3 * sum(e0.elapsed_time(e1) for e0, e1 in evs[n]) / args.steps for n in names}
-    log(f"c4 {step_ms:.2f} ms/step; kernels (ms): " + ", ".join(f"{n}={v * 1e-3:.3f}" for n, v in kern_us.items()))
+    spread = {n: _spread([1e3 * e0.elapsed_time(e1) for e0, e1 in evs[n]]) for n in names}
+    kern_us = {n: spread[n]["mean"] for n in names}
+    log(f"c4 {step_ms:.2f} ms/step (median of {tw['windows']} windows of {args.steps}); kernels (ms): "
+        + ", ".join(f"{n}={v * 1e-3:.3f}" for n, v in kern_us.items()))
     dom = max(names, key=lambda n: kern_us[n])
     cpu = None
     if args.cpu_budget > 0:
@@ -861,8 +1010,10 @@ def bench_c4(args, dev) -> dict:
             "lut_dtype": "f16",
             "mode": "eager module fwd+bwd",
         },
+        **window_fields(tw),
         "roofline": roofline(dom, kern_us[dom], algo[dom], comp[dom], "c4"),
         "cpu_baseline": cpu,
+        "peak_bytes": {"train_step": train_peak, "backward_workspace": workspace},
         "step": {
             "hbm_traffic_bytes": step_traffic,
             "hbm_frac": round(step_traffic / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if step_traffic else None,
@@ -872,7 +1023,8 @@ def bench_c4(args, dev) -> dict:
             "algorithmic_frac": round(total_algo / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         },
         "kernels": {
-            n: {"avg_us": round(kern_us[n], 1), "algorithmic_bytes": algo[n], "compulsory_bytes": comp[n],
+            n: {"avg_us": round(kern_us[n], 1), "min_us": round(spread[n]["min"], 1),
+                "max_us": round(spread[n]["max"], 1), "algorithmic_bytes": algo[n], "compulsory_bytes": comp[n],
                 "hbm_traffic_bytes": traffic[n], "l2_hit_rate": l2_hit_rate(n, "c4"),
                 "achieved_GBs": round(algo[n] / (kern_us[n] * 1e-6) / 1e9, 1) if kern_us[n] > 0 else None}
             for n in names
@@ -916,9 +1068,12 @@ def bench_c2(args, dev) -> dict:
         layer(xs[k]).backward(gs[k])
 
     stream = torch.cuda.current_stream(dev)
-    for w in range(args.warmup):  # eager warmup (allocator, library, anchor index)
+    for w in range(max(args.warmup, nb)):  # eager warmup (allocator, library, anchor index)
         step(w % nb)
     torch.cuda.synchronize()
+    train_peak = train_peak_bytes(layer, xs[0], gs[0], dev)
+    fwd_peak = eval_peak_bytes(layer, xs[0].detach(), dev)
+    layer.train()
 
     # ---- graph capture: one graph per resident batch, one step per graph
     side = torch.cuda.Stream(dev)
@@ -940,64 +1095,66 @@ def bench_c2(args, dev) -> dict:
                 layer(xs[k]).backward(gs[k])
         return gph
 
-    def replay_rate(graphs: list, steps_per_graph: int, steps: int, tail: list | None = None) -> float:
-        """us per step over exactly `steps` steps (steps // steps_per_graph
-        replays of `graphs`, then steps % steps_per_graph one-step replays of
-        `tail`), after >= 0.3 s (and >= --warmup replays) of warmup: the GPU
-        clocks ramp up under sustained load."""
-        torch.cuda.synchronize()
-        t0, w = time.perf_counter(), 0
-        while w < args.warmup or time.perf_counter() - t0 < 0.3:
-            graphs[w % len(graphs)].replay()
-            w += 1
-        torch.cuda.synchronize()
-        n, rest = divmod(steps, steps_per_graph)
-        t0 = time.perf_counter()
-        for k in range(n):
-            graphs[k % len(graphs)].replay()
-        for k in range(rest):
-            tail[k % len(tail)].replay()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) * 1e6 / steps
+    def replay_window(graphs: list, steps_per_graph: int, tail: list | None = None):
+        """One window of exactly --steps steps: steps // steps_per_graph
+        replays of `graphs` round robin, then steps % steps_per_graph
+        one-step replays of `tail`."""
+        n, rest = divmod(args.steps, steps_per_graph)
+        ctr = [0]
+
+        def window() -> None:
+            for _ in range(n):
+                graphs[ctr[0] % len(graphs)].replay()
+                ctr[0] += 1
+            for k in range(rest):
+                tail[k % len(tail)].replay()
+
+        return window
 
     graphs = [capture([k]) for k in range(nb)]
-    graph1_us = replay_rate(graphs, 1, max(args.steps, 200))
-    log(f"graph {graph1_us:.1f} us/step (one step per graph)")
+    t1 = time_windows(replay_window(graphs, 1), args.steps, args.warmup)
+    graph1_us = t1["us_per_step"]
+    log(f"graph {graph1_us:.1f} us/step (one step per graph; median of {t1['windows']} windows of {args.steps}, "
+        f"{t1['min']:.1f}-{t1['max']:.1f})")
     graphs4 = [capture([(j + i) % nb for i in range(4)]) for j in range(nb)]
-    graph_us = replay_rate(graphs4, 4, args.steps, tail=graphs)
+    t4 = time_windows(replay_window(graphs4, 4, tail=graphs), args.steps, args.warmup)
+    graph_us = t4["us_per_step"]
     graph_ms = graph_us * 1e-3
-    log(f"graph {graph_us:.1f} us/step (four steps per graph)")
+    log(f"graph {graph_us:.1f} us/step (four steps per graph; median of {t4['windows']} windows of {args.steps}, "
+        f"{t4['min']:.1f}-{t4['max']:.1f}, wall mean {t4['wall_mean']:.1f})")
+    # the same step with the reference shell's route debug tensors (int64
+    # indices and f32 margins written by every call, layers/base.py:78-83)
+    layer.cache_route_debug = True
+    graphs_dbg = [capture([(j + i) % nb for i in range(4)]) for j in range(nb)]
+    td = time_windows(replay_window(graphs_dbg, 4, tail=graphs_dbg), args.steps, args.warmup)
+    layer.cache_route_debug = False
+    del graphs_dbg
+    log(f"graph {td['us_per_step']:.1f} us/step with cache_route_debug=True")
 
     # ---- eager steps back to back: the host-bound rate of plain autograd
     # steps (the reference harness's loop), then per-kernel durations over
     # eager steps whose kernels stamp armed events
-    esteps = max(args.steps, 200)
-    for w in range(nb):
-        step(w)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(esteps):
-        step(k % nb)
-    torch.cuda.synchronize()
-    eager_us = (time.perf_counter() - t0) * 1e6 / esteps
+    ctr = [0]
+
+    def eager_window() -> None:
+        for _ in range(args.steps):
+            step(ctr[0] % nb)
+            ctr[0] += 1
+
+    te = time_windows(eager_window, args.steps, args.warmup)
+    eager_us = te["us_per_step"]
     log(f"eager {eager_us:.1f} us/step")
     # the same steps with torch's calling-thread autograd engine: the default
     # engine hands every backward to its device thread and back
     with torch.autograd.set_multithreading_enabled(False):
-        for w in range(nb):
-            step(w)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for k in range(esteps):
-            step(k % nb)
-        torch.cuda.synchronize()
-        eager_ct_us = (time.perf_counter() - t0) * 1e6 / esteps
+        tc = time_windows(eager_window, args.steps, args.warmup)
+    eager_ct_us = tc["us_per_step"]
     log(f"eager {eager_ct_us:.1f} us/step (torch.autograd.set_multithreading_enabled(False))")
     fused = fused_backward()
     algo = algorithmic_bytes(fused)
     comp = compulsory_bytes(fused)
     names = tuple(algo)
-    ksteps = min(max(args.steps, 100), 200)
+    ksteps = 200
     evs = _kernel_events(names, ksteps)
     torch.cuda.synchronize()
     for k in range(ksteps):
@@ -1005,27 +1162,29 @@ def bench_c2(args, dev) -> dict:
             arm_kernel_events(n, *evs[n][k])
         step(k % nb)
     torch.cuda.synchronize()
-    kern_us = {n: 1e3 * sum(e0.elapsed_time(e1) for e0, e1 in evs[n]) / ksteps for n in names}
-    log("kernels (us): " + ", ".join(f"{n}={v:.2f}" for n, v in kern_us.items()))
+    spread = {n: _spread([1e3 * e0.elapsed_time(e1) for e0, e1 in evs[n]]) for n in names}
+    kern_us = {n: spread[n]["mean"] for n in names}
+    log("kernels (us, mean): " + ", ".join(f"{n}={v:.2f}" for n, v in kern_us.items()))
 
     dom = max(names, key=lambda n: kern_us[n])
     traffic = {n: measured_traffic(n) for n in names}
     kernels = {
-        n: {"avg_us": round(kern_us[n], 3), "algorithmic_bytes": algo[n], "compulsory_bytes": comp[n],
+        n: {"avg_us": round(kern_us[n], 3), "median_us": round(spread[n]["median"], 3),
+            "min_us": round(spread[n]["min"], 3), "max_us": round(spread[n]["max"], 3),
+            "algorithmic_bytes": algo[n], "compulsory_bytes": comp[n],
             "hbm_traffic_bytes": traffic[n], "l2_hit_rate": l2_hit_rate(n),
-            "hbm_frac": round(traffic[n] / (kern_us[n] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if traffic[n] else None,
-            "algorithmic_GBs": round(algo[n] / (kern_us[n] * 1e-6) / 1e9, 1)}
+            "hbm_frac": round(traffic[n] / (kern_us[n] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if traffic[n] else None}
         for n in names
     }
 
     cpu = None
-    cpus = []
+    zig = None
     if args.cpu_budget > 0:
         log("timing the CPU baselines")
         cpu = cpu_torch_train(I, O, T, C, B, args.cpu_budget, "c2")
-        cpus = [cpu, cpu_zig_eval(I, O, T, C, B, "f32", min(args.cpu_budget, 3.0), "c2 (forward only: the zig path has no backward)")]
+        zig = cpu_zig_eval(I, O, T, C, B, "f32", min(args.cpu_budget, 3.0), "c2 (forward only: the zig path has no backward)")
         log(f"cpu baseline {cpu['value']:.0f} samples/s on {cpu['cores']} cores; zig-equivalent forward "
-            f"{cpus[1]['ms_per_call']:.3f} ms/call")
+            f"{zig['ms_per_call']:.3f} ms/call")
 
     value = B / (graph_ms * 1e-3)
     total_algo = sum(algo.values())
@@ -1052,18 +1211,22 @@ def bench_c2(args, dev) -> dict:
             "tables": T,
             "comparisons": C,
             "lut_dtype": "f32",
-            "mode": "hip-graph replay of the module fwd+bwd, four steps (one per resident batch) per graph",
+            "mode": "hip-graph replay of the module fwd+bwd, four steps (one per resident batch) per graph, "
+            "cache_route_debug=False; ms_per_step = median over back-to-back windows of --steps steps",
         },
+        **window_fields(t4),
+        "us_per_step_route_debug": round(td["us_per_step"], 3),
         "roofline": roofline(dom, kern_us[dom], algo[dom], comp[dom], "c2"),
         "cpu_baseline": cpu,
-        "cpu_baselines": cpus,
+        "cpu_zig_forward_ms": zig["ms_per_call"] if zig else None,
+        "peak_bytes": {"forward": fwd_peak, "train_step": train_peak,
+                       "backward_workspace": backward_workspace_bytes(B, I, O, T, C, False)},
         "step": {
             "hbm_traffic_bytes": step_traffic,
             "hbm_frac": round(step_traffic / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if step_traffic else None,
             "compulsory_bytes": sum(comp.values()),
             "compulsory_frac": round(sum(comp.values()) / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "algorithmic_bytes": total_algo,
-            "algorithmic_GBs": round(total_algo / (graph_ms * 1e-3) / 1e9, 1),
             "algorithmic_frac": round(total_algo / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         },
         "us_per_step_one_step_per_graph": round(graph1_us, 3),
@@ -1072,8 +1235,105 @@ def bench_c2(args, dev) -> dict:
         "kernels": kernels,
     }
     if cpu:
+        cpu["sample"] = cpu["sample"].split(", oracle/")[0] + ", oracle/pairwise_torch.py"
         out["speedup_vs_cpu"] = round(value / cpu["value"], 1)
         out["eager_speedup_vs_cpu"] = round(B / (eager_us * 1e-6) / cpu["value"], 1)
+    return out
+
+
+def _cpu_us(cpus: list, path_prefix: str) -> float | None:
+    for c in cpus or []:
+        if c and c["path"].startswith(path_prefix):
+            return round(c["ms_per_call"] * 1e3, 2)
+    return None
+
+
+def compact_c1(r: dict) -> dict:
+    return {
+        "us_per_call": r["value"], "graph_us_per_call": r["graph_us_per_call"],
+        "sync_latency_us": r["sync_latency_us"], "kernel_us": r["kernel_us"],
+        "frac": r["roofline"]["frac"], "l2_hit_rate": r["roofline"]["l2_hit_rate"],
+        "cpu_zig_us": _cpu_us(r["cpu_baselines"], "Zig"), "cpu_torch_us": _cpu_us(r["cpu_baselines"], "torch"),
+        "forward_peak_bytes": r["peak_bytes"]["forward"], "windows": r["windows"],
+    }
+
+
+def compact_c3(r: dict) -> dict:
+    out = {}
+    for b, res in r["per_batch"].items():
+        cpus = res.get("cpu_baselines")
+        out[f"b{b}"] = {
+            "us_per_call": res["us_per_call"], "mode": res["mode"], "kernel_us": res["kernel_us"],
+            "samples_per_s": res["samples_per_s"], "cpu_zig_us": _cpu_us(cpus, "Zig"),
+            "cpu_torch_us": _cpu_us(cpus, "torch"), "forward_peak_bytes": res["forward_peak_bytes"],
+        }
+    out["b8192"]["frac"] = r["roofline"]["frac"]
+    out["b8192"]["l2_hit_rate"] = r["roofline"]["l2_hit_rate"]
+    return out
+
+
+def compact_c4(r: dict) -> dict:
+    cpu = r.get("cpu_baseline")
+    rf = r["roofline"]
+    return {
+        "ms_per_step": round(r["ms_per_step"], 4), "samples_per_s": r["value"], "windows": r["windows"],
+        "kernel": rf["kernel"], "kernel_ms": round(rf["avg_us"] * 1e-3, 4), "frac": rf["frac"],
+        "l2_hit_rate": rf["l2_hit_rate"], "step_hbm_frac": r["step"]["hbm_frac"],
+        "step_compulsory_frac": r["step"]["compulsory_frac"],
+        "kernel_ms_all": {n: round(k["avg_us"] * 1e-3, 4) for n, k in r["kernels"].items()},
+        "cpu_torch_ms_per_step_batch8": cpu["ms_per_call"] if cpu else None,
+        "speedup_per_sample": r.get("speedup_vs_cpu"),
+        "train_peak_bytes": r["peak_bytes"]["train_step"], "workspace_bytes": r["peak_bytes"]["backward_workspace"],
+    }
+
+
+def compact_c5(r: dict) -> dict:
+    cpu = r.get("cpu_baseline")
+    curve = r.get("loss_curve") or {}
+    return {
+        "us_per_step": round(r["ms_per_step"] * 1e3, 3), "samples_per_s": r["value"], "windows": r["windows"],
+        "window_min_us": r["window_min_us"], "window_max_us": r["window_max_us"],
+        "cpu_torch_ms_per_step": round(512 / cpu["value"] * 1e3, 3) if cpu else None,
+        "speedup_vs_cpu": r.get("speedup_vs_cpu"),
+        "curve_steps": curve.get("steps"),
+        "first_step_codes_differ": curve.get("first_step_codes_differ"),
+        "max_rel_loss_diff_while_codes_equal": curve.get("max_rel_loss_diff_while_codes_equal"),
+        "loss_first_last": [curve["hip"][0], curve["hip"][-1]] if curve.get("hip") else None,
+        "train_peak_bytes": r["peak_bytes"]["train_step"],
+    }
+
+
+def other_configs(args, dev) -> dict:
+    """Compact records of the other four BASELINE.json configs, measured in
+    the same run on the same device after the headline: c1 (latency), c3 at
+    batch 1 / 64 / 8192, c4 fwd+bwd and the c5 training step with its loss
+    curve. Each runs its --workload function at fewer steps and shorter CPU
+    samples (c4's torch-CPU leg at batch 8, >= 3 steps); the full records
+    come from `--workload cN`. A workload that raises is recorded as its
+    error, so the headline line is still printed."""
+    import gc
+
+    import torch
+
+    plan = (
+        ("c1", bench_c1, compact_c1, {"steps": 20, "warmup": 5, "cpu_budget": min(args.cpu_budget, 1.5)}),
+        ("c3", bench_c3, compact_c3, {"steps": 20, "warmup": 5, "cpu_budget": min(args.cpu_budget, 1.0)}),
+        ("c4", bench_c4, compact_c4, {"steps": 4, "warmup": 2, "cpu_budget": min(args.cpu_budget, 1.0)}),
+        ("c5", bench_c5, compact_c5, {"steps": 20, "warmup": 5, "cpu_budget": min(args.cpu_budget, 3.0),
+                                      "curve_steps": 100}),
+    )
+    out = {"host_cores": host_threads()}
+    for name, fn, compact, over in plan:
+        sub = argparse.Namespace(**{**vars(args), **over})
+        t0 = time.perf_counter()
+        log(f"other config {name}")
+        try:
+            out[name] = compact(fn(sub, dev))
+        except Exception as exc:  # noqa: BLE001 -- recorded, the headline line still prints
+            out[name] = {"error": f"{type(exc).__name__}: {exc}"[:300]}
+        out[name]["bench_s"] = round(time.perf_counter() - t0, 1)
+        gc.collect()
+        torch.cuda.empty_cache()
     return out
 
 
@@ -1092,6 +1352,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=None, help="warmup steps (default 50; 3 for c4)")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work (0 = skip)")
     ap.add_argument("--curve-steps", type=int, default=100, help="c5: steps of the loss curve (0 = skip)")
+    ap.add_argument(
+        "--other-configs",
+        choices=("on", "off"),
+        default="on",
+        help="with the default c2 workload, also measure c1, c3, c4 and c5 in the same run and add their "
+        "compact records under other_configs (off: the c2 line alone)",
+    )
     ap.add_argument(
         "--calibrate-copy-bytes",
         type=int,
@@ -1124,9 +1391,11 @@ def main() -> int:
     log(f"device {torch.cuda.get_device_name(dev)}, library {library_path()}, host cores {host_threads()}")
     runner = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.workload]
     out = runner(args, dev)
+    if args.workload == "c2" and args.other_configs == "on":
+        out["other_configs"] = other_configs(args, dev)
     if args.calibrate_copy_bytes > 0:
         calibration_copy(args.calibrate_copy_bytes, dev)
-    print(json.dumps(out))
+    print(json.dumps(out, separators=(",", ":")))
     return 0
 
 

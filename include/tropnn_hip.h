@@ -191,6 +191,11 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
  * on one GPU shares that GPU's buffer: calls that overlap on one GPU (other
  * streams, other threads, without ordering between them) race on it and give
  * wrong gradients; serialise them. The buffer needs no clearing between calls.
+ * The first call on a GPU looks up that GPU's buffer address (a runtime call,
+ * not stream work), so it must not be under stream capture: it fails with
+ * TROPNN_ERR_UNSUPPORTED if it is. Once one call on the GPU has run outside
+ * capture, calls under capture record only kernel launches (no memset, no
+ * allocation) and replay correctly.
  */
 #define TROPNN_NOALLOC_WORKSPACE_BYTES (32u << 20)
 int tropnn_hip_pairwise_backward_noalloc(int64_t items, int64_t in_features, int64_t out_features, int64_t tables,

@@ -432,6 +432,41 @@ def test_ties_zero_margins_and_duplicate_anchors():
     assert_train_parity(ref, hip, *train_step(ref, hip, x, g))
 
 
+@pytest.mark.parametrize(
+    "i,o,t,c,b,min_margin,surrogate",
+    [
+        (128, 128, 136, 6, 512, True, "izhikevich"),  # fused backward (c2's shape)
+        (784, 128, 136, 6, 512, True, "izhikevich"),  # fused backward (c5's first layer)
+        (128, 10, 136, 6, 512, True, "izhikevich"),  # fused backward, 2 columns per lane (c5's last layer)
+        (40, 34, 33, 4, 70, True, "izhikevich"),  # general backward (O % 4 != 0, O > 32)
+        (48, 320, 20, 6, 700, True, "izhikevich"),  # general backward, 64-column chunks
+        (64, 24, 17, 6, 2053, True, "izhikevich"),  # multi-item forward, 3 sort tiles
+        (128, 128, 136, 6, 256, False, "izhikevich"),  # full STE
+        (64, 96, 20, 8, 50, False, "izhikevich"),
+        (128, 128, 136, 6, 256, False, "fast_sigmoid_odd"),
+        (48, 24, 17, 6, 2053, False, "fast_sigmoid_odd"),
+    ],
+)
+def test_sparse_inputs_exact_zero_margins(i, o, t, c, b, min_margin, surrogate):
+    """Sparse inputs as c5's (x = rand * (rand >= 0.8)) with zero thresholds
+    give many margins of exactly 0: the surrogate's u = 0 branch, +0.5 for
+    izhikevich (where(u > 0, -1, +1) takes +1, layers/surrogate.py:9-13) and
+    0 for fast_sigmoid_odd, plus |m| ties resolved to the first comparison,
+    on every backward path, against the oracle at the f32 bars."""
+    ref, hip = make_pair(i, o, t, c, seed=i + t + b, use_min_margin_ste=min_margin, surrogate=surrogate)
+    gen = torch.Generator().manual_seed(b)
+    x = torch.rand(b, i, generator=gen) * (torch.rand(b, i, generator=gen) >= 0.8)
+    g = seeded((b, 1, o), seed=b + 3)
+    yx_ref, yx_hip = train_step(ref, hip, x, g)
+    margins = ref._last_margins.reshape(b, t, c)
+    zero = margins == 0
+    if min_margin:  # the selected comparison has margin 0 wherever any does
+        assert zero.any(-1).float().mean() > 0.3
+    else:
+        assert zero.float().mean() > 0.3
+    assert_train_parity(ref, hip, yx_ref, yx_hip)
+
+
 def test_f16_lut_training():
     """f16 LUT reads in training: forward and gradients within 1e-3 of the f32 oracle."""
     ref, hip = make_pair(128, 128, 136, 6, seed=0, lut_dtype="f16", thr_std=0.1)

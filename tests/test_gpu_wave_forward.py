@@ -107,3 +107,46 @@ def test_wave_forward_training(i, o, t, c, b, min_margin, surrogate):
     g = seeded((b, 1, o), seed=14)
     yx_ref, yx_hip = train_step(ref, hip, x, g)
     assert_train_parity(ref, hip, yx_ref, yx_hip)
+
+
+@pytest.mark.parametrize("lut_dtype,o,lut_off,out_off", [("f16", 64, 1, 1), ("f32", 128, 2, 2), ("f16", 128, 4, 0)])
+def test_wave_shapes_with_lut_or_output_off_16_bytes(lut_dtype, o, lut_off, out_off):
+    """A LUT or output that starts off a 16-byte boundary (views with a
+    storage offset, aligned to the element vector the other kernels load)
+    takes the multi-item kernel instead of the wave-item kernel, whose loads
+    and stores move whole 16-byte pieces: the output equals the aligned
+    call's bit for bit (both kernels sum the one-item kernel's 16-table
+    blocks in order), and the aligned call is within the bar of the oracle."""
+    from tropnn_amd.backends.pairwise_hip import _check, load_library
+
+    i, t, c, b = 128, 136, 6, 8200
+    ref, hip = make_pair(i, o, t, c, seed=4, thr_std=0.3, lut_dtype=lut_dtype)
+    dt = torch.float16 if lut_dtype == "f16" else torch.float32
+    x = seeded((b, i), seed=3)
+    xd = x.to(DEV)
+    lut = hip.lut.detach().to(dt).contiguous()
+    anchors = hip.anchors.contiguous()
+    thr = hip.thresholds.detach().contiguous()
+    lib = load_library()
+    fn = lib.tropnn_hip_lut_forward_batch_f16 if lut_dtype == "f16" else lib.tropnn_hip_lut_forward_batch_f32
+    stream = torch.cuda.current_stream(DEV).cuda_stream
+
+    def call(lut_view, out_view):
+        rc = fn(b, t, c, i, o, lut_view.data_ptr(), anchors.data_ptr(), thr.data_ptr(), xd.data_ptr(),
+                out_view.data_ptr(), 1.0, stream)
+        _check(rc, fn.__name__)
+
+    aligned = torch.full((b, o), float("nan"), device=DEV)
+    call(lut, aligned)
+    lbuf = torch.empty(lut.numel() + lut_off, dtype=dt, device=DEV)
+    lut_v = lbuf[lut_off:].view(lut.shape)
+    lut_v.copy_(lut)
+    obuf = torch.full((b * o + out_off,), float("nan"), device=DEV)
+    out_v = obuf[out_off:].view(b, o)
+    assert (lut_v.data_ptr() % 16 != 0) or (out_v.data_ptr() % 16 != 0)
+    call(lut_v, out_v)
+    torch.cuda.synchronize()
+    assert torch.equal(out_v, aligned)
+    with torch.no_grad():
+        y_ref = ref.eval()(x).reshape(b, o) / ref.output_scale
+    assert rel_err(aligned, y_ref) <= (F16_TOL if lut_dtype == "f16" else F32_TOL)

@@ -17,6 +17,7 @@ What fixes each value, independently of the oracle's vectorised code:
 from __future__ import annotations
 
 import hashlib
+import math
 import json
 from pathlib import Path
 
@@ -238,3 +239,67 @@ def test_zero_margin_and_duplicate_anchor_give_no_input_gradient():
     assert margins[0, 0, 0].tolist() == [1.0, 0.2]
     out.sum().backward()
     assert x2.grad[0, 0, 2] == 0 and torch.count_nonzero(x2.grad) == 0
+
+
+def test_surrogates_at_zero():
+    """The reference's surrogates at u = 0 (layers/surrogate.py:9-17).
+    izhikevich takes the +1 branch of where(u > 0, -1, +1) at u = 0 (and at
+    -0.0, which is not > 0), so izhikevich(0) = 2 sigmoid(0) (1 - sigmoid(0))
+    = +0.5, while its limit from above is -0.5; fast_sigmoid_odd has
+    sign(0) = 0, so 0. A sign(u) slip in izhikevich gives 0 at u = 0 and
+    fails here; a > / >= slip gives -0.5 and fails here."""
+    u = torch.tensor([0.0, -0.0], dtype=torch.float32)
+    assert orc.surrogate_gradient(u, "izhikevich").tolist() == [0.5, 0.5]
+    fso = orc.surrogate_gradient(u, "fast_sigmoid_odd")
+    assert fso.tolist() == [0.0, 0.0]
+    eps = torch.tensor([1e-30, -1e-30], dtype=torch.float32)  # either side of the kink
+    assert orc.surrogate_gradient(eps, "izhikevich").tolist() == [-0.5, 0.5]
+    assert orc.surrogate_gradient(eps, "fast_sigmoid_odd").tolist() == [-0.5, 0.5]
+
+
+def _sigma_prime(u: float, surrogate: str) -> float:
+    """The surrogate derivative from its formula, in float64: fast_sigmoid_odd
+    -0.5 sign(u) / (1 + |u|)^2; izhikevich s' 2 s (1 - s), s = 1 / (1 +
+    exp(-|u|)), s' = -1 for u > 0 else +1."""
+    if surrogate == "fast_sigmoid_odd":
+        sgn = (u > 0) - (u < 0)
+        return -0.5 * sgn / (1.0 + abs(u)) ** 2
+    s = 1.0 / (1.0 + math.exp(-abs(u)))
+    return (-1.0 if u > 0 else 1.0) * 2.0 * s * (1.0 - s)
+
+
+@pytest.mark.parametrize("surrogate,sigma0", [("izhikevich", 0.5), ("fast_sigmoid_odd", 0.0)])
+@pytest.mark.parametrize("full", [False, True])
+def test_exact_zero_margin_gradient_closed_form(surrogate, sigma0, full):
+    """One item, one table, C = 2 with disjoint anchors (0, 1) and (2, 3),
+    thresholds 0, x = [0.7, 0.7, 2.0, 0.5]: m0 = 0 exactly, m1 = 1.5, code
+    = 0b10 = 2. With D_c = G . (L[code ^ 2^c] - L[code]) and
+    gu_c = D_c sigma'(m_c), the STE gives x.grad[a_c] += gu_c,
+    x.grad[b_c] -= gu_c, thr.grad[c] = -gu_c (layers/pairwise.py:137-200
+    through autograd), and lut.grad[code] = G. The min-margin STE selects
+    c = 0 (|m0| = 0 is the smallest), so only gu_0 = D_0 sigma'(0) flows:
+    0.5 D_0 for izhikevich, 0 for fast_sigmoid_odd; the full STE adds gu_1."""
+    anchors = torch.tensor([[[0, 1], [2, 3]]])
+    thr = torch.zeros(1, 2, dtype=torch.float64, requires_grad=True)
+    lut_vals = np.array([[[1.0, -2.0, 0.5], [0.25, 3.0, -1.0], [-0.5, 1.5, 2.0], [4.0, -0.75, 1.25]]])
+    lut = torch.tensor(lut_vals, requires_grad=True)
+    x = torch.tensor([[[0.7, 0.7, 2.0, 0.5]]], dtype=torch.float64, requires_grad=True)
+    g = np.array([0.3, -1.1, 0.8])
+    out, idx, margins = orc.route_output(x, anchors, thr, lut, training=True, use_min_margin_ste=not full,
+                                         surrogate=surrogate)
+    assert margins[0, 0, 0].tolist() == [0.0, 1.5] and int(idx[0, 0, 0]) == 2
+    out.backward(torch.tensor(g).view(1, 1, 3))
+    d0 = float(g @ (lut_vals[0, 3] - lut_vals[0, 2]))
+    d1 = float(g @ (lut_vals[0, 0] - lut_vals[0, 2]))
+    gu0 = d0 * sigma0
+    assert _sigma_prime(0.0, surrogate) == sigma0
+    gu1 = d1 * _sigma_prime(1.5, surrogate) if full else 0.0
+    want_x = np.array([gu0, -gu0, gu1, -gu1])
+    # the reference runs the STE branch in float32 (layers/pairwise.py:145, 148)
+    np.testing.assert_allclose(x.grad.view(-1).numpy(), want_x, rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(thr.grad.view(-1).numpy(), [-gu0, -gu1], rtol=1e-6, atol=1e-7)
+    want_lut = np.zeros_like(lut_vals)
+    want_lut[0, 2] = g
+    np.testing.assert_allclose(lut.grad.numpy(), want_lut, rtol=0, atol=0)
+    if surrogate == "izhikevich":
+        assert gu0 != 0.0  # the u = 0 branch carries a gradient

@@ -100,3 +100,86 @@ def test_noalloc_rejects_a_workspace_over_its_buffer():
                                                   torch.cuda.current_stream(DEV).cuda_stream)
     assert rc == 2
     assert b"allocation-free" in lib.tropnn_hip_last_error()
+
+
+def _noalloc_args(dims, g, lut, rec, margins, offsets, entries, ste_mode, outs):
+    items, i, o, t, c = dims
+    lut_dtype = ph.LUT_F16 if lut.dtype == torch.float16 else ph.LUT_F32
+    gx, gthr, glut = outs
+    return (items, i, o, t, c, g.data_ptr(), lut.data_ptr(), lut_dtype, rec.data_ptr(),
+            None if margins is None else margins.data_ptr(), offsets.data_ptr(), entries.data_ptr(), 0.125,
+            ste_mode, ph.SURROGATE_IDS["fast_sigmoid_odd"], gx.data_ptr(), gthr.data_ptr(), glut.data_ptr())
+
+
+def test_noalloc_backward_replayed_from_a_graph():
+    """The allocation-free backward captured in a HIP graph (after one call
+    on the device outside capture) and replayed three times, with eager work
+    and synchronisation between the replays: before each replay the upstream
+    gradient is rewritten in place and the outputs are filled with NaN; each
+    replay must equal the workspace entry point run eagerly on the same
+    inputs, bit for bit."""
+    i, o, t, c, items = 128, 128, 136, 6, 512
+    dims = (items, i, o, t, c)
+    g, lut, rec, margins, offsets, entries = _inputs(items, i, o, t, c, "f32", False, seed=5)
+    lib = ph.load_library()
+    _backward(True, dims, g, lut, rec, margins, offsets, entries, ph.STE_MIN_MARGIN)  # outside capture first
+    outs = tuple(torch.empty(s, device=DEV) for s in ((items, i), (t, c), (t, 1 << c, o)))
+    args = _noalloc_args(dims, g, lut, rec, margins, offsets, entries, ph.STE_MIN_MARGIN, outs)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.tropnn_hip_pairwise_backward_noalloc(*args, torch.cuda.current_stream(DEV).cuda_stream)
+    ph._check(rc, "noalloc under capture")
+    gen = torch.Generator().manual_seed(9)
+    for replay in range(3):
+        g.copy_(torch.randn(g.shape, generator=gen).to(DEV))
+        for out in outs:
+            out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        print(f"[noalloc graph] replay {replay}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = _backward(False, dims, g, lut, rec, margins, offsets, entries, ph.STE_MIN_MARGIN)
+        for name, a, b in zip(("grad_latent", "grad_thresholds", "grad_lut"), outs, ref):
+            assert torch.equal(a, b), f"replay {replay}: {name} differs, max {float((a - b).abs().max()):.3e}"
+
+
+_FIRST_CALL_UNDER_CAPTURE = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+import torch
+import tests.test_zz_no_alloc as t
+ph = t.ph
+items, i, o, k, c = 64, 32, 16, 8, 4
+inputs = t._inputs(items, i, o, k, c, "f32", False, seed=1)
+outs = tuple(torch.empty(s, device=t.DEV) for s in ((items, i), (k, c), (k, 1 << c, o)))
+args = t._noalloc_args((items, i, o, k, c), *inputs, ph.STE_MIN_MARGIN, outs)
+lib = ph.load_library()
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    rc = lib.tropnn_hip_pairwise_backward_noalloc(*args, torch.cuda.current_stream(t.DEV).cuda_stream)
+    msg = lib.tropnn_hip_last_error()
+assert rc == 2, rc
+assert b"under stream capture" in msg, msg
+rc = lib.tropnn_hip_pairwise_backward_noalloc(*args, torch.cuda.current_stream(t.DEV).cuda_stream)
+assert rc == 0, lib.tropnn_hip_last_error()
+torch.cuda.synchronize()
+print("first call under capture refused; the next call outside capture ran")
+"""
+
+
+def test_noalloc_first_call_under_capture_is_refused():
+    """In a fresh process the first allocation-free backward on the device,
+    made under stream capture, fails with TROPNN_ERR_UNSUPPORTED and a clear
+    message before enqueuing anything (its buffer's address lookup is not
+    stream work); a later call outside capture runs."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parent.parent
+    proc = subprocess.run([sys.executable, "-c", _FIRST_CALL_UNDER_CAPTURE, str(root)], capture_output=True,
+                          text=True, timeout=240, cwd=str(root))
+    assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-2000:]
+    assert "refused" in proc.stdout

@@ -115,6 +115,17 @@ int scratch_for_stream(hipStream_t stream, void **out) {
                     kMaxDevices - 1);
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (g_scratch_ptr[dev] == nullptr) {
+        // the lookup is a runtime call of its own, not stream work: it is
+        // made outside any capture, so a first call under capture is refused
+        if (stream != nullptr) {
+            hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+            if ((e = hipStreamIsCapturing(stream, &st)) != hipSuccess) return hip_fail("hipStreamIsCapturing", e);
+            if (st != hipStreamCaptureStatusNone)
+                return fail(TROPNN_ERR_UNSUPPORTED,
+                            "the first allocation-free backward on device %d is under stream capture; make one call "
+                            "on that device outside capture first (it looks up the device buffer's address)",
+                            dev);
+        }
         int cur = 0;
         if ((e = hipGetDevice(&cur)) != hipSuccess) return hip_fail("hipGetDevice", e);
         if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return hip_fail("hipSetDevice", e);
@@ -216,15 +227,14 @@ int tropnn_hip_pairwise_forward(int64_t items, int64_t in_features, int64_t out_
                                 uint8_t *codes, tropnn_stream_t stream) {
     tropnn::Dims d{};
     if (int rc = make_dims(items, in_features, out_features, tables, comparisons, lut_dtype, d)) return rc;
-    const tropnn::ForwardPlan p = tropnn::plan_forward(d);
+    // a LUT or output off a 16-byte boundary (a view with a storage offset)
+    // takes a kernel whose loads need only the element-vector alignment
+    const tropnn::ForwardPlan p = tropnn::plan_forward(d, !misaligned(lut, 16) && !misaligned(output, 16));
     if (int rc = check_forward_ptrs(d, p, latent, anchors, thresholds, lut, output)) return rc;
     if (d.items == 0) return ok();
     if ((route_record && misaligned(route_record, 8)) || (indices && misaligned(indices, 8)) ||
         (margins && misaligned(margins, 4)))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "route_record, indices and margins must be aligned to their element size");
-    if (route_record && p.stream_ok && (misaligned(lut, 16) || misaligned(output, 16)))
-        return fail(TROPNN_ERR_INVALID_ARGUMENT, "the streamed training forward reads the LUT and writes the output "
-                                                 "in 16-byte pieces: both must be 16-byte aligned");
     if (p.lds_bytes > 64 * 1024)
         return fail(TROPNN_ERR_UNSUPPORTED, "forward needs %d bytes of LDS (tables too large)", p.lds_bytes);
     // the gather addresses the LUT through one buffer resource with 32-bit offsets

@@ -88,6 +88,14 @@ constexpr int rows_batch(int vec) { return vec == 8 ? 4 : kRowsBatch; }
 // workgroup needs under 80 KB and two share a CU: one's staging and combine
 // overlap the other's walk. Otherwise 1024.
 constexpr int rows_threads(bool dots, int lut_esize) { return dots && lut_esize == 2 ? 512 : kRowsThreads; }
+// Whether the row kernel with nb packed in its slot offsets forms the
+// neighbour row's LDS address with one byte permute: the LUT chunk held in
+// LDS (f32 in 1024-thread workgroups, else f16) has rows of 256 bytes. The
+// permute yields the address relative to the chunk, so the chunk must sit at
+// LDS address 0; launch_rows_vs checks that on the host.
+constexpr bool rows_nb_perm(bool dots, int lut_esize, int s, int v) {
+    return dots && s * v * (rows_threads(dots, lut_esize) == kRowsThreads ? 4 : 2) == 256;
+}
 constexpr int kRowsChunk = 64;     // columns of a row-kernel workgroup (at most): 2 MB of G at c4, within an L2
 constexpr uint32_t kSlotPad = 0x80000000u;  // grad-row offset of a padding slot: past any grad buffer (<= 2 GiB)
 constexpr int kEntries = 16;       // index entries a walker reads per batch
@@ -592,7 +600,8 @@ __global__ __launch_bounds__(rows_threads(DOTS, sizeof(T))) void pairwise_bwd_ro
     // the neighbour row's LDS address from one byte permute: the LUT chunk at
     // LDS offset 0 with 256-byte rows, nb (< 256) in the slot offset's low
     // byte, the lane's column offset (< 256) in the address's low byte
-    constexpr bool kNbPerm = NBP && P * sizeof(LT) == 256;
+    constexpr bool kNbPerm = NBP && rows_nb_perm(DOTS, sizeof(T), S, V);
+    static_assert(!kNbPerm || P * sizeof(LT) == 256, "byte-permute addressing needs 256-byte LDS rows");
     extern __shared__ __align__(16) unsigned char lds[];
     int *rs = reinterpret_cast<int *>(lds + a.rs_off);            // [R + 1] row starts (slots)
     float *part = reinterpret_cast<float *>(lds + a.part_off);    // [groups][2][P] split rows
@@ -1398,6 +1407,20 @@ hipError_t launch_rows_vs(const RowsArgs &args, const BackwardPlan &p, int table
     const int lds = DOTS ? p.rows_lds_dots_bytes : p.rows_lds_bytes;
     constexpr int threads = rows_threads(DOTS, sizeof(T));
     if (threads != (DOTS ? p.rows_dots_threads : kRowsThreads)) return hipErrorInvalidConfiguration;  // plan mismatch
+    if constexpr (rows_nb_perm(DOTS, sizeof(T), S, V)) {
+        // the byte-permute neighbour reads address the LUT chunk from LDS
+        // address 0: the kernel must have no static LDS (the dynamic array
+        // then starts at 0) and the chunk must open the dynamic array
+        if (p.rows_nb_pack) {
+            static const size_t static_lds = [kernel] {
+                hipFuncAttributes at{};
+                return hipFuncGetAttributes(&at, reinterpret_cast<const void *>(kernel)) == hipSuccess
+                           ? at.sharedSizeBytes
+                           : ~size_t{0};
+            }();
+            if (static_lds != 0 || args.lut_off != 0) return hipErrorInvalidConfiguration;
+        }
+    }
     if (hipError_t e = allow_lds(kernel, lds); e != hipSuccess) return e;
     return launch_kernel(TROPNN_KERNEL_BACKWARD_TABLE, kernel, dim3(tables * p.rows_chunks), dim3(threads), lds,
                          stream, args);

@@ -942,7 +942,7 @@ int ilog2(int v) {
 
 }  // namespace
 
-ForwardPlan plan_forward(const Dims &d) {
+ForwardPlan plan_forward(const Dims &d, bool rows16) {
     ForwardPlan p{};
     const int esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
     // N elements per lane: the smallest power of two whose 64-lane tile spans
@@ -1014,15 +1014,15 @@ ForwardPlan plan_forward(const Dims &d) {
     // kWaveMinWaves waves) whose row, or 1024-byte column tile of it, is 128
     // to 1024 bytes (a power of two), tables summed in the multi-item
     // kernel's blocks of at most 16; comparators, input rows and code lists
-    // within 64 KB of LDS
+    // within 64 KB of LDS; the LUT and the output 16-byte aligned
     p.wave = false;
     {
         const int row_bytes = d.out_f * esize;
         const int tile = row_bytes <= 1024 ? row_bytes : 1024;
         const bool pow2 = (tile & (tile - 1)) == 0;
         const int ipw = tile >= 128 ? kWave / (tile / 16) : 1;
-        if (d.items >= kWaveMinItems && (d.items + ipw - 1) / ipw >= kWaveMinWaves && tile >= 128 && pow2 &&
-            row_bytes % tile == 0) {
+        if (rows16 && d.items >= kWaveMinItems && (d.items + ipw - 1) / ipw >= kWaveMinWaves && tile >= 128 &&
+            pow2 && row_bytes % tile == 0) {
             const int w16 = (d.tables + kWaveBlock - 1) / kWaveBlock;
             const int per16 = (d.tables + w16 - 1) / w16;
             const int lpr = tile / 16;
@@ -1051,10 +1051,11 @@ ForwardPlan plan_forward(const Dims &d) {
 
     // streamed gather (training only: it reads the codes from the route
     // records): large batches over a LUT far beyond the L2, rows of whole
-    // 64-column chunks, at most 256 rows per table
+    // 64-column chunks, at most 256 rows per table, the LUT and the output
+    // 16-byte aligned (LDS-direct 16-byte pieces)
     const long long lut_bytes = static_cast<long long>(d.tables) * d.rows * d.out_f * esize;
-    p.stream_ok = d.items >= kStreamMinItems && (d.out_f * esize) % kStreamChunkBytes == 0 && d.rows <= 256 &&
-                  lut_bytes >= kStreamMinLutBytes;
+    p.stream_ok = rows16 && d.items >= kStreamMinItems && (d.out_f * esize) % kStreamChunkBytes == 0 &&
+                  d.rows <= 256 && lut_bytes >= kStreamMinLutBytes;
     if (p.stream_ok) {
         p.stream_nblk = (d.items + kStreamItems - 1) / kStreamItems;
         p.stream_blocks = p.stream_nblk * (d.out_f * esize / kStreamChunkBytes);

@@ -110,7 +110,10 @@ struct BackwardPlan {
 // size and elements per lane; sized to stay within 128 VGPRs.
 constexpr int gather_chunk(int esize, int vec) { return esize == 2 && vec == 8 ? 8 : 16; }
 
-ForwardPlan plan_forward(const Dims &d);
+// rows16: the LUT and the output start on 16-byte boundaries (the wave-item
+// kernel moves whole 16-byte pieces of rows; without it the other kernels,
+// whose loads need only the plan's vec * element alignment, serve the shape)
+ForwardPlan plan_forward(const Dims &d, bool rows16 = true);
 // Tables whose two LUT rows an item-kernel wave keeps in flight, by LUT
 // element size and elements per lane: about 48 VGPRs of rows, so the kernel
 // stays within 80 VGPRs and two workgroups share a CU.
