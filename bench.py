@@ -85,7 +85,7 @@ C4_CPU_BATCH = 8
 
 
 def algorithmic_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = T, c: int = C, e: int = E,
-                      streamed: bool = False) -> dict[str, int]:
+                      streamed: bool = False, scatter: bool = False) -> dict[str, int]:
     """Per-launch algorithmic bytes (gather / embedding-bag convention: every
     (item, table) pair moves its LUT row(s) once, streamed tensors and params
     once), split by the kernel that moves them; e = LUT element bytes. Sums to
@@ -97,8 +97,10 @@ def algorithmic_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = 
     fused backward (narrow rows, c2's path):
       backward_fused: G, codes, current + neighbour rows per (item, table),
         one f32 grad-row contribution per (item, table), grad_lut once,
-        grad_thr;
-      backward_scatter: x re-read (margins), grad_x, anchors + thresholds;
+        grad_thr, and (its item role forming the input gradient in the same
+        launch) x re-read (margins), grad_x, anchors + thresholds;
+      with `scatter` (more tables than the item role takes) the last three
+        go to backward_scatter, the kernel that then forms grad_x;
     general backward (min-margin STE):
       backward_sort: nothing algorithmic (the code sort and G's chunk-major
         copy are implementation choices);
@@ -114,7 +116,9 @@ def algorithmic_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = 
     x_side = 4 * b * i + 4 * b * i + 20 * t * c
     lut_rows = 4 * b * t * o + 4 * t * r * o
     if fused:
-        return {"forward": fwd, "backward_fused": g_codes_rows + lut_rows + 4 * t * c, "backward_scatter": x_side}
+        if scatter:
+            return {"forward": fwd, "backward_fused": g_codes_rows + lut_rows + 4 * t * c, "backward_scatter": x_side}
+        return {"forward": fwd, "backward_fused": g_codes_rows + lut_rows + 4 * t * c + x_side}
     head = {"forward": fwd}
     if streamed:
         route = 4 * b * i + 20 * t * c + b * t
@@ -124,7 +128,7 @@ def algorithmic_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = 
 
 
 def compulsory_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = T, c: int = C, e: int = E,
-                     streamed: bool = False) -> dict[str, int]:
+                     streamed: bool = False, scatter: bool = False) -> dict[str, int]:
     """Per-launch compulsory bytes: each tensor a kernel must read or write,
     once, with the LUT capped at the min(B, 2^C) rows per table that items
     can touch. Each kernel counts what it must move by itself, so the LUT,
@@ -134,7 +138,7 @@ def compulsory_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = T
         takes x, anchors + thresholds and the codes, the gather the LUT and y);
       backward_fused / backward_table: G, the codes, the LUT (for the STE
         dots), grad_lut (every row, untouched rows as zeros), and for the
-        fused kernel grad_thr;
+        fused kernel grad_thr and (without `scatter`) grad_x and the anchors;
       backward_reduce: grad_thr;
       backward_scatter: grad_x and the anchors;
       backward_sort: nothing.
@@ -145,27 +149,30 @@ def compulsory_bytes(fused: bool, b: int = B, i: int = I, o: int = O, t: int = T
     grad_lut = 4 * t * r * o
     fwd = 4 * b * i + 20 * t * c + lut + 4 * b * o + b * t
     bwd_rows = 4 * b * o + b * t + lut + grad_lut
-    scatter = 4 * b * i + 16 * t * c
+    x_side = 4 * b * i + 16 * t * c
     if fused:
-        return {"forward": fwd, "backward_fused": bwd_rows + 4 * t * c, "backward_scatter": scatter}
+        if scatter:
+            return {"forward": fwd, "backward_fused": bwd_rows + 4 * t * c, "backward_scatter": x_side}
+        return {"forward": fwd, "backward_fused": bwd_rows + 4 * t * c + x_side}
     head = {"forward": fwd}
     if streamed:
         route = 4 * b * i + 20 * t * c + b * t
         head = {"forward_route": route, "forward": fwd - route}
     return {**head, "backward_sort": 0, "backward_table": bwd_rows, "backward_reduce": 4 * t * c,
-            "backward_scatter": scatter}
+            "backward_scatter": x_side}
 
 
-def fused_backward() -> bool:
-    """Whether the library runs c2's backward as the fused table kernel plus
-    the scatter kernel: its workspace then holds the 8-byte {gu, r} records
-    and at most 4 threshold partials per (table, comparison); the general
+def backward_path() -> tuple[bool, bool]:
+    """(fused, scatter): whether the library runs c2's backward as the fused
+    table kernel, and whether a scatter kernel follows it. The workspace
+    tells: none when the fused launch's item role forms the input gradient,
+    the 8-byte {gu, r} records when the scatter kernel does; the general
     path's also holds the sorted slots, a copy of G and the partial dots."""
     from tropnn_amd.backends.pairwise_hip import LUT_F32, STE_MIN_MARGIN, load_library
 
     lib = load_library()  # declares the C signatures
     ws = lib.tropnn_hip_pairwise_backward_workspace_size(B, I, O, T, C, LUT_F32, STE_MIN_MARGIN)
-    return ws <= 8 * T * B + 16 * T * C + 16
+    return ws <= 8 * T * B + 16 * T * C + 16, ws > 0
 
 
 def log(msg: str) -> None:
@@ -1150,9 +1157,9 @@ def bench_c2(args, dev) -> dict:
         tc = time_windows(eager_window, args.steps, args.warmup)
     eager_ct_us = tc["us_per_step"]
     log(f"eager {eager_ct_us:.1f} us/step (torch.autograd.set_multithreading_enabled(False))")
-    fused = fused_backward()
-    algo = algorithmic_bytes(fused)
-    comp = compulsory_bytes(fused)
+    fused, scatter = backward_path()
+    algo = algorithmic_bytes(fused, scatter=scatter)
+    comp = compulsory_bytes(fused, scatter=scatter)
     names = tuple(algo)
     ksteps = 200
     evs = _kernel_events(names, ksteps)

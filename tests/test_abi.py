@@ -60,8 +60,17 @@ def test_constants_match_header():
 
 def test_workspace_size(lib):
     ws = lib.tropnn_hip_pairwise_backward_workspace_size
-    # c2, min-margin: the fused path's {gu, r} records [T][B] x 8 bytes
-    assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_MIN_MARGIN) == 136 * 512 * 8
+    # min-margin, fused path: the scatter kernel reads {gu, r} records
+    # [T][B] x 8 bytes, unless the fused launch's item role forms the input
+    # gradient itself (no workspace): at most 192 tables and T x row bytes
+    # <= 448 (256 - T)
+    assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_MIN_MARGIN) == 136 * 512 * 8  # c2: 512-byte rows
+    assert ws(512, 128, 96, 136, 6, ph.LUT_F32, ph.STE_MIN_MARGIN) == 0  # 384-byte rows
+    assert ws(512, 128, 128, 136, 6, ph.LUT_F16, ph.STE_MIN_MARGIN) == 0  # f16: 256-byte rows
+    assert ws(512, 128, 10, 136, 6, ph.LUT_F32, ph.STE_MIN_MARGIN) == 0  # c5's last layer
+    assert ws(512, 128, 8, 192, 6, ph.LUT_F32, ph.STE_MIN_MARGIN) == 0
+    assert ws(512, 128, 8, 193, 6, ph.LUT_F32, ph.STE_MIN_MARGIN) == 193 * 512 * 8
+    assert ws(512, 128, 64, 300, 6, ph.LUT_F32, ph.STE_MIN_MARGIN) == 300 * 512 * 8
     # general path: {gu, r} [T][B] u64 (full STE: gu [T][C][B] f32), then
     # the sort kernel's slot offsets [T][slots] (slots = B + R (K - 1),
     # rounded up to whole batches of K: K = 4 when the row kernel takes 8
@@ -81,7 +90,7 @@ def test_workspace_size(lib):
 
     assert ws(64, 1024, 4096, 512, 8, ph.LUT_F16, ph.STE_MIN_MARGIN) == general(64, 4096, 512, 256, 8, 64, False)
     assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_FULL) == general(512, 128, 136, 64, 6, 64, True)
-    assert ws(33, 20, 10, 7, 3, ph.LUT_F32, ph.STE_MIN_MARGIN) == 7 * 33 * 8  # fused, 2 columns per lane
+    assert ws(33, 20, 10, 7, 3, ph.LUT_F32, ph.STE_MIN_MARGIN) == 0  # fused (item role), 2 columns per lane
     assert ws(33, 20, 34, 7, 3, ph.LUT_F32, ph.STE_MIN_MARGIN) == general(33, 34, 7, 8, 3, 64, False)
     assert ws(33, 20, 5, 7, 3, ph.LUT_F32, ph.STE_MIN_MARGIN) == general(33, 5, 7, 8, 3, 8, False)
     # 8 columns per lane below 64 columns: no (batches of 8)

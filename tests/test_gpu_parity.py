@@ -467,6 +467,49 @@ def test_sparse_inputs_exact_zero_margins(i, o, t, c, b, min_margin, surrogate):
     assert_train_parity(ref, hip, yx_ref, yx_hip)
 
 
+@pytest.mark.parametrize(
+    "i,o,t,c,b,lut_dtype",
+    [
+        (128, 10, 136, 6, 8192, "f32"),  # 69 items per item workgroup: three LDS chunks; 8 table-role tiles
+        (128, 96, 136, 6, 512, "f32"),  # 384-byte rows, the widest f32 rows the item role takes at 136 tables
+        (128, 128, 136, 6, 700, "f16"),  # f16 rows of 256 bytes
+        (64, 8, 192, 4, 300, "f32"),  # 192 tables: the most the item role takes, 64 item workgroups
+        (32, 24, 5, 3, 3, "f32"),  # 3 items: one per item workgroup
+    ],
+)
+def test_fused_item_role(i, o, t, c, b, lut_dtype):
+    """Shapes whose fused backward forms the input gradient in the fused
+    launch's item role (no scatter kernel, no workspace): every gradient
+    against the oracle, at the f32 bars on the LUT the kernels read."""
+    lib = __import__("tropnn_amd.backends.pairwise_hip", fromlist=["load_library"])
+    ws = lib.load_library().tropnn_hip_pairwise_backward_workspace_size(
+        b, i, o, t, c, lib.LUT_F16 if lut_dtype == "f16" else lib.LUT_F32, lib.STE_MIN_MARGIN)
+    assert ws == 0  # the item role's plan
+    ref, hip = make_pair(i, o, t, c, seed=i + o + t, thr_std=0.3, lut_dtype=lut_dtype)
+    if lut_dtype == "f16":
+        with torch.no_grad():
+            ref.lut.copy_(ref.lut.half().float())  # the values the kernels read
+    x = seeded((b, i), seed=b + 5)
+    g = seeded((b, 1, o), seed=b + 6)
+    assert_train_parity(ref, hip, *train_step(ref, hip, x, g))
+
+
+def test_fused_item_role_input_gradient_only():
+    """Parameters frozen, only the input gradient asked for: the fused launch
+    is item workgroups alone (no table role), and grad_latent matches the
+    oracle."""
+    ref, hip = make_pair(128, 32, 136, 6, seed=3, thr_std=0.3)
+    for p in list(ref.parameters()) + list(hip.parameters()):
+        p.requires_grad_(False)
+    x = seeded((512, 128), seed=8)
+    g = seeded((512, 1, 32), seed=9)
+    (y_ref, x_ref), (y_hip, x_hip) = train_step(ref, hip, x, g)
+    assert torch.equal(hip._last_indices.cpu(), ref._last_indices)
+    assert hip.lut.grad is None and hip.thresholds.grad is None
+    assert rel_err(x_hip.grad, x_ref.grad) <= F32_TOL
+    assert elem_err(x_hip.grad, x_ref.grad) <= ELEM_RTOL
+
+
 def test_f16_lut_training():
     """f16 LUT reads in training: forward and gradients within 1e-3 of the f32 oracle."""
     ref, hip = make_pair(128, 128, 136, 6, seed=0, lut_dtype="f16", thr_std=0.1)

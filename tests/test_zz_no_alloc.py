@@ -79,7 +79,7 @@ def test_noalloc_backward_matches_workspace_backward(i, o, t, c, lut_dtype, full
     lib = ph.load_library()
     for call, items in enumerate(sizes):
         ws_bytes = lib.tropnn_hip_pairwise_backward_workspace_size(items, i, o, t, c, 0, ste_mode)
-        assert 0 < ws_bytes <= 32 << 20
+        assert ws_bytes <= 32 << 20  # 0 for the fused path whose item role forms grad_latent
         print(f"[noalloc] call {call}: items={items} i={i} o={o} t={t} c={c} {lut_dtype} full={full}", flush=True)
         inputs = _inputs(items, i, o, t, c, lut_dtype, full, seed=17 * call + items)
         dims = (items, i, o, t, c)

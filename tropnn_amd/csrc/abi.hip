@@ -356,10 +356,11 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
         (grad_lut && misaligned(grad_lut, lut_grad_vec * 4)) || misaligned(route_record, 8))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "a device pointer is not aligned to its element/vector size");
     if (grad_latent || grad_thresholds || grad_lut) {
-        if (!workspace || workspace_bytes < p.workspace_bytes)
+        if (p.workspace_bytes > 0 && (!workspace || workspace_bytes < p.workspace_bytes))
             return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace of %zu bytes required, got %zu", p.workspace_bytes,
                         workspace_bytes);
-        if (misaligned(workspace, 16)) return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+        if (p.workspace_bytes > 0 && misaligned(workspace, 16))
+            return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
     }
     // an item's gu slots [T * C] and the inverse anchor index sit in one
     // workgroup's LDS (160 KB on gfx950): 3 T C + in_f words, about 13,000

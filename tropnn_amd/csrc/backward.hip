@@ -64,6 +64,7 @@
 // threshold gradient from gu) and the row kernel without dots.
 //  A third, tiny kernel builds the inverse anchor index; callers rebuild it
 //  only when the anchors change.
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 #include <unordered_map>
@@ -908,6 +909,23 @@ __global__ __launch_bounds__(kReduceThreads) void pairwise_bwd_reduce_kernel(Red
 constexpr int kFusedThreads = 1024;  // threads of a fused workgroup = items per sort tile
 constexpr int kFusedFloats = 32;     // grad-row floats a lane has in flight: 32 / V items per batch
 constexpr uint32_t kPadSlot = 0x80000000u;  // sorted-entry flag of a row's padding slot
+// Item role: at most this many tables (so that, with one table workgroup per
+// CU, at least a quarter of gfx950's 256 CUs take the item workgroups), at
+// least kItemRoleMinWgs item workgroups, at most kItemChunk items in LDS.
+// It gathers two LUT rows per (item, table) through the L2 on the CUs the
+// table workgroups leave free, so its time grows with T / (CUs - T) x row
+// bytes, while the scatter kernel it replaces costs a kernel boundary plus
+// ~4 us. Measured at T = 136, B = 512 (graph-replayed steps): f32 rows of
+// up to 256 bytes 17.8 -> 14.9 us per step, 384 bytes 20.1 -> 19.5 us,
+// 512 bytes (c2) 20.3 -> 22.2 us; f16 rows of 256 bytes 23.6 -> 22.1 us.
+// So the planner takes it while T x row bytes <= kItemRoleRowBytes x
+// (kCus - T), a product between the winning 384 and the losing 512 bytes at
+// T = 136.
+constexpr int kItemRoleMaxTables = 192;
+constexpr int kItemRoleMinWgs = 32;
+constexpr int kItemChunk = 32;
+constexpr int kCus = 256;               // gfx950 (MI355X)
+constexpr int kItemRoleRowBytes = 448;
 
 struct FusedArgs {
     const float *grad_out;
@@ -924,7 +942,156 @@ struct FusedArgs {
     int items, out_f, tables, comps, rows;
     int slots;  // sorted-list capacity: a tile's items plus K - 1 padding slots per row
     int lut_off, cnt_off, off_off, sorted_off, u_off, dt_off, rowbuf_off, thr_off, wtot_off, part_off, brow_off;  // LDS bytes
+    // item role: workgroups table_wgs.. form the input gradient of item_n
+    // items each (no scatter kernel), item_nc items at a time in LDS
+    int table_wgs;  // workgroups of the table role (the first ones): T, or 0
+    const int32_t *index_offsets;
+    const int32_t *index_entries;
+    float *grad_x;  // or null (no item role)
+    int in_f, item_n, item_nc;
+    int ir_rec_off, ir_g_off, ir_gud_off, ir_idx_off;  // LDS bytes
 };
+
+constexpr int kScatterThreads = 256;  // threads of a scatter-kernel workgroup (one item)
+
+// The feature walk of feature_walk for nc items at once over nthr threads:
+// unit w = (item i, feature f), i = w / in_f, with item i's gu slots at
+// gud + i * gstride and its gradient row at grad_x_rows + i * in_f. A pair of
+// lanes walks a unit exactly when the scatter kernel's 256 threads pair
+// them (2 in_f <= 256), so each value is summed in the scatter kernel's
+// order.
+__device__ __forceinline__ void feature_walk_items(const float *gud, int gstride, const int *idx_s, int in_f,
+                                                   int nc, float *grad_x_rows, int tid, int nthr) {
+    const int *off_s = idx_s, *ent_s = idx_s + in_f + 1;
+    const bool pair = in_f * 2 <= kScatterThreads;  // uniform
+    const int h = pair ? tid & 1 : 0;
+    const int wstep = pair ? nthr >> 1 : nthr, estep = pair ? 2 * kEntries : kEntries;
+    const float inv_in = 1.0f / static_cast<float>(in_f);
+    const int nunits = nc * in_f;
+    // both lanes of a pair see the same w, so they leave the loop together
+    for (int w = pair ? tid >> 1 : tid; w < nunits; w += wstep) {
+        const int i = small_div(w, inv_in), f = w - i * in_f;
+        const float *gi = gud + i * gstride;
+        const int f0 = off_s[f], f1 = off_s[f + 1];
+        float gx = 0.f;
+        for (int eb = f0 + h * kEntries; eb < f1; eb += estep) {
+            int en[kEntries];
+#pragma unroll
+            for (int q = 0; q < kEntries; ++q) en[q] = ent_s[eb + q];
+            float v[kEntries];
+#pragma unroll
+            for (int q = 0; q < kEntries; ++q) v[q] = gi[en[q] >> 1];
+#pragma unroll
+            for (int q = 0; q < kEntries; ++q) {
+                const float sv = (en[q] & 1) ? -v[q] : v[q];  // gx + (-v) rounds as gx - v
+                gx = eb + q < f1 ? gx + sv : gx;
+            }
+        }
+        if (pair) {
+            const float other = dpp<kXor1>(gx);  // the partner lane's sum
+            if (h == 0) __builtin_nontemporal_store(gx + other, grad_x_rows + w);
+        } else {
+            __builtin_nontemporal_store(gx, grad_x_rows + w);
+        }
+    }
+}
+
+// Item role of the fused kernel (the workgroups after the table_wgs table
+// ones): the input gradient of item_n consecutive items, with no dependency
+// on the table role, so the step needs no scatter kernel after it. Per chunk
+// of item_nc items the route records [item][T] and G rows go to LDS (and,
+// once, the inverse anchor index). Every (item, table) unit's STE dot
+// s * sum_o G[b,o] (L[t,nb,o] - L[t,code,o]) is formed by a row group of S
+// lanes x V columns exactly as the table role forms it (the same lane
+// columns, per-lane sum and reduce-scatter, so the same bits), from LUT rows
+// read through the L2 in batches of K units of one item; the lane holding a
+// unit's dot forms gu = dot * surrogate'(u) and writes the item's C signed
+// (table, comparison) slots (gu at r*, zeros elsewhere), and the feature walk
+// sums them into grad_latent as the scatter kernel does. Batches past the
+// last unit read zeros and write nothing.
+template <typename T, int V, int S>
+__device__ __forceinline__ void fused_item_role(const FusedArgs &a, unsigned char *lds) {
+    constexpr int NG = kFusedThreads / S;  // row groups
+    constexpr int K = kFusedFloats / V;    // units per batch
+    constexpr int P = S * V;
+    const int tid = threadIdx.x;
+    const int u = static_cast<int>(blockIdx.x) - a.table_wgs;
+    const int b_begin = u * a.item_n;
+    const int b_end = min(a.items, b_begin + a.item_n);
+    const int TT = a.tables, C = a.comps, R = a.rows, O = a.out_f;
+    uint64_t *rec_s = reinterpret_cast<uint64_t *>(lds + a.ir_rec_off);  // [nc][T] route records
+    float *g_s = reinterpret_cast<float *>(lds + a.ir_g_off);            // [nc][O] G rows, then P zeros
+    float *gud = reinterpret_cast<float *>(lds + a.ir_gud_off);          // [nc][T * C] signed slots
+    int *idx_s = reinterpret_cast<int *>(lds + a.ir_idx_off);            // the inverse anchor index
+    const __amdgpu_buffer_rsrc_t lut_rsrc = buffer_rsrc(a.lut, a.lut_bytes);
+    const int n_ent = 2 * TT * C;
+    const int nidx = a.in_f + 1 + n_ent + kEntries;
+    for (int k = tid; k < nidx; k += kFusedThreads)
+        idx_s[k] = index_word(a.index_offsets, a.index_entries, a.in_f, n_ent, k);
+    const int g = tid / S, j = tid % S;
+    const int col = j * V;
+    const bool col_ok = col < O;
+    const uint32_t lane_off = (static_cast<uint32_t>(col) * static_cast<uint32_t>(sizeof(T))) | (col_ok ? 0u : kOutOfRange);
+    const uint32_t row_bytes = static_cast<uint32_t>(O) * static_cast<uint32_t>(sizeof(T));
+    const int nbi = (TT + K - 1) / K;  // batches per item
+    const float inv_nbi = 1.0f / static_cast<float>(nbi);
+    for (int c0 = b_begin; c0 < b_end; c0 += a.item_nc) {
+        const int nc = min(a.item_nc, b_end - c0);
+        // records: consecutive threads take consecutive items of one table
+        for (int q = tid; q < nc * TT; q += kFusedThreads) {
+            const int t = q / nc, i = q - t * nc;
+            rec_s[i * TT + t] = a.rec[static_cast<size_t>(t) * a.items + c0 + i];
+        }
+        for (int q = tid; q < nc * O + P; q += kFusedThreads)
+            g_s[q] = q < nc * O ? a.grad_out[static_cast<size_t>(c0) * O + q] : 0.f;
+        __syncthreads();
+        const int nbatch = nc * nbi;
+        for (int k = 0; __ballot(g + k * NG < nbatch) != 0; ++k) {  // wave-uniform trip count
+            const int bt = g + k * NG;
+            const bool live = bt < nbatch;
+            const int i = live ? small_div(bt, inv_nbi) : 0;
+            const int tb = (bt - i * nbi) * K;
+            float gv[V];
+#pragma unroll
+            for (int e = 0; e < V; ++e) gv[e] = g_s[i * O + col + e];
+            float lc[K][V], ln[K][V];
+#pragma unroll
+            for (int q = 0; q < K; ++q) {
+                const int t = tb + q;
+                const bool ok = live && t < TT;
+                const uint64_t rr = ok ? rec_s[i * TT + t] : 0ull;
+                const int code = rec_code(rr) & (R - 1), r = rec_r(rr) & 7;
+                const int nb = (code ^ (1 << r)) & (R - 1);
+                const uint32_t tbase = static_cast<uint32_t>(t * R) * row_bytes;
+                const uint32_t dead = ok ? 0u : kOutOfRange;
+                buffer_row<T, V>(lut_rsrc, (tbase + static_cast<uint32_t>(code) * row_bytes + lane_off) | dead, 0, lc[q]);
+                buffer_row<T, V>(lut_rsrc, (tbase + static_cast<uint32_t>(nb) * row_bytes + lane_off) | dead, 0, ln[q]);
+            }
+            float d[K];
+#pragma unroll
+            for (int q = 0; q < K; ++q) {
+                float sd = 0.f;
+#pragma unroll
+                for (int e = 0; e < V; ++e) sd += gv[e] * (ln[q][e] - lc[q][e]);
+                d[q] = sd;
+            }
+            const float dot = reduce_scatter<S, K>(d, j) * a.scale;
+            const int q = (j / (S / K)) & (K - 1);  // the unit whose dot this lane holds
+            const int t = tb + q;
+            if (live && t < TT && j % (S / K) == 0) {
+                const uint64_t rr = rec_s[i * TT + t];
+                const int r = rec_r(rr) & 7;
+                const float gu = dot * surrogate_grad(rec_u(rr), a.surrogate);
+                float *slot = gud + (i * TT + t) * C;
+                for (int c = 0; c < C; ++c) slot[c] = c == r ? gu : 0.f;
+            }
+        }
+        __syncthreads();
+        feature_walk_items(gud, TT * C, idx_s, a.in_f, nc, a.grad_x + static_cast<size_t>(c0) * a.in_f, tid,
+                           kFusedThreads);
+        __syncthreads();
+    }
+}
 
 // One workgroup per table; the row group of S lanes x V columns spans the
 // whole output row (S * V >= O). The table's LUT rows sit in LDS as f32.
@@ -960,6 +1127,10 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
     float *part = reinterpret_cast<float *>(lds + a.part_off);             // [groups][2][pitch] split rows
     int *brow = reinterpret_cast<int *>(lds + a.brow_off);                 // [slots / K] row of each batch
 
+    if (static_cast<int>(blockIdx.x) >= a.table_wgs) {  // item role (uniform per workgroup)
+        fused_item_role<T, V, S>(a, lds);
+        return;
+    }
     const int t = blockIdx.x;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -1302,7 +1473,6 @@ struct ScatterArgs {
     int items, in_f, tables, comps;
 };
 
-constexpr int kScatterThreads = 256;
 constexpr int kScatterIndex = 8;  // index words per thread in flight
 
 __global__ __launch_bounds__(kScatterThreads) void pairwise_bwd_scatter_kernel(ScatterArgs a) {
@@ -1465,19 +1635,35 @@ hipError_t launch_item_typed(const ItemArgs &args, const BackwardPlan &p, hipStr
 }
 
 template <typename T, int V, int S>
-hipError_t launch_fused_vs(const FusedArgs &args, const BackwardPlan &p, hipStream_t stream) {
+hipError_t launch_fused_vs(const FusedArgs &args, int wgs, const BackwardPlan &p, hipStream_t stream) {
     auto kernel = pairwise_bwd_fused_kernel<T, V, S>;
-    if (hipError_t e = allow_lds(kernel, p.f_lds_bytes); e != hipSuccess) return e;
-    return launch_kernel(TROPNN_KERNEL_BACKWARD_FUSED, kernel, dim3(args.tables), dim3(kFusedThreads), p.f_lds_bytes,
+    if (hipError_t e = allow_lds(kernel, p.f_launch_lds); e != hipSuccess) return e;
+    return launch_kernel(TROPNN_KERNEL_BACKWARD_FUSED, kernel, dim3(wgs), dim3(kFusedThreads), p.f_launch_lds,
                          stream, args);
 }
 
 template <typename T>
-hipError_t launch_fused_typed(const FusedArgs &args, const BackwardPlan &p, hipStream_t stream) {
-    if (p.fvec == 2) return launch_fused_vs<T, 2, 16>(args, p, stream);
-    if (p.fvec == 4) return launch_fused_vs<T, 4, 16>(args, p, stream);
-    if (p.fslices == 16) return launch_fused_vs<T, 8, 16>(args, p, stream);
-    return launch_fused_vs<T, 8, 32>(args, p, stream);
+hipError_t launch_fused_typed(const FusedArgs &args, int wgs, const BackwardPlan &p, hipStream_t stream) {
+    if (p.fvec == 2) return launch_fused_vs<T, 2, 16>(args, wgs, p, stream);
+    if (p.fvec == 4) return launch_fused_vs<T, 4, 16>(args, wgs, p, stream);
+    if (p.fslices == 16) return launch_fused_vs<T, 8, 16>(args, wgs, p, stream);
+    return launch_fused_vs<T, 8, 32>(args, wgs, p, stream);
+}
+
+// Compute units of the device a stream runs on, looked up once per device
+// (gfx950: 256). 0 if the runtime cannot say.
+int device_cus(hipStream_t stream) {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if ((stream != nullptr ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev)) != hipSuccess || dev < 0 ||
+        dev >= 64)
+        return 0;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 0) v = 0;
+        cache[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
 }
 
 __global__ void fill_zero_kernel(float *p, size_t n) {
@@ -1630,6 +1816,28 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
         off += (p.f_slots / batch + 1) * 4;
         p.f_lds_bytes = off;
         p.fused = d.rows * p.fpitch * 4 <= 64 * 1024 && off <= 160 * 1024;
+        // item role: the most items (up to kItemChunk) whose records [nc][T]
+        // u64, G rows [nc][O] (+ one row pitch of zeros) and signed slots
+        // [nc][T * C] f32, with the inverse anchor index, fit the table role's
+        // LDS (or, for one item, up to 160 KB)
+        const int idx_bytes = (d.in_f + 1 + 2 * d.tables * d.comps + kEntries) * 4;
+        auto a16 = [](int v) { return (v + 15) & ~15; };
+        auto item_bytes = [&](int nc) {
+            return a16(nc * d.tables * 8) + a16((nc * d.out_f + p.fpitch) * 4) + a16(nc * d.tables * d.comps * 4) +
+                   idx_bytes;
+        };
+        const int cap = p.f_lds_bytes > item_bytes(1) ? p.f_lds_bytes : item_bytes(1);
+        int nc = 0;
+        while (nc < kItemChunk && item_bytes(nc + 1) <= cap) ++nc;
+        p.f_item = p.fused && d.tables <= kItemRoleMaxTables && nc >= 1 && item_bytes(1) <= 160 * 1024 &&
+                   static_cast<long long>(d.tables) * d.out_f * esize <=
+                       static_cast<long long>(kItemRoleRowBytes) * (kCus - d.tables);
+        p.f_item_nc = nc;
+        p.f_ir_rec_off = 0;
+        p.f_ir_g_off = a16(nc * d.tables * 8);
+        p.f_ir_gud_off = p.f_ir_g_off + a16((nc * d.out_f + p.fpitch) * 4);
+        p.f_ir_idx_off = p.f_ir_gud_off + a16(nc * d.tables * d.comps * 4);
+        p.f_launch_lds = p.f_item ? cap : p.f_lds_bytes;
     }
     // workspace: fused path {gu, r} [T][B] u64; general path {gu, r} [T][B]
     // u64 (min-margin) or gu [T][C][B] f32 (full STE), then the sort
@@ -1639,7 +1847,7 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     // each region 16-byte aligned
     auto align16 = [](size_t v) { return (v + 15) & ~static_cast<size_t>(15); };
     if (p.fused) {
-        p.workspace_bytes = static_cast<size_t>(d.tables) * d.items * sizeof(uint64_t);
+        p.workspace_bytes = p.f_item ? 0 : static_cast<size_t>(d.tables) * d.items * sizeof(uint64_t);
     } else {
         size_t off = align16(static_cast<size_t>(d.tables) * d.items * (p.full ? d.comps * sizeof(float) : sizeof(uint64_t)));
         p.ws_slot_off = off;
@@ -1666,7 +1874,10 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
     const uint32_t g_bytes = static_cast<uint32_t>(static_cast<size_t>(d.items) * d.out_f * 4);
     if (p.fused) {
         if (grad_x == nullptr && grad_thr == nullptr && grad_lut == nullptr) return hipSuccess;
-        uint64_t *gurec = grad_x != nullptr ? reinterpret_cast<uint64_t *>(workspace) : nullptr;
+        // the item role forms grad_latent in the same launch (no scatter
+        // kernel); otherwise the table role leaves {gu, r} records for it
+        const bool item_role = p.f_item && grad_x != nullptr;
+        uint64_t *gurec = grad_x != nullptr && !item_role ? reinterpret_cast<uint64_t *>(workspace) : nullptr;
         FusedArgs f{};
         f.grad_out = grad_out;
         f.lut = lut;
@@ -1698,9 +1909,31 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
         f.rowbuf_off = p.f_rowbuf_off;
         f.thr_off = p.f_thr_off;
         f.wtot_off = p.f_wtot_off;
-        hipError_t e = d.lut_dtype == TROPNN_LUT_F16 ? launch_fused_typed<_Float16>(f, p, stream)
-                                                      : launch_fused_typed<float>(f, p, stream);
-        if (e != hipSuccess || grad_x == nullptr) return e;
+        // table workgroups first (one per table, unless only grad_latent is
+        // asked for), then the item workgroups on the CUs the table ones
+        // leave free: n items each, all resident at once on MI355X
+        f.table_wgs = !item_role || grad_lut != nullptr || grad_thr != nullptr ? d.tables : 0;
+        int wgs = f.table_wgs;
+        if (item_role) {
+            int ni = device_cus(stream) - f.table_wgs;
+            if (ni < kItemRoleMinWgs) ni = kItemRoleMinWgs;
+            if (ni > d.items) ni = d.items;
+            const int n = (d.items + ni - 1) / ni;
+            f.item_n = n;
+            f.item_nc = n < p.f_item_nc ? n : p.f_item_nc;
+            f.grad_x = grad_x;
+            f.index_offsets = index_offsets;
+            f.index_entries = index_entries;
+            f.in_f = d.in_f;
+            f.ir_rec_off = p.f_ir_rec_off;
+            f.ir_g_off = p.f_ir_g_off;
+            f.ir_gud_off = p.f_ir_gud_off;
+            f.ir_idx_off = p.f_ir_idx_off;
+            wgs += (d.items + n - 1) / n;
+        }
+        hipError_t e = d.lut_dtype == TROPNN_LUT_F16 ? launch_fused_typed<_Float16>(f, wgs, p, stream)
+                                                      : launch_fused_typed<float>(f, wgs, p, stream);
+        if (e != hipSuccess || grad_x == nullptr || item_role) return e;
         return launch_scatter(gurec, index_offsets, index_entries, grad_x, d, p, stream);
     }
     const bool need_gu = grad_x != nullptr || grad_thr != nullptr;

@@ -102,8 +102,15 @@ struct BackwardPlan {
     int f_part_off, f_brow_off;
     int f_slots;        // sorted-list capacity of a tile (items + padding to whole batches)
     int f_lds_bytes;
+    // item role of the fused launch (tables <= kItemRoleMaxTables): workgroups
+    // after the table ones form the input gradient, so no scatter kernel runs
+    // and the fused path needs no workspace
+    bool f_item;
+    int f_item_nc;      // items of an item-role workgroup held in LDS at once
+    int f_ir_rec_off, f_ir_g_off, f_ir_gud_off, f_ir_idx_off;  // LDS bytes
+    int f_launch_lds;   // the launch's dynamic LDS: max of the two roles'
     int scatter_lds_bytes;   // gu slots [T * C] f32 + the inverse anchor index
-    size_t workspace_bytes;  // fused: {gu, r} [T][B] u64; general: gu, then the sort kernel's output
+    size_t workspace_bytes;  // fused: none with the item role, else {gu, r} [T][B] u64; general: gu, then the sort kernel's output
 };
 
 // Row loads a forward wave keeps in flight (its gather chunk), by LUT element
