@@ -734,7 +734,7 @@ def bench_c5(args, dev) -> dict:
     stack and of the oracle stack with torch Adam, from the same init."""
     import torch
 
-    from tropnn_amd import FusedAdam, cross_entropy
+    from tropnn_amd import FusedAdam, cross_entropy, unit_gradient
     from tropnn_amd.examples import EmnistPairwiseClassifier, make_c5_batch
 
     model = EmnistPairwiseClassifier().to(dev).train()
@@ -746,7 +746,8 @@ def bench_c5(args, dev) -> dict:
 
     def step(k: int) -> None:
         x, y = batches[k]
-        cross_entropy(model(x), y).backward()
+        loss = cross_entropy(model(x), y)
+        loss.backward(unit_gradient(loss))  # as loss.backward(), without its fill and scaling launches
         opt.step()
 
     side = torch.cuda.Stream(dev)

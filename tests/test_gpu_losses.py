@@ -95,3 +95,30 @@ def test_empty_batch_gives_nan_loss():
     assert math.isnan(loss.detach().item()) and math.isnan(float(ref))
     loss.backward()
     assert logits.grad is not None and logits.grad.shape == (0, 10)
+
+
+def test_unit_gradient_backward_matches_plain_backward():
+    """loss.backward(unit_gradient(loss)) returns the kernel's logits gradient
+    unscaled (no multiplication launch) and equals loss.backward(); a scaled
+    incoming gradient still scales it."""
+    from tropnn_amd import unit_gradient
+
+    gen = torch.Generator().manual_seed(3)
+    logits = torch.randn(512, 10, generator=gen)
+    target = torch.randint(0, 10, (512,), generator=gen)
+    want_loss, want_grad = reference(logits, target)
+    grads = []
+    for how in ("plain", "unit", "unit again", "scaled"):
+        x = logits.to(DEV).requires_grad_(True)
+        loss = cross_entropy(x, target.to(DEV))
+        if how == "plain":
+            loss.backward()
+        elif how == "scaled":
+            loss.backward(torch.tensor(3.0, device=DEV))
+        else:
+            loss.backward(unit_gradient(loss))
+        grads.append(x.grad.detach().cpu())
+    assert torch.equal(grads[0], grads[1]) and torch.equal(grads[1], grads[2])
+    bad = (grads[1].double() - want_grad).abs() > 1e-5 * want_grad.abs() + 1e-8
+    assert not bad.any()
+    assert torch.allclose(grads[3], 3.0 * grads[0], rtol=1e-6, atol=0)

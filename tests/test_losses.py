@@ -29,3 +29,19 @@ def test_bad_shapes_and_dtypes_raise_before_launch(monkeypatch):
         cross_entropy_hip(Fake((4, 3), torch.float32), Fake((5,), torch.int64))
     with pytest.raises(ValueError, match="rows"):
         cross_entropy_hip(Fake((4, 3, 2), torch.float32), Fake((4,), torch.int64))
+
+
+def test_unit_gradient_is_kept_and_replaced_after_a_write():
+    from tropnn_amd import unit_gradient
+    from tropnn_amd.losses import _is_unit
+
+    loss = torch.tensor(2.5)
+    u = unit_gradient(loss)
+    assert u.shape == () and u.dtype == torch.float32 and float(u) == 1.0
+    assert unit_gradient(torch.tensor(0.0)) is u  # one per device and dtype
+    assert _is_unit(u) and not _is_unit(torch.ones(()))
+    assert unit_gradient(torch.tensor(1.0, dtype=torch.float64)) is not u
+    u.mul_(3.0)  # a write: no longer the unit
+    assert not _is_unit(u)
+    fresh = unit_gradient(loss)
+    assert fresh is not u and float(fresh) == 1.0 and _is_unit(fresh)

@@ -3,7 +3,7 @@ comparator route, LUT gather-sum and min-margin STE backward as gfx950 HIP
 kernels in libtropnn_hip.so (C ABI: include/tropnn_hip.h)."""
 from .backends import has_pairwise_hip, pairwise_hip, pairwise_hip_forward, pairwise_hip_route
 from .layers import PairwiseLinear, RoutedLinearBase
-from .losses import cross_entropy
+from .losses import cross_entropy, unit_gradient
 from .optim import FusedAdam, FusedAdamW
 
 __all__ = [
@@ -16,4 +16,5 @@ __all__ = [
     "pairwise_hip",
     "pairwise_hip_forward",
     "pairwise_hip_route",
+    "unit_gradient",
 ]

@@ -22,6 +22,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from ..layers import PairwiseLinear
+from ..losses import unit_gradient
 
 
 class EmnistPairwiseClassifier(nn.Module):
@@ -71,10 +72,13 @@ def make_c5_batch(batch: int = 512, input_dim: int = 784, num_classes: int = 10,
 def train_step(model: nn.Module, optimizer: torch.optim.Optimizer, x: Tensor, y: Tensor, loss_fn=F.cross_entropy) -> Tensor:
     """One step of the reference's training loop (examples/emnist.py:218-224);
     returns the loss tensor. loss_fn defaults to the reference's
-    F.cross_entropy; tropnn_amd.cross_entropy is its one-launch HIP form."""
+    F.cross_entropy; tropnn_amd.cross_entropy is its one-launch HIP form. The
+    backward starts from the kept unit gradient (loss.backward() computes the
+    same): no fill launch for d loss / d loss, and none for scaling
+    tropnn_amd.cross_entropy's logits gradient."""
     optimizer.zero_grad(set_to_none=True)
     logits = model(x)
     loss = loss_fn(logits, y)
-    loss.backward()
+    loss.backward(unit_gradient(loss))
     optimizer.step()
     return loss
