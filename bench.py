@@ -413,8 +413,14 @@ def _spread(values) -> dict:
     return {"mean": sum(v) / len(v), "median": v[len(v) // 2], "min": v[0], "max": v[-1], "n": len(v)}
 
 
-def time_windows(window, steps: int, warmup: int, min_windows: int = 25, min_steps: int = 100,
-                 min_seconds: float = 0.2) -> dict:
+# (min windows, min steps, min seconds, warmup seconds) of time_windows();
+# --quick (rocprofv3 counter passes, where every dispatch is serialised)
+# lowers them to a few dispatches of each kernel
+WINDOW_FLOORS = {"windows": 25, "steps": 100, "seconds": 0.2, "warmup_s": 0.3}
+
+
+def time_windows(window, steps: int, warmup: int, min_windows: int | None = None, min_steps: int | None = None,
+                 min_seconds: float | None = None) -> dict:
     """Device time per step, measured the way BASELINE.md plans it (the median
     over >= 100 steps). window() issues one window of `steps` steps without
     waiting for them. After >= `warmup` warmup windows and >= 0.3 s of them
@@ -430,10 +436,13 @@ def time_windows(window, steps: int, warmup: int, min_windows: int = 25, min_ste
 
     import torch
 
+    min_windows = WINDOW_FLOORS["windows"] if min_windows is None else min(min_windows, WINDOW_FLOORS["windows"])
+    min_steps = WINDOW_FLOORS["steps"] if min_steps is None else min(min_steps, WINDOW_FLOORS["steps"])
+    min_seconds = WINDOW_FLOORS["seconds"] if min_seconds is None else min(min_seconds, WINDOW_FLOORS["seconds"])
     stream = torch.cuda.current_stream()
     torch.cuda.synchronize()
     t0, w = time.perf_counter(), 0
-    while w < max(warmup, 2) or time.perf_counter() - t0 < 0.3:
+    while w < max(warmup, 2) or time.perf_counter() - t0 < WINDOW_FLOORS["warmup_s"]:
         window()
         w += 1
     torch.cuda.synchronize()
@@ -1162,7 +1171,7 @@ def bench_c2(args, dev) -> dict:
     algo = algorithmic_bytes(fused, scatter=scatter)
     comp = compulsory_bytes(fused, scatter=scatter)
     names = tuple(algo)
-    ksteps = 200
+    ksteps = 20 if args.quick else 200
     evs = _kernel_events(names, ksteps)
     torch.cuda.synchronize()
     for k in range(ksteps):
@@ -1368,6 +1377,12 @@ def main() -> int:
         "compact records under other_configs (off: the c2 line alone)",
     )
     ap.add_argument(
+        "--quick",
+        action="store_true",
+        help="minimal timing for rocprofv3 counter passes (every dispatch serialised): two windows, no time "
+        "floors, 20 event-stamped steps; the times it prints are not benchmarks",
+    )
+    ap.add_argument(
         "--calibrate-copy-bytes",
         type=int,
         default=0,
@@ -1379,6 +1394,8 @@ def main() -> int:
         args.steps = 20 if args.workload == "c4" else 500
     if args.warmup is None:
         args.warmup = 3 if args.workload == "c4" else 50
+    if args.quick:
+        WINDOW_FLOORS.update(windows=2, steps=0, seconds=0.0, warmup_s=0.0)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
             "bench.py measures one GPU only: the PairwiseLinear path is built and measured on a single MI355X "
