@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TROPNN_HIP_ABI_VERSION 10
+#define TROPNN_HIP_ABI_VERSION 11
 
 /* status codes */
 #define TROPNN_OK 0
@@ -48,6 +48,16 @@ extern "C" {
 /* which comparisons carry the STE gradient (layers/pairwise.py:137-200) */
 #define TROPNN_STE_MIN_MARGIN 0
 #define TROPNN_STE_FULL 1
+/* Flags ORed into ste_mode (of the backward and of its workspace size, alike)
+ * that choose where the min-margin backward of narrow rows (out_features a
+ * multiple of 4 up to 64 or of 8 up to 256) forms grad_latent. Neither: by the
+ * row width, the crossover measured on independent inputs. The choice changes
+ * no result bit (both forms sum in the same order), only the time and the
+ * workspace size (none with FUSED). No counterpart in the reference. */
+#define TROPNN_BWD_INPUT_GRAD_FUSED 0x100   /* in the backward's first launch, whenever the shape allows
+                                               (pays where the items' codes concentrate on few LUT rows,
+                                               e.g. a layer fed by another PairwiseLinear) */
+#define TROPNN_BWD_INPUT_GRAD_SCATTER 0x200 /* in a per-item kernel after it */
 
 /* Largest `comparisons` the kernels take (LUT rows per table = 2^comparisons). */
 #define TROPNN_MAX_COMPARISONS 8

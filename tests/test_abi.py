@@ -22,9 +22,9 @@ def header_functions() -> list[str]:
 
 
 def header_define(name: str) -> int:
-    m = re.search(rf"#define {name} (\d+)", HEADER.read_text())
+    m = re.search(rf"#define {name} (0x[0-9a-fA-F]+|\d+)", HEADER.read_text())
     assert m, name
-    return int(m.group(1))
+    return int(m.group(1), 0)
 
 
 @pytest.fixture(scope="module")
@@ -54,6 +54,8 @@ def test_constants_match_header():
     assert header_define("TROPNN_MAX_COMPARISONS") == ph.MAX_COMPARISONS
     assert header_define("TROPNN_STE_MIN_MARGIN") == ph.STE_MIN_MARGIN
     assert header_define("TROPNN_STE_FULL") == ph.STE_FULL
+    assert header_define("TROPNN_BWD_INPUT_GRAD_FUSED") == ph.BWD_INPUT_GRAD_FUSED
+    assert header_define("TROPNN_BWD_INPUT_GRAD_SCATTER") == ph.BWD_INPUT_GRAD_SCATTER
     for name, kid in ph.KERNEL_IDS.items():
         assert header_define("TROPNN_KERNEL_" + name.upper()) == kid
 
@@ -97,6 +99,15 @@ def test_workspace_size(lib):
     assert ws(33, 20, 40, 7, 3, ph.LUT_F32, ph.STE_FULL) == general(33, 40, 7, 8, 3, 64, True)
     assert ws(512, 128, 128, 136, 9, ph.LUT_F32, ph.STE_MIN_MARGIN) == 0
     assert ws(512, 128, 128, 136, 6, ph.LUT_F32, 7) == 0 and "ste_mode" in _err(lib)
+    # the caller's input-gradient flags: FUSED takes the item role past the
+    # row-width rule (not past its limits), SCATTER keeps the scatter kernel
+    fused, scatter = ph.BWD_INPUT_GRAD_FUSED, ph.BWD_INPUT_GRAD_SCATTER
+    assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_MIN_MARGIN | fused) == 0  # c2 rows in the fused launch
+    assert ws(512, 128, 10, 136, 6, ph.LUT_F32, ph.STE_MIN_MARGIN | scatter) == 136 * 512 * 8
+    assert ws(512, 128, 8, 193, 6, ph.LUT_F32, ph.STE_MIN_MARGIN | fused) == 193 * 512 * 8  # over 192 tables
+    assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_FULL | fused) == general(512, 128, 136, 64, 6, 64, True)
+    assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_MIN_MARGIN | fused | scatter) == 0 and "flags" in _err(lib)
+    assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_MIN_MARGIN | 0x400) == 0 and "flags" in _err(lib)
 
 
 def _err(lib) -> str:
@@ -248,7 +259,7 @@ def test_autograd_operator_loads_and_binds(lib):
     op = ph._pairwise_op()
     args = [a.name for a in op._schema.arguments]
     assert args == ["latent", "anchors", "thresholds", "lut", "lut_read", "index_offsets", "index_entries",
-                    "ste", "min_margin", "surrogate", "output_scale", "route_mode"]
+                    "ste", "min_margin", "surrogate", "output_scale", "route_mode", "input_grad"]
     assert len(op._schema.returns) == 3
     addr = ctypes.cast(lib.tropnn_hip_pairwise_forward, ctypes.c_void_p).value
     with pytest.raises(RuntimeError, match="ABI version"):
@@ -261,3 +272,6 @@ def test_autograd_operator_loads_and_binds(lib):
     with pytest.raises(ValueError, match="surrogate"):
         op(x, anchors, torch.zeros(3, 2), torch.zeros(3, 4, 5), torch.zeros(3, 4, 5), None, None,
            True, True, 7, 1.0, 0)
+    with pytest.raises(ValueError, match="input-gradient"):
+        op(x, anchors, torch.zeros(3, 2), torch.zeros(3, 4, 5), torch.zeros(3, 4, 5), None, None,
+           True, True, 0, 1.0, 0, 3)

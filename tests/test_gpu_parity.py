@@ -494,6 +494,42 @@ def test_fused_item_role(i, o, t, c, b, lut_dtype):
     assert_train_parity(ref, hip, *train_step(ref, hip, x, g))
 
 
+@pytest.mark.parametrize(
+    "i,o,t,c,b,lut_dtype",
+    [
+        (128, 128, 136, 6, 512, "f32"),  # c2: scatter kernel by the row-width rule
+        (128, 10, 136, 6, 512, "f32"),  # c5's last layer: item role by the rule
+        (128, 128, 136, 6, 700, "f16"),
+        (64, 8, 193, 4, 300, "f32"),  # past the item role's table limit: "fused" keeps the scatter kernel
+    ],
+)
+def test_input_grad_forms_are_bit_identical(i, o, t, c, b, lut_dtype):
+    """PairwiseLinear(input_grad=...): the fused launch's item role and the
+    scatter kernel give the same bits for every gradient (same dots, same
+    feature walk), so the caller's choice moves only the time; c2's shape on
+    the item role against the oracle at the f32 bars."""
+    results = {}
+    for form in ("auto", "fused", "scatter"):
+        ref, hip = make_pair(i, o, t, c, seed=i + o + t, thr_std=0.3, lut_dtype=lut_dtype)
+        hip.input_grad = form
+        if lut_dtype == "f16":
+            with torch.no_grad():
+                ref.lut.copy_(ref.lut.half().float())
+        x = seeded((b, i), seed=b + 15)
+        g = seeded((b, 1, o), seed=b + 16)
+        yx_ref, yx_hip = train_step(ref, hip, x, g)
+        assert_train_parity(ref, hip, yx_ref, yx_hip)
+        results[form] = [t_.detach().cpu() for t_ in (yx_hip[0], yx_hip[1].grad, hip.thresholds.grad, hip.lut.grad)]
+    for form in ("fused", "scatter"):
+        for k, (a, r) in enumerate(zip(results[form], results["auto"])):
+            assert torch.equal(a, r), (form, k)
+
+
+def test_input_grad_option_is_validated():
+    with pytest.raises(ValueError, match="input_grad"):
+        PairwiseLinear(8, 8, tables=2, comparisons=2, input_grad="sideways")
+
+
 def test_fused_item_role_input_gradient_only():
     """Parameters frozen, only the input gradient asked for: the fused launch
     is item workgroups alone (no table role), and grad_latent matches the

@@ -26,10 +26,11 @@ from typing import Any
 import torch
 from torch import Tensor
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 LUT_F32, LUT_F16 = 0, 1
 SURROGATE_IDS = {"fast_sigmoid_odd": 0, "izhikevich": 1}
 STE_MIN_MARGIN, STE_FULL = 0, 1
+BWD_INPUT_GRAD_FUSED, BWD_INPUT_GRAD_SCATTER = 0x100, 0x200  # flags ORed into the STE mode
 MAX_COMPARISONS = 8
 ERR_NAMES = {1: "invalid argument", 2: "unsupported", 3: "HIP error"}
 
@@ -42,6 +43,10 @@ _LOCK = threading.Lock()
 _LIB: ctypes.CDLL | None = None
 _PAIRWISE_OP: Any = None
 _ROUTE_MODES = {False: 0, True: 1, "codes": 2}
+# where the backward forms the latent gradient of narrow rows (the operator's
+# input_grad argument): the library's row-width rule, the fused launch, or a
+# kernel after it
+INPUT_GRAD_FORMS = {"auto": 0, "fused": 1, "scatter": 2}
 # Per-anchors-tensor caches live as attributes of the anchors tensor object
 # itself (not in a table keyed by address: the caching allocator reuses the
 # addresses of freed tensors), validated by the tensor's version counter,
@@ -379,6 +384,7 @@ def pairwise_hip(
     lut_read: Tensor | None = None,
     ste: bool = True,
     return_route: bool | str = True,
+    input_grad: str = "auto",
 ) -> tuple[Tensor, Tensor, Tensor]:
     """HIP counterpart of pairwise_tilelang (backends/pairwise_tilelang.py:537-549).
 
@@ -409,6 +415,10 @@ def pairwise_hip(
     threshold gradients; only the gradients the backward pass asks for are
     computed. The full STE needs every comparison's margin, which the forward
     then keeps.
+
+    input_grad: "auto", "fused" or "scatter", where the min-margin backward of
+    narrow rows forms the latent gradient (no counterpart in the reference;
+    the results are the same bits either way, see PairwiseLinear).
     """
     surrogate_id = SURROGATE_IDS.get(surrogate)
     if surrogate_id is None:
@@ -416,6 +426,9 @@ def pairwise_hip(
     route_mode = _ROUTE_MODES.get(return_route) if isinstance(return_route, (bool, str)) else None
     if route_mode is None:
         raise ValueError(f"return_route must be True, False or 'codes', got {return_route!r}")
+    input_grad_id = INPUT_GRAD_FORMS.get(input_grad) if isinstance(input_grad, str) else None
+    if input_grad_id is None:
+        raise ValueError(f"input_grad must be 'auto', 'fused' or 'scatter', got {input_grad!r}")
     _require_gpu(latent, anchors, thresholds, lut)
     op = _pairwise_op()
     if latent.ndim != 3:
@@ -440,6 +453,7 @@ def pairwise_hip(
         surrogate_id,
         float(output_scale),
         route_mode,
+        input_grad_id,
     )
 
 

@@ -283,14 +283,24 @@ int tropnn_hip_pairwise_route(int64_t items, int64_t in_features, int64_t tables
     return ok();
 }
 
+// ste_mode: TROPNN_STE_MIN_MARGIN or TROPNN_STE_FULL in the low byte, at
+// most one TROPNN_BWD_INPUT_GRAD_* flag above it.
+static constexpr int kSteModeMask = 0xff;
+static int check_ste_mode(int ste_mode) {
+    const int mode = ste_mode & kSteModeMask, flags = ste_mode & ~kSteModeMask;
+    if (mode != TROPNN_STE_MIN_MARGIN && mode != TROPNN_STE_FULL)
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "ste_mode must be TROPNN_STE_MIN_MARGIN or TROPNN_STE_FULL, "
+                    "optionally with one TROPNN_BWD_INPUT_GRAD_* flag, got %d", ste_mode);
+    if (flags != 0 && flags != TROPNN_BWD_INPUT_GRAD_FUSED && flags != TROPNN_BWD_INPUT_GRAD_SCATTER)
+        return fail(TROPNN_ERR_INVALID_ARGUMENT, "ste_mode carries unknown or conflicting flags: %d", ste_mode);
+    return TROPNN_OK;
+}
+
 size_t tropnn_hip_pairwise_backward_workspace_size(int64_t items, int64_t in_features, int64_t out_features,
                                                    int64_t tables, int64_t comparisons, int lut_dtype, int ste_mode) {
     tropnn::Dims d{};
     if (make_dims(items, in_features, out_features, tables, comparisons, lut_dtype, d) != TROPNN_OK) return 0;
-    if (ste_mode != TROPNN_STE_MIN_MARGIN && ste_mode != TROPNN_STE_FULL) {
-        fail(TROPNN_ERR_INVALID_ARGUMENT, "ste_mode must be TROPNN_STE_MIN_MARGIN or TROPNN_STE_FULL");
-        return 0;
-    }
+    if (check_ste_mode(ste_mode) != TROPNN_OK) return 0;
     ok();
     return tropnn::plan_backward(d, ste_mode).workspace_bytes;
 }
@@ -319,8 +329,7 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
                                  float *grad_lut, void *workspace, size_t workspace_bytes, tropnn_stream_t stream) {
     tropnn::Dims d{};
     if (int rc = make_dims(items, in_features, out_features, tables, comparisons, lut_dtype, d)) return rc;
-    if (ste_mode != TROPNN_STE_MIN_MARGIN && ste_mode != TROPNN_STE_FULL)
-        return fail(TROPNN_ERR_INVALID_ARGUMENT, "ste_mode must be TROPNN_STE_MIN_MARGIN or TROPNN_STE_FULL");
+    if (int rc = check_ste_mode(ste_mode)) return rc;
     if (surrogate != TROPNN_SURROGATE_FAST_SIGMOID_ODD && surrogate != TROPNN_SURROGATE_IZHIKEVICH)
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "surrogate must be a TROPNN_SURROGATE_* value");
     const tropnn::BackwardPlan p = tropnn::plan_backward(d, ste_mode);
@@ -341,7 +350,7 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "grad_output, lut and route_record must be non-NULL");
     if (grad_latent && (!index_offsets || !index_entries))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "grad_latent needs the anchor index (tropnn_hip_build_anchor_index)");
-    if (ste_mode == TROPNN_STE_FULL && (grad_latent || grad_thresholds) && !margins)
+    if ((ste_mode & kSteModeMask) == TROPNN_STE_FULL && (grad_latent || grad_thresholds) && !margins)
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "the full STE needs the forward's margins [items, tables, comparisons]");
     if (margins && misaligned(margins, 4))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "margins must be 4-byte aligned");
@@ -396,8 +405,7 @@ int tropnn_hip_pairwise_backward_noalloc(int64_t items, int64_t in_features, int
                                          float *grad_thresholds, float *grad_lut, tropnn_stream_t stream) {
     tropnn::Dims d{};
     if (int rc = make_dims(items, in_features, out_features, tables, comparisons, lut_dtype, d)) return rc;
-    if (ste_mode != TROPNN_STE_MIN_MARGIN && ste_mode != TROPNN_STE_FULL)
-        return fail(TROPNN_ERR_INVALID_ARGUMENT, "ste_mode must be TROPNN_STE_MIN_MARGIN or TROPNN_STE_FULL");
+    if (int rc = check_ste_mode(ste_mode)) return rc;
     const size_t need = tropnn::plan_backward(d, ste_mode).workspace_bytes;
     if (need > sizeof scratch)
         return fail(TROPNN_ERR_UNSUPPORTED,

@@ -104,6 +104,13 @@ Dims validate(const Tensor &latent, const Tensor &anchors, const Tensor &thresho
 }
 
 constexpr int64_t kRouteNone = 0, kRouteFull = 1, kRouteCodes = 2;
+// Where the backward forms the latent gradient of narrow rows: by the
+// library's row-width rule, in the fused launch, or in a kernel after it.
+constexpr int64_t kInputGradAuto = 0, kInputGradFused = 1, kInputGradScatter = 2;
+int input_grad_flag(int64_t input_grad) {
+    return input_grad == kInputGradFused ? TROPNN_BWD_INPUT_GRAD_FUSED
+                                         : input_grad == kInputGradScatter ? TROPNN_BWD_INPUT_GRAD_SCATTER : 0;
+}
 
 // One forward launch and the tensors it writes.
 struct Forward {
@@ -160,7 +167,8 @@ struct PairwiseFunction : public torch::autograd::Function<PairwiseFunction> {
                                  const Tensor &thresholds, const Tensor &lut, const Tensor &lut_read,
                                  const std::optional<Tensor> &index_offsets,
                                  const std::optional<Tensor> &index_entries, bool ste, bool min_margin,
-                                 int64_t surrogate, double output_scale, int64_t route_mode, bool recorded) {
+                                 int64_t surrogate, double output_scale, int64_t route_mode, int64_t input_grad,
+                                 bool recorded) {
         const Dims d = validate(latent, anchors, thresholds, lut_read);
         // What the backward may be asked for: every input that requires a
         // gradient, when autograd records this call. (needs_input_grad is
@@ -191,7 +199,8 @@ struct PairwiseFunction : public torch::autograd::Function<PairwiseFunction> {
             }
             ctx->saved_data["dims"] = std::vector<int64_t>{d.batch, d.steps, d.in_f, d.tables, d.comps, d.out_f};
             ctx->saved_data["ste"] = ste;
-            ctx->saved_data["ste_mode"] = static_cast<int64_t>(min_margin ? TROPNN_STE_MIN_MARGIN : TROPNN_STE_FULL);
+            ctx->saved_data["ste_mode"] =
+                static_cast<int64_t>((min_margin ? TROPNN_STE_MIN_MARGIN : TROPNN_STE_FULL) | input_grad_flag(input_grad));
             ctx->saved_data["surrogate"] = surrogate;
             ctx->saved_data["output_scale"] = output_scale;
         }
@@ -201,7 +210,7 @@ struct PairwiseFunction : public torch::autograd::Function<PairwiseFunction> {
     // Computes only the gradients this backward pass asks for (a subset of
     // those the forward recorded for).
     static variable_list backward(AutogradContext *ctx, variable_list grad_outputs) {
-        variable_list grads(13);
+        variable_list grads(14);  // one per forward argument
         const Tensor &grad_output = grad_outputs[0];
         if (!grad_output.defined()) return grads;
         const bool ste = ctx->saved_data["ste"].toBool();
@@ -251,11 +260,14 @@ std::tuple<Tensor, Tensor, Tensor> pairwise(const Tensor &latent, const Tensor &
                                             const Tensor &lut, const Tensor &lut_read,
                                             const std::optional<Tensor> &index_offsets,
                                             const std::optional<Tensor> &index_entries, bool ste, bool min_margin,
-                                            int64_t surrogate, double output_scale, int64_t route_mode) {
+                                            int64_t surrogate, double output_scale, int64_t route_mode,
+                                            int64_t input_grad) {
     TORCH_CHECK_VALUE(surrogate == TROPNN_SURROGATE_FAST_SIGMOID_ODD || surrogate == TROPNN_SURROGATE_IZHIKEVICH,
                       "unknown surrogate id ", surrogate);
     TORCH_CHECK_VALUE(route_mode == kRouteNone || route_mode == kRouteFull || route_mode == kRouteCodes,
                       "unknown route mode ", route_mode);
+    TORCH_CHECK_VALUE(input_grad == kInputGradAuto || input_grad == kInputGradFused || input_grad == kInputGradScatter,
+                      "unknown input-gradient form ", input_grad);
     const bool recorded =
         at::GradMode::is_enabled() && (latent.requires_grad() || thresholds.requires_grad() || lut.requires_grad());
     if (!recorded) {
@@ -266,7 +278,7 @@ std::tuple<Tensor, Tensor, Tensor> pairwise(const Tensor &latent, const Tensor &
     }
     auto outs = PairwiseFunction::apply(latent, anchors, thresholds, lut, lut_read.detach(), index_offsets,
                                         index_entries, ste, min_margin, surrogate, output_scale, route_mode,
-                                        recorded);
+                                        input_grad, recorded);
     return {outs[0], outs[1], outs[2]};
 }
 
@@ -277,6 +289,6 @@ TORCH_LIBRARY(tropnn_hip, m) {
           &bind_abi);
     m.def("pairwise(Tensor latent, Tensor anchors, Tensor thresholds, Tensor lut, Tensor lut_read, "
           "Tensor? index_offsets, Tensor? index_entries, bool ste, bool min_margin, int surrogate, "
-          "float output_scale, int route_mode) -> (Tensor, Tensor, Tensor)",
+          "float output_scale, int route_mode, int input_grad=0) -> (Tensor, Tensor, Tensor)",
           &pairwise);
 }

@@ -1719,7 +1719,7 @@ hipError_t launch_scatter(const uint64_t *gurec, const int32_t *index_offsets, c
 
 BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     BackwardPlan p{};
-    p.full = ste_mode == TROPNN_STE_FULL;
+    p.full = (ste_mode & 0xff) == TROPNN_STE_FULL;
     const int esize = d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4;
     // row kernel: V columns per lane (8 for rows of 64 columns or more that
     // 8 divides, else the largest divisor of the row up to 4), S lanes per
@@ -1829,9 +1829,12 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
         const int cap = p.f_lds_bytes > item_bytes(1) ? p.f_lds_bytes : item_bytes(1);
         int nc = 0;
         while (nc < kItemChunk && item_bytes(nc + 1) <= cap) ++nc;
-        p.f_item = p.fused && d.tables <= kItemRoleMaxTables && nc >= 1 && item_bytes(1) <= 160 * 1024 &&
-                   static_cast<long long>(d.tables) * d.out_f * esize <=
-                       static_cast<long long>(kItemRoleRowBytes) * (kCus - d.tables);
+        // (a caller's flag overrides the row-width rule, not the limits)
+        const bool by_width = (ste_mode & TROPNN_BWD_INPUT_GRAD_FUSED) != 0 ||
+                              static_cast<long long>(d.tables) * d.out_f * esize <=
+                                  static_cast<long long>(kItemRoleRowBytes) * (kCus - d.tables);
+        p.f_item = p.fused && d.tables <= kItemRoleMaxTables && nc >= 1 && item_bytes(1) <= 160 * 1024 && by_width &&
+                   (ste_mode & TROPNN_BWD_INPUT_GRAD_SCATTER) == 0;
         p.f_item_nc = nc;
         p.f_ir_rec_off = 0;
         p.f_ir_g_off = a16(nc * d.tables * 8);

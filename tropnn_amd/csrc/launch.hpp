@@ -128,7 +128,8 @@ constexpr int item_wave_tables(int esize, int vec) {
     return esize * vec <= 4 ? 16 : (esize * vec == 8 ? 12 : (esize == 4 ? 6 : 3));
 }
 
-// ste_mode: TROPNN_STE_MIN_MARGIN or TROPNN_STE_FULL (general path only).
+// ste_mode: TROPNN_STE_MIN_MARGIN or TROPNN_STE_FULL (general path only),
+// optionally with one TROPNN_BWD_INPUT_GRAD_* flag (fused path's item role).
 BackwardPlan plan_backward(const Dims &d, int ste_mode);
 
 hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, const int64_t *anchors,

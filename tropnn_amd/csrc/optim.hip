@@ -20,7 +20,8 @@ namespace tropnn {
 namespace {
 
 constexpr int kAdamThreads = 256;
-constexpr int kAdamMaxBlocks = 65536;  // a quad per thread up to 16 M quads
+constexpr int kAdamQuads = 2;          // quads per thread and round
+constexpr int kAdamMaxBlocks = 65536;  // one round up to 32 M quads
 
 struct AdamArgs {
     float *p[kAdamGroup];
@@ -59,70 +60,109 @@ __device__ __forceinline__ void adam_one(float &p, float g, float &m, float &v, 
     p = p - s.step_size * (m / denom);
 }
 
+// Scalar bias corrections of tensor k from its step counter, in f64 as torch
+// forms them on the host.
+__device__ __forceinline__ AdamScalars adam_scalars(const AdamArgs &a, float step) {
+    const double t = static_cast<double>(step + 1.f);
+    AdamScalars s;
+    s.step_size = static_cast<float>(a.lr / (1.0 - pow(a.b1, t)));
+    s.bc2_sqrt = static_cast<float>(sqrt(1.0 - pow(a.b2, t)));
+    return s;
+}
+
+// One quad (4 elements) of tensor k at element i, when its four pointers are
+// 16-byte aligned and the quad is whole; else element by element.
+__device__ __forceinline__ void adam_quad_general(const AdamArgs &a, const AdamScalars *sc, int64_t q) {
+    int k = 0;
+    while (k < a.n - 1 && q >= a.qstart[k + 1]) ++k;
+    const int64_t i = (q - a.qstart[k]) * 4;
+    const AdamScalars s = sc[k];
+    if ((a.vec_mask >> k & 1u) && i + 4 <= a.numel[k]) {
+        float4 p = *reinterpret_cast<const float4 *>(a.p[k] + i);
+        const float4 g = *reinterpret_cast<const float4 *>(a.g[k] + i);
+        float4 m = *reinterpret_cast<const float4 *>(a.m[k] + i);
+        float4 v = *reinterpret_cast<const float4 *>(a.v[k] + i);
+        adam_one(p.x, g.x, m.x, v.x, a, s);
+        adam_one(p.y, g.y, m.y, v.y, a, s);
+        adam_one(p.z, g.z, m.z, v.z, a, s);
+        adam_one(p.w, g.w, m.w, v.w, a, s);
+        *reinterpret_cast<float4 *>(a.p[k] + i) = p;
+        *reinterpret_cast<float4 *>(a.m[k] + i) = m;
+        *reinterpret_cast<float4 *>(a.v[k] + i) = v;
+    } else {
+        const int64_t end = i + 4 < a.numel[k] ? i + 4 : a.numel[k];
+        for (int64_t e = i; e < end; ++e) {
+            float p = a.p[k][e], m = a.m[k][e], v = a.v[k][e];
+            adam_one(p, a.g[k][e], m, v, a, s);
+            a.p[k][e] = p;
+            a.m[k][e] = m;
+            a.v[k][e] = v;
+        }
+    }
+}
+
+// A thread takes kAdamQuads quads per round, kAdamThreads apart (a wave's 64
+// quads of a round are consecutive). Every load of a round is issued before
+// the thread waits for any: in the first round also before the step counters
+// and the bias corrections the update needs, which wave 0 forms while the
+// data is in flight.
 __global__ __launch_bounds__(kAdamThreads) void adam_kernel(AdamArgs a) {
     __shared__ AdamScalars sc[kAdamGroup];
-    if (threadIdx.x < static_cast<unsigned>(a.n)) {
-        const double t = static_cast<double>(*a.steps[threadIdx.x] + 1.f);
-        sc[threadIdx.x].step_size = static_cast<float>(a.lr / (1.0 - pow(a.b1, t)));
-        sc[threadIdx.x].bc2_sqrt = static_cast<float>(sqrt(1.0 - pow(a.b2, t)));
-    }
-    __syncthreads();
     const int64_t total = a.qstart[a.n];
-    const int lane = threadIdx.x % 64;
-    int k = 0;  // the tensor holding quad q: quads only grow along the loop
-    for (int64_t q = blockIdx.x * static_cast<int64_t>(kAdamThreads) + threadIdx.x; q < total;
-         q += static_cast<int64_t>(gridDim.x) * kAdamThreads) {
-        // A wave's 64 quads are consecutive. When they lie in one tensor whose
-        // pointers are 16-byte aligned and none is its partial last quad (the
-        // common case), the tensor index and pointers are wave-uniform: scalar
-        // loads of the arguments instead of per-lane ones.
-        const int64_t qw = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(q - lane)) |
-                           (static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>((q - lane) >> 32))) << 32);
-        int kw = 0;
-        while (qw >= a.qstart[kw + 1]) ++kw;
-        if (qw + 64 <= a.qstart[kw + 1] && (a.vec_mask >> kw & 1u) && (qw + 64 - a.qstart[kw]) * 4 <= a.numel[kw]) {
-            const int64_t i = (q - a.qstart[kw]) * 4;
-            const AdamScalars s = sc[kw];
-            float *pp = a.p[kw], *mp = a.m[kw], *vp = a.v[kw];
-            const float *gp = a.g[kw];
-            float4 p = *reinterpret_cast<const float4 *>(pp + i);
-            const float4 g = *reinterpret_cast<const float4 *>(gp + i);
-            float4 m = *reinterpret_cast<const float4 *>(mp + i);
-            float4 v = *reinterpret_cast<const float4 *>(vp + i);
-            adam_one(p.x, g.x, m.x, v.x, a, s);
-            adam_one(p.y, g.y, m.y, v.y, a, s);
-            adam_one(p.z, g.z, m.z, v.z, a, s);
-            adam_one(p.w, g.w, m.w, v.w, a, s);
-            *reinterpret_cast<float4 *>(pp + i) = p;
-            *reinterpret_cast<float4 *>(mp + i) = m;
-            *reinterpret_cast<float4 *>(vp + i) = v;
-            continue;
-        }
-        while (q >= a.qstart[k + 1]) ++k;
-        const int64_t i = (q - a.qstart[k]) * 4;
-        const AdamScalars s = sc[k];
-        if ((a.vec_mask >> k & 1u) && i + 4 <= a.numel[k]) {
-            float4 p = *reinterpret_cast<const float4 *>(a.p[k] + i);
-            const float4 g = *reinterpret_cast<const float4 *>(a.g[k] + i);
-            float4 m = *reinterpret_cast<const float4 *>(a.m[k] + i);
-            float4 v = *reinterpret_cast<const float4 *>(a.v[k] + i);
-            adam_one(p.x, g.x, m.x, v.x, a, s);
-            adam_one(p.y, g.y, m.y, v.y, a, s);
-            adam_one(p.z, g.z, m.z, v.z, a, s);
-            adam_one(p.w, g.w, m.w, v.w, a, s);
-            *reinterpret_cast<float4 *>(a.p[k] + i) = p;
-            *reinterpret_cast<float4 *>(a.m[k] + i) = m;
-            *reinterpret_cast<float4 *>(a.v[k] + i) = v;
-        } else {
-            const int64_t end = i + 4 < a.numel[k] ? i + 4 : a.numel[k];
-            for (int64_t e = i; e < end; ++e) {
-                float p = a.p[k][e], m = a.m[k][e], v = a.v[k][e];
-                adam_one(p, a.g[k][e], m, v, a, s);
-                a.p[k][e] = p;
-                a.m[k][e] = m;
-                a.v[k][e] = v;
+    const int lane = threadIdx.x % kWave;
+    const bool counter = threadIdx.x < static_cast<unsigned>(a.n);
+    const float step = counter ? *a.steps[threadIdx.x] : 0.f;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * (kAdamThreads * kAdamQuads);
+    bool have_scalars = false;  // uniform
+    for (int64_t base = static_cast<int64_t>(blockIdx.x) * (kAdamThreads * kAdamQuads);; base += stride) {
+        // A wave whose 64 quads lie in one tensor with 16-byte aligned
+        // pointers, none of them its partial last quad (the common case),
+        // has a wave-uniform tensor index and pointers: scalar loads of the
+        // arguments instead of per-lane ones.
+        float4 p[kAdamQuads], g[kAdamQuads], m[kAdamQuads], v[kAdamQuads];
+        int kw[kAdamQuads];
+        bool fast[kAdamQuads];
+#pragma unroll
+        for (int u = 0; u < kAdamQuads; ++u) {
+            const int64_t q = base + u * kAdamThreads + threadIdx.x;
+            const int64_t qw = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(q - lane)) |
+                               (static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>((q - lane) >> 32))) << 32);
+            int k = 0;
+            while (k < a.n - 1 && qw >= a.qstart[k + 1]) ++k;
+            kw[u] = k;
+            fast[u] = qw + kWave <= a.qstart[k + 1] && (a.vec_mask >> k & 1u) && (qw + kWave - a.qstart[k]) * 4 <= a.numel[k];
+            if (fast[u]) {
+                const int64_t i = (q - a.qstart[k]) * 4;
+                p[u] = *reinterpret_cast<const float4 *>(a.p[k] + i);
+                g[u] = *reinterpret_cast<const float4 *>(a.g[k] + i);
+                m[u] = *reinterpret_cast<const float4 *>(a.m[k] + i);
+                v[u] = *reinterpret_cast<const float4 *>(a.v[k] + i);
             }
         }
+        if (!have_scalars) {
+            if (counter) sc[threadIdx.x] = adam_scalars(a, step);
+            __syncthreads();
+            have_scalars = true;
+        }
+#pragma unroll
+        for (int u = 0; u < kAdamQuads; ++u) {
+            const int64_t q = base + u * kAdamThreads + threadIdx.x;
+            if (fast[u]) {
+                const int k = kw[u];
+                const int64_t i = (q - a.qstart[k]) * 4;
+                const AdamScalars s = sc[k];
+                adam_one(p[u].x, g[u].x, m[u].x, v[u].x, a, s);
+                adam_one(p[u].y, g[u].y, m[u].y, v[u].y, a, s);
+                adam_one(p[u].z, g[u].z, m[u].z, v[u].z, a, s);
+                adam_one(p[u].w, g[u].w, m[u].w, v[u].w, a, s);
+                *reinterpret_cast<float4 *>(a.p[k] + i) = p[u];
+                *reinterpret_cast<float4 *>(a.m[k] + i) = m[u];
+                *reinterpret_cast<float4 *>(a.v[k] + i) = v[u];
+            } else if (q < total) {
+                adam_quad_general(a, sc, q);
+            }
+        }
+        if (base + stride >= total) break;
     }
 }
 
@@ -174,7 +214,7 @@ hipError_t launch_adam(int n, float *const *params, const float *const *grads, f
         a.decoupled = decoupled;
         const int64_t total = a.qstart[a.n];
         if (total == 0) continue;
-        int64_t blocks = (total + kAdamThreads - 1) / kAdamThreads;
+        int64_t blocks = (total + kAdamThreads * kAdamQuads - 1) / (kAdamThreads * kAdamQuads);
         if (blocks > kAdamMaxBlocks) blocks = kAdamMaxBlocks;
         hipLaunchKernelGGL(adam_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kAdamThreads), 0, stream, a);
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;

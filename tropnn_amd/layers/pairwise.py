@@ -15,7 +15,7 @@ import torch.nn as nn
 from torch import Tensor
 
 from ..backend import REFERENCE_BACKENDS, Backend
-from ..backends.pairwise_hip import pairwise_hip, pairwise_hip_route
+from ..backends.pairwise_hip import INPUT_GRAD_FORMS, pairwise_hip, pairwise_hip_route
 from .base import RoutedLinearBase
 from .surrogate import check_surrogate
 
@@ -36,6 +36,15 @@ class PairwiseLinear(RoutedLinearBase):
                         bump it) and cast afresh by every replay of a forward
                         captured in a HIP graph; gradients still go to the
                         f32 LUT.
+      input_grad        "auto" (default), "fused" or "scatter": where the
+                        backward forms the input gradient of narrow rows
+                        (out_features a multiple of 4 up to 64 or of 8 up
+                        to 256), in its first launch or in a kernel after it.
+                        "auto" decides by the row width, which is right for
+                        inputs whose codes spread over the LUT; "fused" pays
+                        where the items' codes concentrate on few rows, as in
+                        a layer fed by another PairwiseLinear. Results are
+                        bit-identical either way.
     Attribute `cache_route_debug` (default True, as the reference's shell
     assumes) keeps `_last_indices` [B,S,T] int64 and `_last_margins`
     [B,S,T,C] f32 of the last call; False skips writing them; "lazy" writes
@@ -62,6 +71,7 @@ class PairwiseLinear(RoutedLinearBase):
         surrogate: str = "fast_sigmoid_odd",
         cpu_lut_dtype: Literal["f32", "f16"] = "f32",
         device_lut_dtype: Literal["f32", "f16"] = "f32",
+        input_grad: Literal["auto", "fused", "scatter"] = "auto",
     ) -> None:
         if tables < 1:
             raise ValueError(f"tables must be >= 1, got {tables}")
@@ -77,6 +87,8 @@ class PairwiseLinear(RoutedLinearBase):
             raise ValueError(f"cpu_lut_dtype must be 'f32' or 'f16', got {cpu_lut_dtype!r}")
         if device_lut_dtype not in {"f32", "f16"}:
             raise ValueError(f"device_lut_dtype must be 'f32' or 'f16', got {device_lut_dtype!r}")
+        if input_grad not in INPUT_GRAD_FORMS:
+            raise ValueError(f"input_grad must be 'auto', 'fused' or 'scatter', got {input_grad!r}")
         check_surrogate(surrogate)
 
         output_scale = 1.0 / math.sqrt(tables) if use_output_scaling else 1.0
@@ -88,6 +100,7 @@ class PairwiseLinear(RoutedLinearBase):
         self.surrogate = surrogate
         self.cpu_lut_dtype = cpu_lut_dtype
         self.device_lut_dtype = device_lut_dtype
+        self.input_grad = input_grad
         self.cache_route_debug = True
         self._lut_f16: Tensor | None = None
         self._lut_f16_key: tuple | None = None
@@ -115,6 +128,7 @@ class PairwiseLinear(RoutedLinearBase):
             f"in_features={self.in_features}, out_features={self.out_features}, tables={self.tables}, "
             f"comparisons={self.comparisons}, backend={self.backend!r}, use_min_margin_ste={self.use_min_margin_ste}, "
             f"surrogate={self.surrogate!r}, device_lut_dtype={self.device_lut_dtype!r}"
+            + (f", input_grad={self.input_grad!r}" if self.input_grad != "auto" else "")
         )
 
     def _project_input(self, x: Tensor, compute_dtype: torch.dtype) -> Tensor:
@@ -163,6 +177,7 @@ class PairwiseLinear(RoutedLinearBase):
             lut_read=self._lut_for_reading(),
             ste=ste,
             return_route=self._route_mode(),
+            input_grad=self.input_grad,
         )
 
     def _route_mode(self) -> bool | str:
