@@ -582,6 +582,7 @@ def _eval_forward_gpu(layer, xs, steps: int, warmup: int) -> dict:
             ctr[0] += 1
 
     graph = time_windows(graph_window, steps, warmup)
+    abi = _abi_eval_windows(layer, xs, steps, warmup)
     evs = _kernel_events(("forward",), 100)["forward"]
     with torch.no_grad():
         for k, (e0, e1) in enumerate(evs):
@@ -590,8 +591,55 @@ def _eval_forward_gpu(layer, xs, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     kern = _spread([1e3 * e0.elapsed_time(e1) for e0, e1 in evs])
     return {"eager_us_per_call": eager["us_per_step"], "sync_latency_us": sync_us,
-            "graph_us_per_call": graph["us_per_step"], "kernel_us": kern["median"], "kernel_us_mean": kern["mean"],
-            "kernel_spread": kern, "eager_windows": eager, "graph_windows": graph}
+            "graph_us_per_call": graph["us_per_step"], "abi_us_per_call": abi["us_per_step"],
+            "kernel_us": kern["median"], "kernel_us_mean": kern["mean"],
+            "kernel_spread": kern, "eager_windows": eager, "graph_windows": graph, "abi_windows": abi}
+
+
+def _abi_eval_windows(layer, xs, steps: int, warmup: int) -> dict:
+    """The eval entry point of the C ABI (tropnn_hip_lut_forward_batch_f32 /
+    _f16, the Zig exports' counterpart) called the way cpu_zig_eval calls the
+    Zig-equivalent CPU forward: the LUT in the read dtype prepared once, per
+    call an output allocation and the call (through ctypes, on torch's
+    current stream), calls back to back on resident inputs. Both CPU and GPU
+    figures then leave out the module's Python (shared by every backend of
+    the reference's module)."""
+    import torch
+
+    from tropnn_amd.backends.pairwise_hip import load_library
+
+    lib = load_library()
+    w = layer._lut_for_reading().detach().contiguous()
+    f16 = w.dtype == torch.float16
+    fn = lib.tropnn_hip_lut_forward_batch_f16 if f16 else lib.tropnn_hip_lut_forward_batch_f32
+    anc = layer.anchors.contiguous()
+    thr = layer.thresholds.detach().contiguous()
+    b, i = xs[0].shape
+    t, c, o = layer.tables, layer.comparisons, layer.out_features
+    dev = xs[0].device
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    scale = float(layer.output_scale)
+    args = (t, c, i, o, w.data_ptr(), anc.data_ptr(), thr.data_ptr())
+    ptrs = [x.contiguous().data_ptr() for x in xs]
+    nb = len(xs)
+    ctr = [0]
+
+    def window() -> None:
+        for _ in range(steps):
+            out = torch.empty(b, o, dtype=torch.float32, device=dev)
+            rc = fn(b, *args, ptrs[ctr[0] % nb], out.data_ptr(), scale, stream)
+            if rc != 0:
+                raise RuntimeError(lib.tropnn_hip_last_error().decode())
+            ctr[0] += 1
+
+    # the ABI call gives the module's output (checked once)
+    out = torch.empty(b, o, dtype=torch.float32, device=dev)
+    fn(b, *args, ptrs[0], out.data_ptr(), scale, stream)
+    with torch.no_grad():
+        ref = layer(xs[0]).reshape(b, o)
+    if not torch.equal(out, ref):
+        raise AssertionError("the C ABI's eval forward differs from the module's")
+    return time_windows(window, steps, warmup)
 
 
 # ---------------------------------------------------------------- workloads
@@ -640,6 +688,7 @@ def bench_c1(args, dev) -> dict:
                    "[16,64,512], batch 8", "batch": b, "mode": "eager module calls under torch.no_grad"},
         "sync_latency_us": round(gpu["sync_latency_us"], 3),
         "graph_us_per_call": round(gpu["graph_us_per_call"], 3),
+        "abi_us_per_call": round(gpu["abi_us_per_call"], 3),
         "kernel_us": round(gpu["kernel_us"], 3),
         **window_fields(gpu["eager_windows"]),
         "roofline": roofline("forward", gpu["kernel_us_mean"], algo,
@@ -688,6 +737,7 @@ def bench_c3(args, dev) -> dict:
             "mode": mode,
             "eager_us_per_call": round(gpu["eager_us_per_call"], 3),
             "graph_us_per_call": round(gpu["graph_us_per_call"], 3),
+            "abi_us_per_call": round(gpu["abi_us_per_call"], 3),
             "sync_latency_us": round(gpu["sync_latency_us"], 3),
             **window_fields(gpu[f"{mode}_windows"]),
             "samples_per_s": round(b / (us * 1e-6), 1),
@@ -696,7 +746,7 @@ def bench_c3(args, dev) -> dict:
             "forward_peak_bytes": eval_peak_bytes(layer, xs[0], dev),
         }
         log(f"c3 batch {b}: graph {gpu['graph_us_per_call']:.2f} us/call, eager {gpu['eager_us_per_call']:.2f}, "
-            f"kernel {gpu['kernel_us']:.2f} us")
+            f"C ABI {gpu['abi_us_per_call']:.2f}, kernel {gpu['kernel_us']:.2f} us")
         if args.cpu_budget > 0:
             budget = min(args.cpu_budget, 4.0)
             cpus = [cpu_zig_eval(I, O, T, C, b, "f16", budget, "c3"), cpu_torch_eval(I, O, T, C, b, budget, "c3")]
@@ -1268,6 +1318,7 @@ def _cpu_us(cpus: list, path_prefix: str) -> float | None:
 def compact_c1(r: dict) -> dict:
     return {
         "us_per_call": r["value"], "graph_us_per_call": r["graph_us_per_call"],
+        "abi_us_per_call": r["abi_us_per_call"],
         "sync_latency_us": r["sync_latency_us"], "kernel_us": r["kernel_us"],
         "frac": r["roofline"]["frac"], "l2_hit_rate": r["roofline"]["l2_hit_rate"],
         "cpu_zig_us": _cpu_us(r["cpu_baselines"], "Zig"), "cpu_torch_us": _cpu_us(r["cpu_baselines"], "torch"),
@@ -1280,7 +1331,8 @@ def compact_c3(r: dict) -> dict:
     for b, res in r["per_batch"].items():
         cpus = res.get("cpu_baselines")
         out[f"b{b}"] = {
-            "us_per_call": res["us_per_call"], "mode": res["mode"], "kernel_us": res["kernel_us"],
+            "us_per_call": res["us_per_call"], "mode": res["mode"], "abi_us_per_call": res["abi_us_per_call"],
+            "kernel_us": res["kernel_us"],
             "samples_per_s": res["samples_per_s"], "cpu_zig_us": _cpu_us(cpus, "Zig"),
             "cpu_torch_us": _cpu_us(cpus, "torch"), "forward_peak_bytes": res["forward_peak_bytes"],
         }
