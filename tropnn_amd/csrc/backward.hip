@@ -1384,8 +1384,19 @@ __global__ __launch_bounds__(kFusedThreads) void pairwise_bwd_fused_kernel(Fused
                 if (nbk > 0 && gf == gl) continue;  // finished in the walk
                 vec_t<float, V> w = 0.f;
                 if (nbk > 0) {
+                    // a long row (codes concentrated on few rows) spans many
+                    // ranges: the pieces' reads go four at a time, the adds
+                    // stay in range order
                     w = *reinterpret_cast<const vec_t<float, V> *>(part + (gf * 2 + 1) * P + col);
-                    for (int gg = gf + 1; gg <= gl; ++gg) w += *reinterpret_cast<const vec_t<float, V> *>(part + gg * 2 * P + col);
+                    int gg = gf + 1;
+                    for (; gg + 3 <= gl; gg += 4) {
+                        vec_t<float, V> pc[4];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) pc[u] = *reinterpret_cast<const vec_t<float, V> *>(part + (gg + u) * 2 * P + col);
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) w += pc[u];
+                    }
+                    for (; gg <= gl; ++gg) w += *reinterpret_cast<const vec_t<float, V> *>(part + gg * 2 * P + col);
                 }
                 if (single) {
                     if (col_ok) {
