@@ -20,8 +20,10 @@ namespace tropnn {
 namespace {
 
 constexpr int kAdamThreads = 256;
-constexpr int kAdamQuads = 2;          // quads per thread and round
-constexpr int kAdamMaxBlocks = 65536;  // one round up to 32 M quads
+// quads per thread and round (c5 step: 1 quad 78.5 us, 2 quads 78.7 us, 4
+// quads 80.3 us; A/B on one box)
+constexpr int kAdamQuads = 1;
+constexpr int kAdamMaxBlocks = 65536;  // one round up to 16 M quads
 
 struct AdamArgs {
     float *p[kAdamGroup];
@@ -105,7 +107,8 @@ __device__ __forceinline__ void adam_quad_general(const AdamArgs &a, const AdamS
 // quads of a round are consecutive). Every load of a round is issued before
 // the thread waits for any: in the first round also before the step counters
 // and the bias corrections the update needs, which wave 0 forms while the
-// data is in flight.
+// data is in flight (before, the data loads waited for them: c5 step
+// 85.9 -> 84.2 us).
 __global__ __launch_bounds__(kAdamThreads) void adam_kernel(AdamArgs a) {
     __shared__ AdamScalars sc[kAdamGroup];
     const int64_t total = a.qstart[a.n];
