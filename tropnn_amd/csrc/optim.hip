@@ -107,8 +107,7 @@ __device__ __forceinline__ void adam_quad_general(const AdamArgs &a, const AdamS
 // quads of a round are consecutive). Every load of a round is issued before
 // the thread waits for any: in the first round also before the step counters
 // and the bias corrections the update needs, which wave 0 forms while the
-// data is in flight (before, the data loads waited for them: c5 step
-// 85.9 -> 84.2 us).
+// data is in flight.
 __global__ __launch_bounds__(kAdamThreads) void adam_kernel(AdamArgs a) {
     __shared__ AdamScalars sc[kAdamGroup];
     const int64_t total = a.qstart[a.n];
