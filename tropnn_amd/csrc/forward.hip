@@ -80,15 +80,12 @@ __device__ __forceinline__ Comparator load_comparator(const FwdArgs &p, int t, i
     return q;
 }
 
-// One DPP step of the min-margin argmin: keep the smaller 64-bit key of this
-// lane and its CTRL partner.
+// One DPP step of the min-margin argmin: the smaller key of this lane and
+// its CTRL partner.
 template <int CTRL>
-__device__ __forceinline__ void key_min_step(uint32_t &hi, uint32_t &lo) {
-    const uint32_t ohi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(hi), CTRL, 0xF, 0xF, false));
-    const uint32_t olo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(lo), CTRL, 0xF, 0xF, false));
-    const bool take = ohi < hi || (ohi == hi && olo < lo);
-    hi = take ? ohi : hi;
-    lo = take ? olo : lo;
+__device__ __forceinline__ uint32_t key_min_step(uint32_t key) {
+    const uint32_t other = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(key), CTRL, 0xF, 0xF, false));
+    return other < key ? other : key;
 }
 
 // Route record of a table, held by the lane that wins its min-margin pick.
@@ -115,16 +112,20 @@ __device__ __forceinline__ RouteOut route_ballot(const FwdArgs &p, const float *
     RouteOut r{0ull, false};
     if constexpr (TRAIN) {
         // torch.argmin over |m|: NaN first, then the smaller magnitude, then
-        // the lower comparison index. Key (hi, lo) = (0 for NaN else
-        // bits(|m|) + 1, c); padding lanes carry the largest key.
+        // the lower comparison index. Key = 0 for NaN else bits(|m|) + 1
+        // (below 2^31 + 2); padding lanes carry the largest key. The group's
+        // smallest key by a DPP butterfly, then the lowest lane holding it
+        // (the lowest comparison index) wins.
         const float mag = fabsf(m);
-        uint32_t hi = q.valid ? (mag != mag ? 0u : __builtin_bit_cast(uint32_t, mag) + 1u) : 0xFFFFFFFFu;
-        uint32_t lo = static_cast<uint32_t>(c);
+        const uint32_t key = q.valid ? (mag != mag ? 0u : __builtin_bit_cast(uint32_t, mag) + 1u) : 0xFFFFFFFFu;
+        uint32_t mn = key;
         const int lpt = 1 << p.lpt_log2;   // wave-uniform
-        if (lpt >= 2) key_min_step<0xB1>(hi, lo);   // quad_perm [1,0,3,2]
-        if (lpt >= 4) key_min_step<0x4E>(hi, lo);   // quad_perm [2,3,0,1]
-        if (lpt >= 8) key_min_step<0x141>(hi, lo);  // row_half_mirror
-        r.win = q.valid && lo == static_cast<uint32_t>(c);
+        if (lpt >= 2) mn = key_min_step<0xB1>(mn);   // quad_perm [1,0,3,2]
+        if (lpt >= 4) mn = key_min_step<0x4E>(mn);   // quad_perm [2,3,0,1]
+        if (lpt >= 8) mn = key_min_step<0x141>(mn);  // row_half_mirror
+        const uint64_t holders = __ballot(key == mn);  // lanes holding their group's smallest key
+        const uint32_t before = static_cast<uint32_t>(holders >> (slot << p.lpt_log2)) & ((1u << c) - 1u);
+        r.win = q.valid && key == mn && before == 0u;
         r.rec = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, m)) | (static_cast<uint64_t>(code) << 32) |
                 (static_cast<uint64_t>(c) << 48);
     }
