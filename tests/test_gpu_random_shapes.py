@@ -2,8 +2,9 @@
 wave-item) and both backward paths (fused, general; min-margin and full STE,
 both surrogates), f32 and f16 LUTs, against the CPU oracle: route codes
 exact, outputs and every gradient within the f32 tolerance (f16 LUT reads
-against the oracle run on the same RNE f16 copy of the LUT). A regression
-guard beside the hand-picked cases of test_gpu_parity."""
+against the oracle run on the same RNE f16 copy of the LUT), and the
+gradients also within it of the float64 closed forms (oracle/closed_form.py).
+A regression guard beside the hand-picked cases of test_gpu_parity."""
 from __future__ import annotations
 
 import random
@@ -13,6 +14,7 @@ import pytest
 import torch
 
 from oracle import routing_np
+from oracle.closed_form import gradients_f64
 from test_gpu_parity import DEV, F32_TOL, assert_train_parity, make_pair, rel_err, seeded, train_step
 
 pytestmark = pytest.mark.gpu
@@ -50,7 +52,14 @@ def test_random_shape(case):
     x = seeded((b, i), seed=b + c)
     if kind == "train":
         g = seeded((b, 1, o), seed=b + c + 1)
-        assert_train_parity(ref, hip, *train_step(ref, hip, x, g), tol=F32_TOL)
+        yx_ref, yx_hip = train_step(ref, hip, x, g)
+        assert_train_parity(ref, hip, yx_ref, yx_hip, tol=F32_TOL)
+        # and against the float64 closed forms on the same codes: the HIP
+        # gradients within 1e-5 of exact arithmetic, norm-wise
+        gx, gt, gl = gradients_f64(x, ref.anchors, ref.thresholds, ref.lut, g.reshape(b, o), min_margin=min_margin,
+                                   surrogate=surrogate, output_scale=1.0 / t ** 0.5)
+        for got, exact in ((yx_hip[1].grad, gx), (hip.thresholds.grad, gt), (hip.lut.grad, gl)):
+            assert rel_err(got.double(), exact) <= F32_TOL
         return
     hip.eval()
     with torch.no_grad():

@@ -303,3 +303,37 @@ def test_exact_zero_margin_gradient_closed_form(surrogate, sigma0, full):
     np.testing.assert_allclose(lut.grad.numpy(), want_lut, rtol=0, atol=0)
     if surrogate == "izhikevich":
         assert gu0 != 0.0  # the u = 0 branch carries a gradient
+
+
+@pytest.mark.parametrize("min_margin", [True, False])
+@pytest.mark.parametrize("surrogate", ["fast_sigmoid_odd", "izhikevich"])
+@pytest.mark.parametrize("sparse", [False, True])
+def test_closed_form_gradients_match_the_oracle_autograd(min_margin, surrogate, sparse):
+    """oracle/closed_form.py (float64 sums of the gradients' closed forms on
+    the forward's own codes) against the autograd of the torch restatement,
+    on shapes with ties and exact-zero margins (sparse input): two separate
+    statements of the same backward agree to f32 rounding, so neither drops
+    a term, a sign or an index the other keeps."""
+    from oracle.closed_form import gradients_f64
+
+    i, o, t, c, b = 20, 24, 9, 4, 64
+    ref = orc.OraclePairwiseLinear(i, o, tables=t, comparisons=c, seed=3, use_min_margin_ste=min_margin,
+                                   surrogate=surrogate).train()
+    gen = torch.Generator().manual_seed(21)
+    with torch.no_grad():
+        ref.thresholds.copy_(0.0 if sparse else 0.3 * torch.randn(t, c, generator=gen))
+    if sparse:
+        x = torch.rand(b, i, generator=gen) * (torch.rand(b, i, generator=gen) >= 0.8)
+    else:
+        x = torch.randn(b, i, generator=gen)
+    g = torch.randn(b, 1, o, generator=gen)
+    xr = x.clone().requires_grad_(True)
+    ref(xr).backward(g)
+    gx, gt, gl = gradients_f64(x, ref.anchors, ref.thresholds, ref.lut, g.reshape(b, o), min_margin=min_margin,
+                               surrogate=surrogate, output_scale=1.0 / math.sqrt(t))
+    for got, exact in ((xr.grad, gx), (ref.thresholds.grad, gt), (ref.lut.grad, gl)):
+        scale = float(exact.abs().max())
+        assert scale > 0
+        assert float((got.double() - exact).abs().max()) <= 1e-5 * scale
+    if sparse:
+        assert (torch.from_numpy(np.abs(ref._last_margins.numpy())) == 0).any()  # exact-zero margins ran
