@@ -128,7 +128,7 @@ class PairwiseLinear(RoutedLinearBase):
             f"in_features={self.in_features}, out_features={self.out_features}, tables={self.tables}, "
             f"comparisons={self.comparisons}, backend={self.backend!r}, use_min_margin_ste={self.use_min_margin_ste}, "
             f"surrogate={self.surrogate!r}, device_lut_dtype={self.device_lut_dtype!r}"
-            + (f", input_grad={self.input_grad!r}" if self.input_grad != "auto" else "")
+            + (f", input_grad={self.input_grad!r}" if getattr(self, "input_grad", "auto") != "auto" else "")
         )
 
     def _project_input(self, x: Tensor, compute_dtype: torch.dtype) -> Tensor:
@@ -177,7 +177,7 @@ class PairwiseLinear(RoutedLinearBase):
             lut_read=self._lut_for_reading(),
             ste=ste,
             return_route=self._route_mode(),
-            input_grad=self.input_grad,
+            input_grad=getattr(self, "input_grad", "auto"),  # modules pickled before the option
         )
 
     def _route_mode(self) -> bool | str:
