@@ -67,20 +67,23 @@ def _backward(noalloc, dims, g, lut, rec, margins, offsets, entries, ste_mode):
 
 
 @pytest.mark.parametrize(
-    "i,o,t,c,lut_dtype,full,sizes",
+    "i,o,t,c,lut_dtype,full,sizes,flag",
     [
-        (128, 128, 136, 6, "f32", False, (512, 200)),  # c2's layer: fused table kernel + scatter
-        (96, 300, 24, 6, "f16", False, (700, 257)),  # general path: sort, row, reduce, scatter
-        (64, 48, 20, 5, "f32", True, (600, 130)),  # full STE: item, sort, row
+        (128, 128, 136, 6, "f32", False, (512, 200), 0),  # c2's layer: fused table kernel + scatter
+        (128, 128, 136, 6, "f32", False, (512, 200), ph.BWD_INPUT_GRAD_FUSED),  # item role, no workspace
+        (128, 64, 40, 6, "f32", False, (300, 77), ph.BWD_INPUT_GRAD_SCATTER),  # narrow rows sent to the scatter
+        (96, 300, 24, 6, "f16", False, (700, 257), 0),  # general path: sort, row, reduce, scatter
+        (64, 48, 20, 5, "f32", True, (600, 130), 0),  # full STE: item, sort, row
     ],
 )
-def test_noalloc_backward_matches_workspace_backward(i, o, t, c, lut_dtype, full, sizes):
-    ste_mode = ph.STE_FULL if full else ph.STE_MIN_MARGIN
+def test_noalloc_backward_matches_workspace_backward(i, o, t, c, lut_dtype, full, sizes, flag):
+    ste_mode = (ph.STE_FULL if full else ph.STE_MIN_MARGIN) | flag
     lib = ph.load_library()
     for call, items in enumerate(sizes):
         ws_bytes = lib.tropnn_hip_pairwise_backward_workspace_size(items, i, o, t, c, 0, ste_mode)
         assert ws_bytes <= 32 << 20  # 0 for the fused path whose item role forms grad_latent
-        print(f"[noalloc] call {call}: items={items} i={i} o={o} t={t} c={c} {lut_dtype} full={full}", flush=True)
+        print(f"[noalloc] call {call}: items={items} i={i} o={o} t={t} c={c} {lut_dtype} full={full} flag={flag:#x}",
+              flush=True)
         inputs = _inputs(items, i, o, t, c, lut_dtype, full, seed=17 * call + items)
         dims = (items, i, o, t, c)
         ref = _backward(False, dims, *inputs, ste_mode)
