@@ -100,11 +100,18 @@ def test_in_place_change_of_a_saved_lut_is_detected():
 def test_library_errors_keep_their_python_exception_types():
     """Status codes of the C ABI raise as the ctypes bindings raise them:
     unsupported -> NotImplementedError, invalid argument -> ValueError."""
-    latent = torch.randn(2, 1, 8200, device=DEV)
+    latent = torch.randn(2, 1, 40, device=DEV)
     anchors = torch.zeros(3, 2, 2, dtype=torch.int64, device=DEV)
     thr = torch.zeros(3, 2, device=DEV)
-    with pytest.raises(NotImplementedError, match="8192"):
-        pairwise_hip(latent, anchors, thr, torch.zeros(3, 4, 5, device=DEV))
+    with pytest.raises(NotImplementedError, match="comparisons <= 8"):  # the operator's own check
+        pairwise_hip(latent, torch.zeros(3, 9, 2, dtype=torch.int64, device=DEV), torch.zeros(3, 9, device=DEV),
+                     torch.zeros(3, 512, 5, device=DEV))
+    # the library's TROPNN_ERR_UNSUPPORTED: two million one-comparison tables
+    # give the forward's waves code lists past a workgroup's LDS
+    many = 2_000_000
+    with pytest.raises(NotImplementedError, match="tables too many"):
+        pairwise_hip(latent[:1], torch.zeros(many, 1, 2, dtype=torch.int64, device=DEV),
+                     torch.zeros(many, 1, device=DEV), torch.zeros(many, 2, 1, device=DEV))
     with pytest.raises(ValueError, match="out_features"):
         pairwise_hip(latent[:, :, :16].contiguous(), anchors, thr, torch.zeros(3, 4, 0, device=DEV))
     with pytest.raises(TypeError, match="float32"):

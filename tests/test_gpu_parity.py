@@ -888,13 +888,18 @@ def test_backward_is_deterministic():
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("i,t,c", [(37, 29, 5), (2000, 300, 8), (8192, 600, 8), (1, 70, 3), (3, 700, 8)])
+@pytest.mark.parametrize(
+    "i,t,c",
+    [(37, 29, 5), (2000, 300, 8), (8192, 600, 8), (1, 70, 3), (3, 700, 8), (8193, 5, 2), (16384, 300, 8),
+     (20000, 40, 6)],
+)
 def test_anchor_index_matches_numpy(i, t, c):
-    """The inverse anchor index (a stable counting sort) against numpy: one
-    chunk of 1024 anchors, several chunks, in_features = 8192, one feature
-    (no feature bits to compare), and three features shared by 11,200
-    anchors (long runs of equal features inside every wave and across
-    chunks)."""
+    """The inverse anchor index (a stable counting sort over windows of 8192
+    features) against numpy: one chunk of 1024 anchors, several chunks,
+    in_features = 8192 (one whole window), one feature (no feature bits to
+    compare), three features shared by 11,200 anchors (long runs of equal
+    features inside every wave and across chunks), and two or three windows
+    (the last one of a single feature, two whole ones, a partial third)."""
     from tropnn_amd.backends.pairwise_hip import anchor_index
 
     gen = torch.Generator().manual_seed(3)

@@ -63,7 +63,6 @@ int make_dims(int64_t items, int64_t in_f, int64_t out_f, int64_t tables, int64_
     const int64_t rows = int64_t{1} << comps;
     if (items * tables > std::numeric_limits<int>::max() || tables * rows > std::numeric_limits<int>::max())
         return fail(TROPNN_ERR_UNSUPPORTED, "items*tables or tables*2^comparisons exceeds INT_MAX");
-    if (in_f > 8192) return fail(TROPNN_ERR_UNSUPPORTED, "in_features=%lld exceeds 8192", (long long)in_f);
     d.items = static_cast<int>(items);
     d.in_f = static_cast<int>(in_f);
     d.out_f = static_cast<int>(out_f);
@@ -235,8 +234,9 @@ int tropnn_hip_pairwise_forward(int64_t items, int64_t in_features, int64_t out_
     if ((route_record && misaligned(route_record, 8)) || (indices && misaligned(indices, 8)) ||
         (margins && misaligned(margins, 4)))
         return fail(TROPNN_ERR_INVALID_ARGUMENT, "route_record, indices and margins must be aligned to their element size");
-    if (p.lds_bytes > 64 * 1024)
-        return fail(TROPNN_ERR_UNSUPPORTED, "forward needs %d bytes of LDS (tables too large)", p.lds_bytes);
+    if (p.lds_bytes > tropnn::kMaxLdsBytes)
+        return fail(TROPNN_ERR_UNSUPPORTED, "forward needs more than %d bytes of LDS per workgroup (tables too many)",
+                    tropnn::kMaxLdsBytes);
     // the gather addresses the LUT through one buffer resource with 32-bit offsets
     const int64_t lut_bytes = int64_t{d.tables} * d.rows * d.out_f * (d.lut_dtype == TROPNN_LUT_F16 ? 2 : 4);
     if (lut_bytes > (int64_t{1} << 31))
@@ -371,13 +371,6 @@ int tropnn_hip_pairwise_backward(int64_t items, int64_t in_features, int64_t out
         if (p.workspace_bytes > 0 && misaligned(workspace, 16))
             return fail(TROPNN_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
     }
-    // an item's gu slots [T * C] and the inverse anchor index sit in one
-    // workgroup's LDS (160 KB on gfx950): 3 T C + in_f words, about 13,000
-    // (table, comparison) pairs at in_f = 128
-    if (p.item_lds_bytes > 160 * 1024)
-        return fail(TROPNN_ERR_UNSUPPORTED,
-                    "backward needs %d bytes of LDS per item, over the 160 KB of a workgroup (tables * comparisons "
-                    "or in_features too large)", p.item_lds_bytes);
     // grad rows and the LUT are addressed through buffer resources with 32-bit offsets
     const int64_t lut_bytes = int64_t{d.tables} * d.rows * d.out_f * esize;
     const int64_t g_bytes = int64_t{d.items} * d.out_f * 4;

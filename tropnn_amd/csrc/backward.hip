@@ -65,6 +65,7 @@
 //  A third, tiny kernel builds the inverse anchor index; callers rebuild it
 //  only when the anchors change.
 #include <atomic>
+#include <limits>
 #include <mutex>
 #include <type_traits>
 #include <unordered_map>
@@ -357,7 +358,7 @@ __global__ __launch_bounds__(1024) void pairwise_bwd_full_kernel(ItemArgs a) {
             const int t = tb + q;
             const float gu =
                 dot * surrogate_grad(a.margins[(static_cast<size_t>(b) * a.tables + t) * C + c], a.surrogate);
-            gud[t * C + c] = gu;
+            if (a.grad_x != nullptr) gud[t * C + c] = gu;  // (no LDS with the wide scatter kernel)
             if (a.gu != nullptr) a.gu[(static_cast<size_t>(t) * C + c) * a.items + b] = gu;
         }
     }
@@ -1519,59 +1520,115 @@ __global__ __launch_bounds__(kScatterThreads) void pairwise_bwd_scatter_kernel(S
     feature_walk(gud, idx_s, a.in_f, a.grad_x + static_cast<size_t>(b) * a.in_f, tid, kScatterThreads);
 }
 
+// Input gradient of inputs too wide (or tables too many) for an item's gu
+// slots and the inverse index to sit in LDS: one thread per (item, feature),
+// 256 consecutive features of one item per workgroup. The feature's entries
+// come from the index in global memory, each entry's value from the
+// records: min-margin {gu, r} [T][B] (gu where the entry's comparison is r,
+// else zero), full STE gu [T][C][B]. Summed in entry order with the LDS
+// walk's one-lane arithmetic (side 1 subtracts), so the values equal that
+// walk's wherever both apply.
+struct ScatterWideArgs {
+    const uint64_t *gurec;  // min-margin
+    const float *gu;        // full STE
+    const int32_t *index_offsets;
+    const int32_t *index_entries;
+    float *grad_x;
+    int items, in_f, comps, fblocks;
+};
+
+constexpr int kWideThreads = 256;
+
+template <bool FULL>
+__global__ __launch_bounds__(kWideThreads) void pairwise_bwd_scatter_wide_kernel(ScatterWideArgs a) {
+    const int b = blockIdx.x / a.fblocks;
+    const int f = (blockIdx.x - b * a.fblocks) * kWideThreads + threadIdx.x;
+    if (f >= a.in_f) return;
+    const int e0 = a.index_offsets[f], e1 = a.index_offsets[f + 1];
+    float gx = 0.f;
+    for (int e = e0; e < e1; ++e) {
+        const int k = a.index_entries[e];
+        const int tc = k >> 1;
+        float v;
+        if constexpr (FULL) {
+            v = a.gu[static_cast<size_t>(tc) * a.items + b];
+        } else {
+            const int t = tc / a.comps, c = tc - t * a.comps;
+            const uint64_t rr = a.gurec[static_cast<size_t>(t) * a.items + b];
+            v = static_cast<int>(rr >> 32) == c ? __builtin_bit_cast(float, static_cast<uint32_t>(rr)) : 0.f;
+        }
+        gx = gx + ((k & 1) ? -v : v);
+    }
+    __builtin_nontemporal_store(gx, a.grad_x + static_cast<size_t>(b) * a.in_f + f);
+}
+
 // Inverse anchor index: for every input feature f, the entries
 // ((t * C + c) << 1) | side of the anchors[t][c][side] equal to f, in
-// increasing order: a stable counting sort in one workgroup. LDS counts per
-// feature (integer atomics), one wave's exclusive scan gives the offsets, and
-// the entries are placed in chunks of 1024 in entry order: inside a wave the
-// lanes with the same feature are found with one ballot per feature bit (a
-// lane's rank is the number of such lanes below it), and the chunk's waves
-// take turns, each advancing the features' LDS cursors, so the order is fixed.
-// Anchors outside [0, in_f) are left out.
+// increasing order: a stable counting sort in one workgroup, over windows of
+// kIdxWindow features (one window unless the input is wider). Per window: LDS
+// counts per feature (integer atomics), one wave's exclusive scan gives the
+// offsets (after the entries of the windows before), and the window's entries
+// are placed in chunks of 1024 in entry order: inside a wave the lanes with
+// the same feature are found with one ballot per feature bit (a lane's rank
+// is the number of such lanes below it), and the chunk's waves take turns,
+// each advancing the features' LDS cursors, so the order is fixed. Anchors
+// outside [0, in_f) are left out.
 constexpr int kIdxThreads = 1024;
+constexpr int kIdxWindow = 8192;  // features per pass: their cursors in LDS
 
 __global__ __launch_bounds__(kIdxThreads) void anchor_index_kernel(const int64_t *anchors, int in_f, int tables,
                                                                   int comps, int32_t *offsets, int32_t *entries) {
     extern __shared__ __align__(16) unsigned char lds[];
-    int *cursor = reinterpret_cast<int *>(lds);  // [in_f + 1]: counts, then each feature's next position
+    int *cursor = reinterpret_cast<int *>(lds);  // [window + 1]: counts, then each feature's next position
     const int n = tables * comps * 2, tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    for (int f = tid; f <= in_f; f += kIdxThreads) cursor[f] = 0;
-    __syncthreads();
-    for (int k = tid; k < n; k += kIdxThreads) {
-        const int64_t v = anchors[k];
-        if (v >= 0 && v < in_f) atomicAdd(&cursor[v], 1);
-    }
-    __syncthreads();
-    if (tid < kWave) wave_exclusive_scan(cursor, in_f, tid);
-    __syncthreads();
-    for (int f = tid; f <= in_f; f += kIdxThreads) offsets[f] = cursor[f];
-    const int fbits = in_f > 1 ? 32 - __clz(in_f - 1) : 0;
     const uint64_t below = (1ull << lane) - 1ull, upto = below | (1ull << lane);
-    for (int k0 = 0; k0 < n; k0 += kIdxThreads) {
-        const int k = k0 + tid;
-        int v = -1;
-        if (k < n) {
-            const int64_t a = anchors[k];
-            v = a >= 0 && a < in_f ? static_cast<int>(a) : -1;
+    int placed = 0;  // entries of the windows before
+    for (int lo = 0; lo < in_f; lo += kIdxWindow) {
+        const int w = min(kIdxWindow, in_f - lo);
+        for (int f = tid; f <= w; f += kIdxThreads) cursor[f] = 0;
+        __syncthreads();
+        for (int k = tid; k < n; k += kIdxThreads) {
+            const int64_t v = anchors[k] - lo;
+            if (v >= 0 && v < w) atomicAdd(&cursor[v], 1);
         }
-        const bool valid = v >= 0;
-        uint64_t same = __ballot(valid);
-        for (int b = 0; b < fbits; ++b) {
-            const bool bit = (v >> b) & 1;
-            const uint64_t ones = __ballot(valid && bit);
-            same &= bit ? ones : ~ones;
+        __syncthreads();
+        if (tid < kWave) wave_exclusive_scan(cursor, w, tid);
+        __syncthreads();
+        for (int f = tid; f < w; f += kIdxThreads) {
+            cursor[f] += placed;
+            offsets[lo + f] = cursor[f];
         }
-        const int rank = __popcll(same & below);
-        const bool last = (same & ~upto) == 0;
-        for (int w = 0; w < kIdxThreads / kWave; ++w) {
-            if (wave == w && valid) {
-                const int pos = cursor[v] + rank;  // every lane reads before the group's last lane writes
-                entries[pos] = k;
-                if (last) cursor[v] = pos + 1;
+        const int here = cursor[w];  // the window's entries (cursor[w] is left alone above)
+        __syncthreads();
+        const int fbits = w > 1 ? 32 - __clz(w - 1) : 0;
+        for (int k0 = 0; k0 < n; k0 += kIdxThreads) {
+            const int k = k0 + tid;
+            int v = -1;
+            if (k < n) {
+                const int64_t a = anchors[k] - lo;
+                v = a >= 0 && a < w ? static_cast<int>(a) : -1;
             }
-            __syncthreads();
+            const bool valid = v >= 0;
+            uint64_t same = __ballot(valid);
+            for (int b = 0; b < fbits; ++b) {
+                const bool bit = (v >> b) & 1;
+                const uint64_t ones = __ballot(valid && bit);
+                same &= bit ? ones : ~ones;
+            }
+            const int rank = __popcll(same & below);
+            const bool last = (same & ~upto) == 0;
+            for (int wv = 0; wv < kIdxThreads / kWave; ++wv) {
+                if (wave == wv && valid) {
+                    const int pos = cursor[v] + rank;  // every lane reads before the group's last lane writes
+                    entries[pos] = k;
+                    if (last) cursor[v] = pos + 1;
+                }
+                __syncthreads();
+            }
         }
+        placed += here;
     }
+    if (tid == 0) offsets[in_f] = placed;
 }
 
 // Kernels that may need more than the default 64 KB of dynamic LDS opt in
@@ -1707,13 +1764,33 @@ hipError_t launch_fill_zero(float *p, size_t n, hipStream_t stream) {
 
 hipError_t launch_anchor_index(const int64_t *anchors, int in_f, int tables, int comps, int32_t *offsets,
                                int32_t *entries, hipStream_t stream) {
-    hipLaunchKernelGGL(anchor_index_kernel, dim3(1), dim3(kIdxThreads), (in_f + 1) * 4, stream, anchors, in_f,
-                       tables, comps, offsets, entries);
+    hipLaunchKernelGGL(anchor_index_kernel, dim3(1), dim3(kIdxThreads), (min(in_f, kIdxWindow) + 1) * 4, stream,
+                       anchors, in_f, tables, comps, offsets, entries);
     return hipGetLastError();
+}
+
+hipError_t launch_scatter_wide(const uint64_t *gurec, const float *gu, const int32_t *index_offsets,
+                               const int32_t *index_entries, float *grad_x, const Dims &d, hipStream_t stream) {
+    ScatterWideArgs s{};
+    s.gurec = gurec;
+    s.gu = gu;
+    s.index_offsets = index_offsets;
+    s.index_entries = index_entries;
+    s.grad_x = grad_x;
+    s.items = d.items;
+    s.in_f = d.in_f;
+    s.comps = d.comps;
+    s.fblocks = (d.in_f + kWideThreads - 1) / kWideThreads;
+    const long long blocks = static_cast<long long>(d.items) * s.fblocks;
+    if (blocks > std::numeric_limits<int>::max()) return hipErrorInvalidConfiguration;
+    auto kernel = gu != nullptr ? pairwise_bwd_scatter_wide_kernel<true> : pairwise_bwd_scatter_wide_kernel<false>;
+    return launch_kernel(TROPNN_KERNEL_BACKWARD_SCATTER, kernel, dim3(static_cast<unsigned>(blocks)),
+                         dim3(kWideThreads), 0, stream, s);
 }
 
 hipError_t launch_scatter(const uint64_t *gurec, const int32_t *index_offsets, const int32_t *index_entries,
                           float *grad_x, const Dims &d, const BackwardPlan &p, hipStream_t stream) {
+    if (p.wide_index) return launch_scatter_wide(gurec, nullptr, index_offsets, index_entries, grad_x, d, stream);
     ScatterArgs s{};
     s.gurec = gurec;
     s.index_offsets = index_offsets;
@@ -1784,7 +1861,14 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
     p.item_per_wave = (d.tables + w - 1) / w;
     p.item_waves = (d.tables + p.item_per_wave - 1) / p.item_per_wave;
     p.item_threads = p.item_waves * kWave;
-    p.item_lds_bytes = (d.tables * d.comps + d.in_f + 1 + 2 * d.tables * d.comps + kEntries) * 4;
+    // an item's gu slots [T * C] f32 and the inverse anchor index in LDS; past
+    // a workgroup's LDS (wide inputs, many tables) the input gradient is
+    // formed by the wide scatter kernel from the index and the records in
+    // global memory instead
+    const long long tc = static_cast<long long>(d.tables) * d.comps;
+    const long long item_lds = (tc + d.in_f + 1 + 2 * tc + kEntries) * 4;
+    p.wide_index = item_lds > kMaxLdsBytes;
+    p.item_lds_bytes = p.wide_index ? 0 : static_cast<int>(item_lds);
     p.scatter_lds_bytes = p.item_lds_bytes;
 
     // fused path: the row group spans the row, lanes own whole V-column
@@ -1826,32 +1910,33 @@ BackwardPlan plan_backward(const Dims &d, int ste_mode) {
         p.f_brow_off = off;
         off += (p.f_slots / batch + 1) * 4;
         p.f_lds_bytes = off;
-        p.fused = d.rows * p.fpitch * 4 <= 64 * 1024 && off <= 160 * 1024;
+        p.fused = d.rows * p.fpitch * 4 <= 64 * 1024 && off <= kMaxLdsBytes;
         // item role: the most items (up to kItemChunk) whose records [nc][T]
         // u64, G rows [nc][O] (+ one row pitch of zeros) and signed slots
         // [nc][T * C] f32, with the inverse anchor index, fit the table role's
         // LDS (or, for one item, up to 160 KB)
-        const int idx_bytes = (d.in_f + 1 + 2 * d.tables * d.comps + kEntries) * 4;
-        auto a16 = [](int v) { return (v + 15) & ~15; };
+        const long long idx_bytes = (d.in_f + 1 + 2 * tc + kEntries) * 4;
+        auto a16 = [](long long v) { return (v + 15) & ~15ll; };
         auto item_bytes = [&](int nc) {
-            return a16(nc * d.tables * 8) + a16((nc * d.out_f + p.fpitch) * 4) + a16(nc * d.tables * d.comps * 4) +
-                   idx_bytes;
+            return a16(nc * 8ll * d.tables) + a16((static_cast<long long>(nc) * d.out_f + p.fpitch) * 4) +
+                   a16(nc * 4ll * tc) + idx_bytes;
         };
-        const int cap = p.f_lds_bytes > item_bytes(1) ? p.f_lds_bytes : item_bytes(1);
+        const long long cap = p.f_lds_bytes > item_bytes(1) ? p.f_lds_bytes : item_bytes(1);
         int nc = 0;
         while (nc < kItemChunk && item_bytes(nc + 1) <= cap) ++nc;
         // (a caller's flag overrides the row-width rule, not the limits)
         const bool by_width = (ste_mode & TROPNN_BWD_INPUT_GRAD_FUSED) != 0 ||
                               static_cast<long long>(d.tables) * d.out_f * esize <=
                                   static_cast<long long>(kItemRoleRowBytes) * (kCus - d.tables);
-        p.f_item = p.fused && d.tables <= kItemRoleMaxTables && nc >= 1 && item_bytes(1) <= 160 * 1024 && by_width &&
+        p.f_item = p.fused && d.tables <= kItemRoleMaxTables && nc >= 1 && item_bytes(1) <= kMaxLdsBytes && by_width &&
                    (ste_mode & TROPNN_BWD_INPUT_GRAD_SCATTER) == 0;
         p.f_item_nc = nc;
         p.f_ir_rec_off = 0;
-        p.f_ir_g_off = a16(nc * d.tables * 8);
-        p.f_ir_gud_off = p.f_ir_g_off + a16((nc * d.out_f + p.fpitch) * 4);
-        p.f_ir_idx_off = p.f_ir_gud_off + a16(nc * d.tables * d.comps * 4);
-        p.f_launch_lds = p.f_item ? cap : p.f_lds_bytes;
+        // (offsets and sizes used only with the item role, within the LDS then)
+        p.f_ir_g_off = static_cast<int>(a16(nc * 8ll * d.tables));
+        p.f_ir_gud_off = p.f_ir_g_off + static_cast<int>(a16((static_cast<long long>(nc) * d.out_f + p.fpitch) * 4));
+        p.f_ir_idx_off = p.f_ir_gud_off + static_cast<int>(a16(nc * 4ll * tc));
+        p.f_launch_lds = p.f_item ? static_cast<int>(cap) : p.f_lds_bytes;
     }
     // workspace: fused path {gu, r} [T][B] u64; general path {gu, r} [T][B]
     // u64 (min-margin) or gu [T][C][B] f32 (full STE), then the sort
@@ -1961,8 +2046,10 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
         a.index_entries = index_entries;
         a.scale = scale;
         a.surrogate = surrogate;
-        a.grad_x = grad_x;
-        a.gu = grad_thr != nullptr ? workspace : nullptr;
+        // wide inputs: the kernel leaves every gu in the workspace and the
+        // wide scatter kernel forms grad_latent from them
+        a.grad_x = p.wide_index ? nullptr : grad_x;
+        a.gu = grad_thr != nullptr || (p.wide_index && grad_x != nullptr) ? workspace : nullptr;
         a.lut_bytes = static_cast<uint32_t>(static_cast<size_t>(d.tables) * d.rows * d.out_f * esize);
         a.g_bytes = g_bytes;
         a.items = d.items;
@@ -1991,6 +2078,10 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
             }
         }
         if (e != hipSuccess) return e;
+        if (p.wide_index && grad_x != nullptr) {
+            e = launch_scatter_wide(nullptr, workspace, index_offsets, index_entries, grad_x, d, stream);
+            if (e != hipSuccess) return e;
+        }
     }
     // min-margin: the row kernel forms the STE dots, so it runs whenever any
     // gradient is asked for; the full STE needs it for the LUT gradient only

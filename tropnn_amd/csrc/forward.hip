@@ -132,11 +132,13 @@ __device__ __forceinline__ RouteOut route_ballot(const FwdArgs &p, const float *
     return r;
 }
 
-template <typename T, int N, bool TRAIN, bool DEBUG>
+// XG (inputs too wide for LDS): the route reads the item's input row from
+// global memory instead of the LDS copy, and the LDS holds the code lists and
+// partial rows only. Same arithmetic, same outputs.
+template <typename T, int N, bool TRAIN, bool DEBUG, bool XG>
 __global__ __launch_bounds__(1024) void pairwise_forward_kernel(FwdArgs a) {
     constexpr int kG = gather_chunk(static_cast<int>(sizeof(T)), N);
     extern __shared__ __align__(16) unsigned char lds[];
-    float *xs = reinterpret_cast<float *>(lds);
     float *red = reinterpret_cast<float *>(lds + a.red_off);
 
     const int tid = threadIdx.x;
@@ -145,6 +147,9 @@ __global__ __launch_bounds__(1024) void pairwise_forward_kernel(FwdArgs a) {
     const int nwaves = blockDim.x >> 6;
     const int item = xcd_block_unit(blockIdx.x, gridDim.x);  // route records of adjacent items share lines
     uint8_t *my_codes = lds + a.codes_off + wave * a.codes_pitch;
+    const float *xrow = a.x + static_cast<size_t>(item) * a.in_f;
+    float *xl = reinterpret_cast<float *>(lds);
+    const float *xs = XG ? xrow : xl;
 
     const int tpb = kWave >> a.lpt_log2;
     const int slot = lane >> a.lpt_log2;
@@ -158,16 +163,15 @@ __global__ __launch_bounds__(1024) void pairwise_forward_kernel(FwdArgs a) {
     Comparator pre[kBallots];
 #pragma unroll
     for (int j = 0; j < kBallots; ++j) pre[j] = load_comparator(a, t_begin + j * tpb + slot, t_end, c);
-    {
-        const float *src = a.x + static_cast<size_t>(item) * a.in_f;
-        if ((a.in_f & 3) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    if constexpr (!XG) {
+        if ((a.in_f & 3) == 0 && (reinterpret_cast<uintptr_t>(xrow) & 15) == 0) {
             for (int k = tid; k < (a.in_f >> 2); k += blockDim.x)
-                reinterpret_cast<vec_t<float, 4> *>(xs)[k] = reinterpret_cast<const vec_t<float, 4> *>(src)[k];
+                reinterpret_cast<vec_t<float, 4> *>(xl)[k] = reinterpret_cast<const vec_t<float, 4> *>(xrow)[k];
         } else {
-            for (int k = tid; k < a.in_f; k += blockDim.x) xs[k] = src[k];
+            for (int k = tid; k < a.in_f; k += blockDim.x) xl[k] = xrow[k];
         }
+        __syncthreads();
     }
-    __syncthreads();
 
     // 2. route this wave's tables; codes go to the wave's LDS list, route
     //    records are stored after the last ballot (off the ballots' path)
@@ -253,6 +257,7 @@ __global__ __launch_bounds__(1024) void pairwise_forward_kernel(FwdArgs a) {
         store_f32_nt<N>(a.out + static_cast<size_t>(item) * a.out_f + col, y);
     }
 }
+
 
 // Large batches: one workgroup takes kMultiItems consecutive items (and one
 // output tile of 64 * N columns). Its waves load their comparators once for
@@ -923,8 +928,19 @@ hipError_t launch_typed(const FwdArgs &args, const ForwardPlan &p, bool train, b
             return launch_kernel(TROPNN_KERNEL_FORWARD, kernel, grid, block, p.lds_bytes, stream, args);
         }
     }
-    auto kernel = train ? (debug ? pairwise_forward_kernel<T, N, true, true> : pairwise_forward_kernel<T, N, true, false>)
-                        : (debug ? pairwise_forward_kernel<T, N, false, true> : pairwise_forward_kernel<T, N, false, false>);
+    if (p.wide_x) {
+        auto kernel = train ? (debug ? pairwise_forward_kernel<T, N, true, true, true>
+                                     : pairwise_forward_kernel<T, N, true, false, true>)
+                            : (debug ? pairwise_forward_kernel<T, N, false, true, true>
+                                     : pairwise_forward_kernel<T, N, false, false, true>);
+        if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void *>(kernel), p.lds_bytes); e != hipSuccess)
+            return e;
+        return launch_kernel(TROPNN_KERNEL_FORWARD, kernel, grid, block, p.lds_bytes, stream, args);
+    }
+    auto kernel = train ? (debug ? pairwise_forward_kernel<T, N, true, true, false>
+                                 : pairwise_forward_kernel<T, N, true, false, false>)
+                        : (debug ? pairwise_forward_kernel<T, N, false, true, false>
+                                 : pairwise_forward_kernel<T, N, false, false, false>);
     return launch_kernel(TROPNN_KERNEL_FORWARD, kernel, grid, block, p.lds_bytes, stream, args);
 }
 
@@ -974,19 +990,27 @@ ForwardPlan plan_forward(const Dims &d, bool rows16) {
     p.blocks = d.items;
     p.codes_pitch = ((p.per_wave + chunk - 1) / chunk) * chunk;
 
-    int off = ((d.in_f * 4) + 15) & ~15;
-    p.codes_off = off;
-    off += p.waves_per_item * p.codes_pitch;
-    off = (off + 15) & ~15;
-    p.red_off = off;
-    off += (p.waves_per_item - 1) * kWave * p.vec * 4;
-    p.lds_bytes = off;
+    // LDS: the item's input row (unless it would take the workgroup past the
+    // default 64 KB: then the route reads it from global memory), the waves'
+    // code lists, the waves' partial rows
+    auto one_item_lds = [&](long long x_bytes, int &codes_off, int &red_off) {
+        long long o = (x_bytes + 15) & ~15ll;
+        codes_off = static_cast<int>(o);
+        o += static_cast<long long>(p.waves_per_item) * p.codes_pitch;
+        o = (o + 15) & ~15ll;
+        red_off = static_cast<int>(o);
+        return o + static_cast<long long>(p.waves_per_item - 1) * kWave * p.vec * 4;
+    };
+    long long lds = one_item_lds(static_cast<long long>(d.in_f) * 4, p.codes_off, p.red_off);
+    p.wide_x = lds > 64 * 1024;
+    if (p.wide_x) lds = one_item_lds(0, p.codes_off, p.red_off);
+    p.lds_bytes = static_cast<int>(lds <= kMaxLdsBytes ? lds : kMaxLdsBytes + 1);  // above the maximum: refused
 
     // large batches: kMultiItems items per workgroup when every wave's
     // tables fit one gather chunk of 16 in at most kBallots ballots and a
     // lane's row chunk is at most 8 bytes
     p.multi = false;
-    if (d.items >= kMultiMinItems && p.vec * esize <= 8) {
+    if (d.items >= kMultiMinItems && p.vec * esize <= 8 && d.in_f <= 16384) {
         const int w16 = (d.tables + 15) / 16;
         const int per16 = (d.tables + w16 - 1) / w16;
         const int tpb = kWave >> p.lpt_log2;
@@ -1023,7 +1047,7 @@ ForwardPlan plan_forward(const Dims &d, bool rows16) {
         const bool pow2 = (tile & (tile - 1)) == 0;
         const int ipw = tile >= 128 ? kWave / (tile / 16) : 1;
         if (rows16 && d.items >= kWaveMinItems && (d.items + ipw - 1) / ipw >= kWaveMinWaves && tile >= 128 &&
-            pow2 && row_bytes % tile == 0) {
+            pow2 && row_bytes % tile == 0 && d.in_f <= 16384) {
             const int w16 = (d.tables + kWaveBlock - 1) / kWaveBlock;
             const int per16 = (d.tables + w16 - 1) / w16;
             const int lpr = tile / 16;
@@ -1056,7 +1080,7 @@ ForwardPlan plan_forward(const Dims &d, bool rows16) {
     // 16-byte aligned (LDS-direct 16-byte pieces)
     const long long lut_bytes = static_cast<long long>(d.tables) * d.rows * d.out_f * esize;
     p.stream_ok = rows16 && d.items >= kStreamMinItems && (d.out_f * esize) % kStreamChunkBytes == 0 &&
-                  d.rows <= 256 && lut_bytes >= kStreamMinLutBytes;
+                  d.rows <= 256 && lut_bytes >= kStreamMinLutBytes && d.in_f <= 16384;
     if (p.stream_ok) {
         p.stream_nblk = (d.items + kStreamItems - 1) / kStreamItems;
         p.stream_blocks = p.stream_nblk * (d.out_f * esize / kStreamChunkBytes);

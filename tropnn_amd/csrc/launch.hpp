@@ -22,6 +22,9 @@ struct Dims {
     int lut_dtype;  // TROPNN_LUT_F32 / TROPNN_LUT_F16
 };
 
+// LDS of one workgroup on gfx950.
+constexpr int kMaxLdsBytes = 160 * 1024;
+
 // Launch shape of the fused route + gather + scale forward.
 struct ForwardPlan {
     int vec;             // N: LUT elements per lane load (16 bytes at most)
@@ -36,6 +39,7 @@ struct ForwardPlan {
     int codes_off;       // LDS byte offsets
     int red_off;
     int lds_bytes;
+    bool wide_x;         // input row beyond the LDS budget: the one-item kernel reads it from global memory
     bool multi;          // large batch: several items per workgroup (blocks = ceil(items / kMultiItems))
     // wave-item kernel (large batch, 128..1024-byte row tiles): every wave
     // owns 64 / (tile bytes / 16) items; replaces the multi-item kernel
@@ -88,7 +92,8 @@ struct BackwardPlan {
     int item_per_wave;  // tables per wave
     int item_waves;     // waves per workgroup (one item per workgroup)
     int item_threads;
-    int item_lds_bytes; // the item's gu slots [T * C] f32 + the inverse anchor index
+    bool wide_index;    // gu slots and index past one workgroup's LDS: the wide scatter kernel forms grad_latent
+    int item_lds_bytes; // the item's gu slots [T * C] f32 + the inverse anchor index (0 with wide_index)
     bool full;          // full STE (every comparison): item kernel variant, general path only
     // fused path (O a multiple of 4 up to 64, or of 8 up to 256, a table's LUT
     // rows within 64 KB as f32): one kernel per table does the LUT gradient, the
