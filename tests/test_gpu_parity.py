@@ -744,6 +744,24 @@ def test_route_only_entry_point():
     assert c0.shape == (0, 1, 13) and i0.shape == (0, 1, 13) and m0.shape == (0, 1, 13, 7)
 
 
+def test_module_compute_indices():
+    """PairwiseLinear._compute_indices, the reference's route method
+    (layers/pairwise.py:127-135), on a [B, S, I] latent: int64 indices and f32
+    margins equal to the oracle's compute_route bit for bit, and to the
+    module's own forward debug cache."""
+    ref, hip = make_pair(40, 4, 13, 7, seed=6, thr_std=0.4)
+    x = seeded((3, 7, 40), seed=12)
+    idx, mar = hip._compute_indices(x.to(DEV))
+    want_idx, want_mar = orc.compute_route(x, ref.anchors, ref.thresholds.detach())
+    assert idx.dtype == torch.int64 and mar.dtype == torch.float32
+    assert torch.equal(idx.cpu(), want_idx)
+    assert torch.equal(mar.cpu().view(torch.int32), want_mar.view(torch.int32))
+    hip.eval()
+    with torch.no_grad():
+        hip(x.to(DEV))
+    assert torch.equal(hip._last_indices, idx) and torch.equal(hip._last_margins, mar)
+
+
 @pytest.mark.parametrize("min_margin", [True, False])
 def test_lazy_route_debug_training(min_margin):
     """Training with the lazy codes format gives the eager path's gradients;

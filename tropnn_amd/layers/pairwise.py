@@ -180,6 +180,19 @@ class PairwiseLinear(RoutedLinearBase):
             input_grad=getattr(self, "input_grad", "auto"),  # modules pickled before the option
         )
 
+    def _compute_indices(self, latent: Tensor) -> tuple[Tensor, Tensor]:
+        """Route only, as the reference's method of this name
+        (layers/pairwise.py:127-135): latent [B, S, I] f32 on the GPU ->
+        (indices int64 [B, S, T], margins f32 [B, S, T, C]), from the route
+        kernel (bit-identical to the forward's codes and margins). The margins
+        carry no autograd graph; training goes through forward()."""
+        if not latent.is_cuda:
+            raise ValueError("PairwiseLinear backend='hip' requires GPU input tensors")
+        _, indices, margins = pairwise_hip_route(
+            latent, self.anchors, self.thresholds.detach(), codes=False, indices=True, margins=True
+        )
+        return indices, margins
+
     def _route_mode(self) -> bool | str:
         mode = getattr(self, "cache_route_debug", True)
         return "codes" if mode == "lazy" else bool(mode)
