@@ -39,9 +39,43 @@ def _cases(seed: int, n: int):
     return out
 
 
+def _wide_cases(seed: int, n: int):
+    """Inputs past the kernels' LDS copies (12,000 to 45,000 features) and
+    many tables (2,000 to 3,500): the forward's global-memory input row, the
+    windowed anchor index and the wide scatter kernel."""
+    rng = random.Random(seed)
+    out = []
+    while len(out) < n:
+        kind = rng.choice(["eval", "train", "train", "train"])
+        if rng.random() < 0.5:
+            i, t = rng.choice([12000, 20000, 45000]), rng.choice([1, 9, 40])
+        else:
+            i, t = rng.choice([16, 64, 300]), rng.choice([2000, 3500])
+        c = rng.choice([1, 3, 5, 6, 8])
+        o = rng.choice([2, 10, 32, 64, 96, 300])
+        b = rng.choice([1, 5, 33, 300])
+        if t * (2**c) * o * 4 > (256 << 20) or b * t * o > 20_000_000 or b * i > 4_000_000:
+            continue  # keep the CPU oracle within seconds
+        out.append(
+            (kind, i, o, t, c, b, rng.choice(["f32", "f16"]), rng.random() < 0.7,
+             rng.choice(["fast_sigmoid_odd", "izhikevich"]), rng.choice([0.0, 0.3]))
+        )
+    return out
+
+
 @pytest.mark.parametrize("case", _cases(2024, 36), ids=lambda c: "-".join(str(v) for v in c))
 def test_random_shape(case):
+    _run(case)
+
+
+@pytest.mark.parametrize("case", _wide_cases(77, 16), ids=lambda c: "-".join(str(v) for v in c))
+def test_random_wide_shape(case):
+    _run(case)
+
+
+def _run(case):
     kind, i, o, t, c, b, lut_dtype, min_margin, surrogate, thr = case
+    print(f"[random shape] {case}", flush=True)
     ref, hip = make_pair(
         i, o, t, c, seed=i + o + t, thr_std=thr, lut_dtype=lut_dtype, use_min_margin_ste=min_margin,
         surrogate=surrogate,
