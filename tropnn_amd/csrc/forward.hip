@@ -12,7 +12,8 @@
 // batch sizes of interest, so each wave keeps its instruction count small and
 // issues every independent load before it waits:
 //   1. each wave loads the comparators of its first ballots while the
-//      workgroup stages the item's input row in LDS (one round trip);
+//      workgroup stages the item's input row in LDS (one round trip; a row
+//      too wide for LDS is read from global memory by the route instead);
 //   2. route: one wave ballot evaluates 64 / P of the wave's tables (P lanes
 //      per table, one comparison per lane, P = next power of two >= C); the
 //      P-bit fields of the ballot mask are the LUT row codes, which the table's
