@@ -43,6 +43,7 @@ CASES = [
     (50000, 300, 20, 5, 257, "f16", {}, "auto"),
     (50000, 48, 20, 5, 150, "f32", {"use_min_margin_ste": False}, "auto"),  # full STE + wide scatter (gu of every comparison)
     (64, 32, 3000, 6, 64, "f32", {}, "auto"),  # 18,000 (table, comparison) pairs: wide scatter at a narrow input
+    # 13,000 pairs: the full-STE item kernel's own walk with 156 KB of LDS, just inside a workgroup's
     (96, 40, 2600, 5, 48, "f32", {"use_min_margin_ste": False, "surrogate": "izhikevich"}, "auto"),
 ]
 
