@@ -108,6 +108,15 @@ def test_workspace_size(lib):
     assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_FULL | fused) == general(512, 128, 136, 64, 6, 64, True)
     assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_MIN_MARGIN | fused | scatter) == 0 and "flags" in _err(lib)
     assert ws(512, 128, 128, 136, 6, ph.LUT_F32, ph.STE_MIN_MARGIN | 0x400) == 0 and "flags" in _err(lib)
+    # wide inputs and many tables: past 160 KB of gu slots plus inverse index
+    # per item the item role is off and the wide scatter kernel reads the
+    # {gu, r} records (the FUSED flag does not lift that limit); below it the
+    # item role holds an 80 KB index
+    assert ws(300, 20000, 64, 24, 6, ph.LUT_F32, ph.STE_MIN_MARGIN) == 0
+    assert ws(200, 50000, 64, 24, 6, ph.LUT_F32, ph.STE_MIN_MARGIN) == 24 * 200 * 8
+    assert ws(200, 50000, 64, 24, 6, ph.LUT_F32, ph.STE_MIN_MARGIN | fused) == 24 * 200 * 8
+    assert ws(64, 64, 32, 3000, 6, ph.LUT_F32, ph.STE_MIN_MARGIN) == 3000 * 64 * 8
+    assert ws(150, 50000, 48, 20, 5, ph.LUT_F32, ph.STE_FULL) == general(150, 48, 20, 32, 5, 64, True)
 
 
 def _err(lib) -> str:
@@ -122,6 +131,10 @@ def test_forward_rejects_bad_arguments(lib):
     # comparisons above the supported maximum: unsupported, not invalid
     assert fwd(4, 8, 5, 3, 9, 8, 8, 8, 8, 0, 1.0, 8, None, None, None, None, None) == 2
     assert "comparisons" in _err(lib)
+    # no in_features limit of its own: a 100,000-feature input is checked like
+    # any other (here: its NULL latent)
+    assert fwd(4, 100000, 5, 3, 3, None, 8, 8, 8, 0, 1.0, 8, None, None, None, None, None) == 1
+    assert "non-NULL" in _err(lib)
     # unknown LUT dtype
     assert fwd(4, 8, 5, 3, 3, 8, 8, 8, 8, 7, 1.0, 8, None, None, None, None, None) == 1
     # NULL buffers
