@@ -973,13 +973,15 @@ def test_retain_graph_backward_twice():
 
 @pytest.mark.parametrize("lut_dtype,t,o", [("f32", 64, 512), ("f16", 128, 512)])
 def test_streamed_training_forward(lut_dtype, t, o):
-    """Large training shapes (>= 4096 items, rows of whole 64-column chunks,
+    """Large training shapes (>= 4096 items, rows of whole 64-byte chunks,
     a LUT of >= 32 MiB: here exactly 32 MiB) take the streamed forward: a
     route-record kernel, then per (item block, column chunk) workgroups that
-    walk the tables with each table's LUT chunk in LDS. Its output is
-    bit-identical to the eval forward's (the one-item kernel, same table
-    blocks), its route debug tensors to the eval forward's, and the training
-    step (4100 items: a partial last item block) matches the oracle."""
+    walk the tables with each table's LUT chunk in LDS. Its route debug
+    tensors are bit-identical to the eval forward's (the one-item kernel);
+    its output, a sum over the tables in table order, equals the eval
+    forward's to f32 rounding (that kernel sums its waves' blocks of tables)
+    and repeats bit for bit; the training step (4100 items: a partial last
+    item block) matches the oracle."""
     i, c, b = 64, 8, 4100
     ref, hip = make_pair(i, o, t, c, seed=1, thr_std=0.2, lut_dtype=lut_dtype)
     x = seeded((b, i), seed=3)
@@ -988,10 +990,13 @@ def test_streamed_training_forward(lut_dtype, t, o):
         y_eval = hip.eval()(x.to(DEV)).clone()
         idx_eval, mar_eval = hip._last_indices.clone(), hip._last_margins.clone()
     yx_ref, yx_hip = train_step(ref, hip, x, g)
-    assert torch.equal(yx_hip[0].detach(), y_eval)
+    y_train = yx_hip[0].detach()
+    assert rel_err(y_train, y_eval) <= 1e-6 and elem_err(y_train, y_eval) <= ELEM_RTOL
     assert torch.equal(hip._last_indices, idx_eval)
     assert torch.equal(hip._last_margins.view(torch.int32), mar_eval.view(torch.int32))
     assert_train_parity(ref, hip, yx_ref, yx_hip, tol=F16_TOL if lut_dtype == "f16" else F32_TOL)
+    # a second training forward (grad mode: the streamed path) repeats the sum bit for bit
+    assert torch.equal(hip.train()(x.to(DEV).requires_grad_(True)).detach(), y_train)
 
 
 @pytest.mark.parametrize(

@@ -709,18 +709,19 @@ __global__ __launch_bounds__(kRouteRecThreads) void pairwise_route_records_kerne
     }
 }
 
-// Streamed gather: one workgroup per (block of 512 items, chunk of 128 bytes
-// of every LUT row: 64 f16 or 32 f32 columns), the workgroups of a chunk
+// Streamed gather: one workgroup per (block of 2048 items, chunk of 64 bytes
+// of every LUT row: 32 f16 or 16 f32 columns), the workgroups of a chunk
 // adjacent on one XCD. The workgroup walks the tables in order with the
-// tables' LUT chunks (R rows x 128 bytes) and the items' codes in four LDS
+// tables' LUT chunks (R rows x 64 bytes) and the items' codes in four LDS
 // buffers, filled by LDS-direct loads (global_load_lds: no registers, no LDS
 // write instructions) three tables ahead. Thread (slot, piece) owns items
-// 4 slot .. 4 slot + 3 and one 16-byte piece of the chunk: per table four LDS
-// row reads and the adds. The workgroups of one chunk stream the same LUT
+// 8 slot .. 8 slot + 7 and one 16-byte piece of the chunk: per table eight
+// LDS row reads and the adds. The workgroups of one chunk stream the same LUT
 // chunks at about the same time, so the LUT crosses HBM about once instead of
-// once per (item, table) row gather. Tables are summed in blocks of the
-// one-item kernel's tables per wave, and the blocks in order, as that kernel
-// sums its waves: the outputs are bit-identical to it.
+// once per (item, table) row gather. Each item's row is summed over the tables
+// in table order: deterministic, but not the one-item kernel's association
+// (its waves' blocks), whose second set of accumulators would not fit the
+// registers beside eight items' rows.
 //   The buffers are four distinct LDS arrays and the table loop is unrolled
 // by four, so that the compiler tells them apart: a read of one buffer does
 // not wait for the LDS-direct loads still filling the others.
@@ -729,21 +730,21 @@ struct StreamArgs {
     const uint64_t *rec;
     float *out;
     float scale;
-    int items, out_f, tables, rows, nblk, block_tables;
+    int items, out_f, tables, rows, nblk;
 };
 
 constexpr int kStreamThreads = 1024;
-constexpr int kStreamChunkBytes = 128;                       // bytes of a LUT row in a chunk
+constexpr int kStreamChunkBytes = 64;                        // bytes of a LUT row in a chunk
 constexpr int kStreamPieces = kStreamChunkBytes / 16;        // 16-byte pieces of a row chunk
-constexpr int kStreamIpt = 4;                                // items per thread
+constexpr int kStreamIpt = 8;                                // items per thread
 constexpr int kStreamItems = kStreamThreads / kStreamPieces * kStreamIpt;  // items per workgroup
 constexpr int kStreamChunkLds = 256 * kStreamChunkBytes;     // one table's chunk, room for R = 256 rows
-// a buffer: the chunk, then one word per thread: the upper word of item
-// b0 + tid's route record (code | r << 16) for the first kStreamItems
-// threads, a repeat for the others (every thread issues the same loads)
-constexpr int kStreamBufBytes = kStreamChunkLds + kStreamThreads * 4;
+constexpr int kStreamRecLoads = kStreamItems / kStreamThreads;  // record words per thread per table
+// a buffer: the chunk, then one word per item: the upper word of its route
+// record (code | r << 16)
+constexpr int kStreamBufBytes = kStreamChunkLds + kStreamItems * 4;
 constexpr int kStreamAhead = 3;                              // tables in flight beside the one summed
-constexpr int kStreamLoads = kStreamChunkLds / 16 / kStreamThreads + 1;  // LDS-direct loads per thread per table
+constexpr int kStreamLoads = kStreamChunkLds / 16 / kStreamThreads + kStreamRecLoads;  // LDS-direct loads per thread per table
 constexpr int kStreamMinItems = 4096;
 constexpr long long kStreamMinLutBytes = 32ll << 20;
 
@@ -753,7 +754,7 @@ __global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel
     constexpr int COLS = kStreamChunkBytes / static_cast<int>(sizeof(T));
     constexpr int M = kStreamItems;
     constexpr int STAGE = kStreamChunkLds / 16 / kStreamThreads;  // chunk loads per thread per table
-    static_assert(kStreamLoads == STAGE + 1 && kStreamAhead == 3, "the wait below counts 2 tables of loads");
+    static_assert(kStreamLoads == 3 && kStreamAhead == 3, "the wait below counts 2 tables of loads");
     __shared__ __align__(16) unsigned char sb0[kStreamBufBytes];
     __shared__ __align__(16) unsigned char sb1[kStreamBufBytes];
     __shared__ __align__(16) unsigned char sb2[kStreamBufBytes];
@@ -767,16 +768,12 @@ __global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel
     const int wave = tid >> 6;
     const size_t row_bytes = static_cast<size_t>(a.out_f) * sizeof(T);
     const unsigned char *lut = static_cast<const unsigned char *>(a.lut) + static_cast<size_t>(chunk) * kStreamChunkBytes;
-    // upper word of the record of item b0 + (tid mod M) (past the batch: of
-    // the last item, never read), table 0
-    const uint32_t *rec_hi = reinterpret_cast<const uint32_t *>(a.rec) +
-                             2 * static_cast<size_t>(min(b0 + (tid & (M - 1)), a.items - 1)) + 1;
+    const uint32_t *rec_hi[kStreamRecLoads];
+#pragma unroll
+    for (int j = 0; j < kStreamRecLoads; ++j)
+        rec_hi[j] = reinterpret_cast<const uint32_t *>(a.rec) +
+                    2 * static_cast<size_t>(min(b0 + j * kStreamThreads + tid, a.items - 1)) + 1;
 
-    // table t's chunk into `buf`: piece q = tid + i * 1024 (row q / 8, piece
-    // q % 8) lands at byte 16 q, i.e. row-major with a 128-byte pitch, as
-    // lane l of a wave writes 16 bytes at the wave's base + 16 l. Rows past R
-    // load row R - 1 (in bounds) into buffer rows no code reads. Then the
-    // thread's record word.
     auto issue_table = [&](int t, unsigned char *buf) {
         const unsigned char *base = lut + static_cast<size_t>(t) * R * row_bytes;
 #pragma unroll
@@ -786,37 +783,35 @@ __global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel
                                              (__attribute__((address_space(3))) void *)(buf + (i * kStreamThreads + wave * kWave) * 16),
                                              16, 0, 0);
         }
-        __builtin_amdgcn_global_load_lds(rec_hi + 2 * static_cast<size_t>(t) * a.items,
-                                         (__attribute__((address_space(3))) void *)(buf + kStreamChunkLds + wave * kWave * 4),
-                                         4, 0, 0);
+#pragma unroll
+        for (int j = 0; j < kStreamRecLoads; ++j)
+            __builtin_amdgcn_global_load_lds(rec_hi[j] + 2 * static_cast<size_t>(t) * a.items,
+                                             (__attribute__((address_space(3))) void *)(buf + kStreamChunkLds + (j * kStreamThreads + wave * kWave) * 4),
+                                             4, 0, 0);
     };
 
-    float blk_acc[kStreamIpt][PE], tot[kStreamIpt][PE];
+    float acc[kStreamIpt][PE];
 #pragma unroll
     for (int k = 0; k < kStreamIpt; ++k)
 #pragma unroll
-        for (int e = 0; e < PE; ++e) blk_acc[k][e] = tot[k][e] = 0.f;
-    int first_block = 1;
-    int next_block_end = min(a.block_tables, a.tables);  // the table count at which the current block ends
+        for (int e = 0; e < PE; ++e) acc[k][e] = 0.f;
 
-    // step t: table t has landed in every wave (the loads of the two tables
-    // issued after it may still be in flight: 2 * kStreamLoads), the
-    // workgroup meets, table t's codes and rows are read, table t + 3's loads
-    // are issued into the buffer of table t - 1 (read by every thread before
-    // the meeting), and table t is summed. Past the last table the loads
-    // repeat it, so that every step waits for the same count.
     auto step = [&](int t, const unsigned char *cur, unsigned char *nxt) {
         asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         const bool live = t < a.tables;  // workgroup-uniform
         vec_t<uint32_t, 4> w[kStreamIpt];
         if (live) {
-            const vec_t<uint32_t, 4> cv = *reinterpret_cast<const vec_t<uint32_t, 4> *>(cur + kStreamChunkLds + slot * 16);
 #pragma unroll
-            for (int k = 0; k < kStreamIpt; ++k)
-                w[k] = *reinterpret_cast<const vec_t<uint32_t, 4> *>(cur + (cv[k] & static_cast<uint32_t>(R - 1)) * kStreamChunkBytes + piece * 16);
+            for (int h = 0; h < kStreamIpt / 4; ++h) {
+                const vec_t<uint32_t, 4> cv =
+                    *reinterpret_cast<const vec_t<uint32_t, 4> *>(cur + kStreamChunkLds + slot * kStreamIpt * 4 + h * 16);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    w[4 * h + k] = *reinterpret_cast<const vec_t<uint32_t, 4> *>(
+                        cur + (cv[k] & static_cast<uint32_t>(R - 1)) * kStreamChunkBytes + piece * 16);
+            }
         }
-        // the reads stay ahead of the next loads
         __builtin_amdgcn_sched_barrier(0);
         issue_table(min(t + kStreamAhead, a.tables - 1), nxt);
         if (live) {
@@ -825,31 +820,14 @@ __global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel
                 if constexpr (sizeof(T) == 2) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        blk_acc[k][2 * e] = add_f16_mix<false>(blk_acc[k][2 * e], w[k][e]);
-                        blk_acc[k][2 * e + 1] = add_f16_mix<true>(blk_acc[k][2 * e + 1], w[k][e]);
+                        acc[k][2 * e] = add_f16_mix<false>(acc[k][2 * e], w[k][e]);
+                        acc[k][2 * e + 1] = add_f16_mix<true>(acc[k][2 * e + 1], w[k][e]);
                     }
                 } else {
-                    // the whole vector, then its elements: hipcc bit-casts an
-                    // element of an ext_vector_type value as its first element
                     const vec_t<float, 4> f = __builtin_bit_cast(vec_t<float, 4>, w[k]);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) blk_acc[k][e] += f[e];
+                    for (int e = 0; e < 4; ++e) acc[k][e] += f[e];
                 }
-            }
-            if (t + 1 == next_block_end) {
-                // a branch, once per block: without the barrier the compiler
-                // turns the block sum into selects run at every table (three
-                // times the adds' own instructions)
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int k = 0; k < kStreamIpt; ++k)
-#pragma unroll
-                    for (int e = 0; e < PE; ++e) {
-                        tot[k][e] = first_block ? blk_acc[k][e] : tot[k][e] + blk_acc[k][e];
-                        blk_acc[k][e] = 0.f;
-                    }
-                first_block = 0;
-                next_block_end = min(next_block_end + a.block_tables, a.tables);
             }
         }
     };
@@ -863,7 +841,6 @@ __global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel
         step(t0 + 2, sb2, sb1);
         step(t0 + 3, sb3, sb2);
     }
-    // no LDS-direct load may still be writing when the workgroup ends
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     const int col = chunk * COLS + piece * PE;
 #pragma unroll
@@ -872,7 +849,7 @@ __global__ __launch_bounds__(kStreamThreads) void pairwise_forward_stream_kernel
         if (b < a.items) {
             float y[PE];
 #pragma unroll
-            for (int e = 0; e < PE; ++e) y[e] = tot[k][e] * a.scale;
+            for (int e = 0; e < PE; ++e) y[e] = acc[k][e] * a.scale;
             store_f32_nt<PE>(a.out + static_cast<size_t>(b) * a.out_f + col, y);
         }
     }
@@ -947,7 +924,7 @@ hipError_t launch_typed(const FwdArgs &args, const ForwardPlan &p, bool train, b
 
 template <typename T>
 hipError_t launch_stream(const StreamArgs &args, const ForwardPlan &p, hipStream_t stream) {
-    // the LDS buffers are static (4 x 36 KB)
+    // the LDS buffers are static (4 x 24 KB)
     return launch_kernel(TROPNN_KERNEL_FORWARD, pairwise_forward_stream_kernel<T>, dim3(p.stream_blocks),
                          dim3(kStreamThreads), 0, stream, args);
 }
@@ -1077,7 +1054,7 @@ ForwardPlan plan_forward(const Dims &d, bool rows16) {
 
     // streamed gather (training only: it reads the codes from the route
     // records): large batches over a LUT far beyond the L2, rows of whole
-    // 64-column chunks, at most 256 rows per table, the LUT and the output
+    // 64-byte chunks, at most 256 rows per table, the LUT and the output
     // 16-byte aligned (LDS-direct 16-byte pieces)
     const long long lut_bytes = static_cast<long long>(d.tables) * d.rows * d.out_f * esize;
     p.stream_ok = rows16 && d.items >= kStreamMinItems && (d.out_f * esize) % kStreamChunkBytes == 0 &&
@@ -1134,7 +1111,7 @@ hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, c
                                          dim3(kRouteRecThreads), p.route_lds, stream, r);
             e != hipSuccess)
             return e;
-        StreamArgs g{lut, a.rec, out, scale, d.items, d.out_f, d.tables, d.rows, p.stream_nblk, p.per_wave};
+        StreamArgs g{lut, a.rec, out, scale, d.items, d.out_f, d.tables, d.rows, p.stream_nblk};
         return d.lut_dtype == TROPNN_LUT_F16 ? launch_stream<_Float16>(g, p, stream) : launch_stream<float>(g, p, stream);
     }
     if (p.wave)
