@@ -977,11 +977,11 @@ def test_streamed_training_forward(lut_dtype, t, o):
     a LUT of >= 32 MiB: here exactly 32 MiB) take the streamed forward: a
     route-record kernel, then per (item block, column chunk) workgroups that
     walk the tables with each table's LUT chunk in LDS. Its route debug
-    tensors are bit-identical to the eval forward's (the one-item kernel);
-    its output, a sum over the tables in table order, equals the eval
-    forward's to f32 rounding (that kernel sums its waves' blocks of tables)
-    and repeats bit for bit; the training step (4100 items: a partial last
-    item block) matches the oracle."""
+    tensors are bit-identical to the eval forward's (a kernel that routes and
+    gathers in one launch); its output, a sum over the tables in table order,
+    equals the eval forward's to f32 rounding (that kernel sums blocks of
+    tables, then the blocks) and repeats bit for bit; the training step (4100
+    items: a partial last item block) matches the oracle."""
     i, c, b = 64, 8, 4100
     ref, hip = make_pair(i, o, t, c, seed=1, thr_std=0.2, lut_dtype=lut_dtype)
     x = seeded((b, i), seed=3)
