@@ -1583,8 +1583,8 @@ __global__ __launch_bounds__(kIdxThreads) void anchor_index_kernel(const int64_t
     const int n = tables * comps * 2, tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const uint64_t below = (1ull << lane) - 1ull, upto = below | (1ull << lane);
     int placed = 0;  // entries of the windows before
-    for (int lo = 0; lo < in_f; lo += kIdxWindow) {
-        const int w = min(kIdxWindow, in_f - lo);
+    for (int lo = 0, w = 0; lo < in_f; lo += w) {  // lo + w <= in_f: no overflow at any in_f
+        w = min(kIdxWindow, in_f - lo);
         for (int f = tid; f <= w; f += kIdxThreads) cursor[f] = 0;
         __syncthreads();
         for (int k = tid; k < n; k += kIdxThreads) {
@@ -1780,7 +1780,7 @@ hipError_t launch_scatter_wide(const uint64_t *gurec, const float *gu, const int
     s.items = d.items;
     s.in_f = d.in_f;
     s.comps = d.comps;
-    s.fblocks = (d.in_f + kWideThreads - 1) / kWideThreads;
+    s.fblocks = static_cast<int>((static_cast<long long>(d.in_f) + kWideThreads - 1) / kWideThreads);
     const long long blocks = static_cast<long long>(d.items) * s.fblocks;
     if (blocks > std::numeric_limits<int>::max()) return hipErrorInvalidConfiguration;
     auto kernel = gu != nullptr ? pairwise_bwd_scatter_wide_kernel<true> : pairwise_bwd_scatter_wide_kernel<false>;
