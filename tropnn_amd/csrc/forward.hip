@@ -671,13 +671,41 @@ __global__ __launch_bounds__(kRouteRecThreads) void pairwise_route_records_kerne
     extern __shared__ __align__(16) float xs[];  // [block_items][in_f]
     const int b0 = blockIdx.x * a.block_items, n = min(a.block_items, a.items - b0);
     const float *src = a.x + static_cast<size_t>(b0) * a.in_f;
-    for (int k = threadIdx.x; k < n * a.in_f; k += kRouteRecThreads) xs[k] = src[k];
+    const int total = n * a.in_f, tid = threadIdx.x;
+    // the rows in 16-byte pieces, eight loads per thread in flight before
+    // their LDS stores (one or two round trips, not one per piece)
+    constexpr int kU = 8;
+    if ((a.in_f & 3) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+        const vec_t<float, 4> *s4 = reinterpret_cast<const vec_t<float, 4> *>(src);
+        vec_t<float, 4> *d4 = reinterpret_cast<vec_t<float, 4> *>(xs);
+        const int n4 = total >> 2;
+        for (int k0 = tid; k0 < n4; k0 += kU * kRouteRecThreads) {
+            vec_t<float, 4> v[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u)
+                if (k0 + u * kRouteRecThreads < n4) v[u] = s4[k0 + u * kRouteRecThreads];
+#pragma unroll
+            for (int u = 0; u < kU; ++u)
+                if (k0 + u * kRouteRecThreads < n4) d4[k0 + u * kRouteRecThreads] = v[u];
+        }
+    } else {
+        for (int k0 = tid; k0 < total; k0 += kU * kRouteRecThreads) {
+            float v[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u)
+                if (k0 + u * kRouteRecThreads < total) v[u] = src[k0 + u * kRouteRecThreads];
+#pragma unroll
+            for (int u = 0; u < kU; ++u)
+                if (k0 + u * kRouteRecThreads < total) xs[k0 + u * kRouteRecThreads] = v[u];
+        }
+    }
     __syncthreads();
-    for (int t = threadIdx.x; t < a.tables; t += kRouteRecThreads) {
+    for (int t = tid; t < a.tables; t += kRouteRecThreads) {
         int ia[TROPNN_MAX_COMPARISONS], ib[TROPNN_MAX_COMPARISONS];
         float th[TROPNN_MAX_COMPARISONS];
-        for (int c = 0; c < a.comps; ++c) {
-            const size_t q = static_cast<size_t>(t) * a.comps + c;
+#pragma unroll
+        for (int c = 0; c < TROPNN_MAX_COMPARISONS; ++c) {
+            const size_t q = static_cast<size_t>(t) * a.comps + (c < a.comps ? c : 0);
             ia[c] = clamp_index(a.anchors[2 * q], a.in_f);
             ib[c] = clamp_index(a.anchors[2 * q + 1], a.in_f);
             th[c] = a.thr[q];
