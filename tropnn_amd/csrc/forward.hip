@@ -1091,7 +1091,7 @@ ForwardPlan plan_forward(const Dims &d, bool rows16) {
         p.stream_nblk = (d.items + kStreamItems - 1) / kStreamItems;
         p.stream_blocks = p.stream_nblk * (d.out_f * esize / kStreamChunkBytes);
         p.stream_lds = 4 * kStreamBufBytes;  // static
-        p.route_block_items = 16;
+        p.route_block_items = 8;
         while (p.route_block_items > 1 && p.route_block_items * d.in_f * 4 > 64 * 1024) p.route_block_items >>= 1;
         p.route_lds = p.route_block_items * d.in_f * 4;
     }
