@@ -240,6 +240,25 @@ __device__ __forceinline__ int index_word(const int32_t *offs, const int32_t *en
     return k <= in_f ? offs[k] : (k - in_f - 1 < n_ent ? ents[k - in_f - 1] : 0);
 }
 
+// Words [k_begin, nidx) of the index into idx_s, kStageWords per thread in
+// flight (all loaded, then all stored): a few round trips instead of one per
+// word of a large index.
+constexpr int kStageWords = 8;
+__device__ __forceinline__ void stage_index(int *idx_s, const int32_t *offs, const int32_t *ents, int in_f, int n_ent,
+                                            int k_begin, int nidx, int tid, int nthr) {
+    for (int k0 = k_begin + tid; k0 < nidx; k0 += kStageWords * nthr) {
+        int iv[kStageWords];
+#pragma unroll
+        for (int q = 0; q < kStageWords; ++q) {
+            const int k = k0 + q * nthr;
+            iv[q] = k < nidx ? index_word(offs, ents, in_f, n_ent, k) : 0;
+        }
+#pragma unroll
+        for (int q = 0; q < kStageWords; ++q)
+            if (k0 + q * nthr < nidx) idx_s[k0 + q * nthr] = iv[q];
+    }
+}
+
 // grad_x row of one item: the item's signed gu slots gud[(t * C + c)] named
 // by feature f's entries of the inverse anchor index (staged in LDS as
 // index_word lays it out), summed in entry order; side 1 subtracts. A batch
@@ -311,7 +330,7 @@ __global__ __launch_bounds__(1024) void pairwise_bwd_full_kernel(ItemArgs a) {
     const int n_ent = 2 * a.tables * C;
     const int nidx = a.grad_x != nullptr ? a.in_f + 1 + n_ent + kEntries : 0;
     int *idx_s = reinterpret_cast<int *>(gud + a.tables * C);  // [in_f + 1 + 2 T C + kEntries]
-    for (int k = tid; k < nidx; k += nthr) idx_s[k] = index_word(a.index_offsets, a.index_entries, a.in_f, n_ent, k);
+    stage_index(idx_s, a.index_offsets, a.index_entries, a.in_f, n_ent, 0, nidx, tid, nthr);
 
     const __amdgpu_buffer_rsrc_t lut_rsrc = buffer_rsrc(a.lut, a.lut_bytes);
     const __amdgpu_buffer_rsrc_t g_rsrc = buffer_rsrc(a.grad_out, a.g_bytes);
@@ -1487,6 +1506,9 @@ struct ScatterArgs {
 
 constexpr int kScatterIndex = 8;  // index words per thread in flight
 
+// BIG: an index longer than the first loads' kScatterIndex words per thread
+// (c4: 9,233 words), whose rest is staged eight words per thread at a time.
+template <bool BIG>
 __global__ __launch_bounds__(kScatterThreads) void pairwise_bwd_scatter_kernel(ScatterArgs a) {
     extern __shared__ __align__(16) unsigned char lds[];
     const int C = a.comps;
@@ -1514,8 +1536,9 @@ __global__ __launch_bounds__(kScatterThreads) void pairwise_bwd_scatter_kernel(S
             for (int c = 0; c < C; ++c) gud[tt * C + c] = c == r ? gu : 0.f;
         }
     }
-    for (int k = tid + kScatterIndex * kScatterThreads; k < nidx; k += kScatterThreads)
-        idx_s[k] = index_word(a.index_offsets, a.index_entries, a.in_f, n_ent, k);
+    if constexpr (BIG)
+        stage_index(idx_s, a.index_offsets, a.index_entries, a.in_f, n_ent, kScatterIndex * kScatterThreads, nidx,
+                    tid, kScatterThreads);
     __syncthreads();
     feature_walk(gud, idx_s, a.in_f, a.grad_x + static_cast<size_t>(b) * a.in_f, tid, kScatterThreads);
 }
@@ -1800,8 +1823,11 @@ hipError_t launch_scatter(const uint64_t *gurec, const int32_t *index_offsets, c
     s.in_f = d.in_f;
     s.tables = d.tables;
     s.comps = d.comps;
-    if (hipError_t e = allow_lds(pairwise_bwd_scatter_kernel, p.scatter_lds_bytes); e != hipSuccess) return e;
-    return launch_kernel(TROPNN_KERNEL_BACKWARD_SCATTER, pairwise_bwd_scatter_kernel, dim3(d.items),
+    const long long nidx = d.in_f + 1 + 2ll * d.tables * d.comps + kEntries;
+    auto kernel = nidx > kScatterIndex * kScatterThreads ? pairwise_bwd_scatter_kernel<true>
+                                                         : pairwise_bwd_scatter_kernel<false>;
+    if (hipError_t e = allow_lds(kernel, p.scatter_lds_bytes); e != hipSuccess) return e;
+    return launch_kernel(TROPNN_KERNEL_BACKWARD_SCATTER, kernel, dim3(d.items),
                          dim3(kScatterThreads), p.scatter_lds_bytes, stream, s);
 }
 
