@@ -165,6 +165,7 @@ struct ReduceArgs {
     int surrogate;
     int items, chunks, comps, rows, slots;
     int item_shift;        // slot offset >> item_shift = item (offsets are item * P * 4)
+    int stage;             // gurec's records of a table gathered in LDS first (items * 8 bytes of dynamic LDS)
 };
 
 __device__ __forceinline__ int rec_code(uint64_t r) { return static_cast<int>((r >> 32) & 0xffffu); }
@@ -871,10 +872,15 @@ __global__ __launch_bounds__(rows_threads(DOTS, sizeof(T))) void pairwise_bwd_ro
 // tree per wave, waves in order, tiles in order: slots in sorted order).
 // Padding slots carry no gu.
 constexpr int kReduceThreads = 1024;
+constexpr int kReduceStageBytes = 64 * 1024;  // a table's {gu, r} records staged in LDS up to 8192 items
 
 __global__ __launch_bounds__(kReduceThreads) void pairwise_bwd_reduce_kernel(ReduceArgs a) {
     constexpr int kWaves = kReduceThreads / kWave;
     __shared__ float tp[kWaves * 8];
+    // with `stage`, the table's {gu, r} records gather in LDS (in item order)
+    // and leave as whole lines after the walk, instead of as scattered
+    // 8-byte stores
+    extern __shared__ __align__(16) uint64_t gstage[];  // [items]
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint64_t *rec_t = a.rec + static_cast<size_t>(t) * a.items;
@@ -903,9 +909,13 @@ __global__ __launch_bounds__(kReduceThreads) void pairwise_bwd_reduce_kernel(Red
         }
         const int r = rec_r(rr) & 7;  // the slot's low bits may hold the neighbour row instead
         const float gu = live ? dot * a.scale * surrogate_grad(rec_u(rr), a.surrogate) : 0.f;
-        if (live && a.gurec != nullptr)
-            a.gurec[static_cast<size_t>(t) * a.items + b] =
-                static_cast<uint64_t>(__builtin_bit_cast(uint32_t, gu)) | (static_cast<uint64_t>(r) << 32);
+        if (live && a.gurec != nullptr) {
+            const uint64_t out = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, gu)) | (static_cast<uint64_t>(r) << 32);
+            if (a.stage)
+                gstage[b] = out;
+            else
+                a.gurec[static_cast<size_t>(t) * a.items + b] = out;
+        }
         if (a.grad_thr != nullptr) {
             float tv[8];
 #pragma unroll
@@ -914,8 +924,10 @@ __global__ __launch_bounds__(kReduceThreads) void pairwise_bwd_reduce_kernel(Red
             if ((lane & 7) == 0) tp[wave * 8 + (lane >> 3)] += sum;
         }
     }
+    if (a.stage || a.grad_thr != nullptr) __syncthreads();
+    if (a.stage)  // every item of the table had one live slot
+        for (int k = tid; k < a.items; k += kReduceThreads) a.gurec[static_cast<size_t>(t) * a.items + k] = gstage[k];
     if (a.grad_thr != nullptr) {
-        __syncthreads();
         if (tid < a.comps) {
             float sum = tp[tid];
             for (int w = 1; w < kWaves; ++w) sum += tp[w * 8 + tid];
@@ -2176,8 +2188,9 @@ hipError_t launch_backward(const Dims &d, const BackwardPlan &p, const float *gr
     ra.items = d.items;
     ra.chunks = p.rows_chunks;
     ra.comps = d.comps;
+    ra.stage = ra.gurec != nullptr && d.items <= kReduceStageBytes / 8;
     if (hipError_t e = launch_kernel(TROPNN_KERNEL_BACKWARD_REDUCE, pairwise_bwd_reduce_kernel, dim3(d.tables),
-                                     dim3(kReduceThreads), 0, stream, ra);
+                                     dim3(kReduceThreads), ra.stage ? d.items * 8 : 0, stream, ra);
         e != hipSuccess || grad_x == nullptr)
         return e;
     return launch_scatter(ra.gurec, index_offsets, index_entries, grad_x, d, p, stream);
