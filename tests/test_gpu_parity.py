@@ -93,7 +93,7 @@ def train_step(ref, hip, x, g, *, x_grad=True):
     return (y_ref, x_ref), (y_hip, x_hip)
 
 
-def assert_train_parity(ref, hip, yx_ref, yx_hip, tol=F32_TOL, x_grad=True):
+def assert_train_parity(ref, hip, yx_ref, yx_hip, tol=F32_TOL, x_grad=True, elem_rtol=ELEM_RTOL):
     (y_ref, x_ref), (y_hip, x_hip) = yx_ref, yx_hip
     assert torch.equal(hip._last_indices.cpu(), ref._last_indices), "route codes differ"
     errs = {
@@ -117,8 +117,8 @@ def assert_train_parity(ref, hip, yx_ref, yx_hip, tol=F32_TOL, x_grad=True):
         if x_grad:
             pairs["grad_x"] = (x_hip.grad, x_ref.grad)
         elem = {k: elem_err(h, r) for k, (h, r) in pairs.items()}
-        bad = {k: v for k, v in elem.items() if not v <= ELEM_RTOL}
-        assert not bad, f"element-wise beyond {ELEM_RTOL}: {bad} (all: {elem})"
+        bad = {k: v for k, v in elem.items() if not v <= elem_rtol}
+        assert not bad, f"element-wise beyond {elem_rtol}: {bad} (all: {elem})"
     return errs
 
 
@@ -971,7 +971,9 @@ def test_retain_graph_backward_twice():
     assert rel_err(first[0], x_ref.grad) <= F32_TOL
 
 
-@pytest.mark.parametrize("lut_dtype,t,o,c", [("f32", 64, 512, 8), ("f16", 128, 512, 8), ("f32", 256, 512, 6)])
+@pytest.mark.parametrize(
+    "lut_dtype,t,o,c", [("f32", 64, 512, 8), ("f16", 128, 512, 8), ("f32", 256, 512, 6), ("f32", 1100, 128, 6)]
+)
 def test_streamed_training_forward(lut_dtype, t, o, c):
     """Large training shapes (>= 4096 items, rows of whole 64-byte chunks,
     a LUT of >= 32 MiB: here exactly 32 MiB) take the streamed forward: a
@@ -983,7 +985,9 @@ def test_streamed_training_forward(lut_dtype, t, o, c):
     tables, then the blocks) and repeats bit for bit; the training step (4100
     items: a partial last item block) matches the oracle. With 64-row tables
     (C = 6) the staged chunks' rows past the table repeat its last row and no
-    code reads them."""
+    code reads them. The route kernel gathers a block's records in LDS when
+    they fit beside its input rows (T * 8 items * 8 bytes); 1100 tables
+    (70 KB of records) take its direct stores."""
     i, b = 64, 4100
     ref, hip = make_pair(i, o, t, c, seed=1, thr_std=0.2, lut_dtype=lut_dtype)
     x = seeded((b, i), seed=3)
@@ -993,10 +997,14 @@ def test_streamed_training_forward(lut_dtype, t, o, c):
         idx_eval, mar_eval = hip._last_indices.clone(), hip._last_margins.clone()
     yx_ref, yx_hip = train_step(ref, hip, x, g)
     y_train = yx_hip[0].detach()
-    assert rel_err(y_train, y_eval) <= 1e-6 and elem_err(y_train, y_eval) <= ELEM_RTOL
+    # two f32 summation orders of t terms: the norm-wise gap grows as sqrt(t) eps,
+    # an element's worst case (cancellation) as t eps
+    assert rel_err(y_train, y_eval) <= max(1e-6, 4 * 2.0**-24 * t**0.5)
+    elem_rtol = ELEM_RTOL * max(1.0, t / 256)
+    assert elem_err(y_train, y_eval) <= elem_rtol
     assert torch.equal(hip._last_indices, idx_eval)
     assert torch.equal(hip._last_margins.view(torch.int32), mar_eval.view(torch.int32))
-    assert_train_parity(ref, hip, yx_ref, yx_hip, tol=F16_TOL if lut_dtype == "f16" else F32_TOL)
+    assert_train_parity(ref, hip, yx_ref, yx_hip, tol=F16_TOL if lut_dtype == "f16" else F32_TOL, elem_rtol=elem_rtol)
     # a second training forward (grad mode: the streamed path) repeats the sum bit for bit
     assert torch.equal(hip.train()(x.to(DEV).requires_grad_(True)).detach(), y_train)
 

@@ -663,13 +663,16 @@ struct RouteRecArgs {
     float *margins;
     uint8_t *codes;
     int items, in_f, tables, comps, block_items;
+    int rec_stage;  // the block's records gathered in LDS after its input rows, then stored as whole runs
 };
 
 constexpr int kRouteRecThreads = 512;
+constexpr int kRouteStageBytes = 64 * 1024;  // rows plus staged records, two workgroups per CU
 
 __global__ __launch_bounds__(kRouteRecThreads) void pairwise_route_records_kernel(RouteRecArgs a) {
-    extern __shared__ __align__(16) float xs[];  // [block_items][in_f]
+    extern __shared__ __align__(16) float xs[];  // [block_items][in_f], then (rec_stage) records [T][block_items]
     const int b0 = blockIdx.x * a.block_items, n = min(a.block_items, a.items - b0);
+    uint64_t *rs = reinterpret_cast<uint64_t *>(xs + ((a.block_items * a.in_f + 3) & ~3));
     const float *src = a.x + static_cast<size_t>(b0) * a.in_f;
     const int total = n * a.in_f, tid = threadIdx.x;
     // the rows in 16-byte pieces, eight loads per thread in flight before
@@ -728,11 +731,23 @@ __global__ __launch_bounds__(kRouteRecThreads) void pairwise_route_records_kerne
                 }
                 if (a.margins != nullptr) a.margins[bt * a.comps + c] = mg;
             }
-            a.rec[static_cast<size_t>(t) * a.items + b0 + m] = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, best_m)) |
-                                                             (static_cast<uint64_t>(code) << 32) |
-                                                             (static_cast<uint64_t>(best) << 48);
+            const uint64_t rec = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, best_m)) |
+                                 (static_cast<uint64_t>(code) << 32) | (static_cast<uint64_t>(best) << 48);
+            if (a.rec_stage)
+                rs[t * a.block_items + m] = rec;
+            else
+                a.rec[static_cast<size_t>(t) * a.items + b0 + m] = rec;
             if (a.indices != nullptr) a.indices[bt] = code;
             if (a.codes != nullptr) a.codes[bt] = static_cast<uint8_t>(code);
+        }
+    }
+    if (a.rec_stage) {
+        // a table's n records are one contiguous run of rec: consecutive
+        // lanes store consecutive records of a run
+        __syncthreads();
+        for (int k = tid; k < a.tables * n; k += kRouteRecThreads) {
+            const int t = k / n, m = k - t * n;
+            a.rec[static_cast<size_t>(t) * a.items + b0 + m] = rs[t * a.block_items + m];
         }
     }
 }
@@ -1094,6 +1109,10 @@ ForwardPlan plan_forward(const Dims &d, bool rows16) {
         p.route_block_items = 8;
         while (p.route_block_items > 1 && p.route_block_items * d.in_f * 4 > 64 * 1024) p.route_block_items >>= 1;
         p.route_lds = p.route_block_items * d.in_f * 4;
+        const long long rec_lds = static_cast<long long>(d.tables) * p.route_block_items * 8;
+        const int x_lds = ((p.route_block_items * d.in_f + 3) & ~3) * 4;
+        p.route_rec_stage = x_lds + rec_lds <= kRouteStageBytes;
+        if (p.route_rec_stage) p.route_lds = x_lds + static_cast<int>(rec_lds);
     }
     return p;
 }
@@ -1133,7 +1152,7 @@ hipError_t launch_forward(const Dims &d, const ForwardPlan &p, const float *x, c
     const bool debug = indices != nullptr || margins != nullptr || codes != nullptr;
     if (train && p.stream_ok) {
         RouteRecArgs r{x, anchors, thr, a.rec, indices, margins, codes, d.items, d.in_f, d.tables, d.comps,
-                       p.route_block_items};
+                       p.route_block_items, p.route_rec_stage ? 1 : 0};
         if (hipError_t e = launch_kernel(TROPNN_KERNEL_FORWARD_ROUTE, pairwise_route_records_kernel,
                                          dim3((d.items + p.route_block_items - 1) / p.route_block_items),
                                          dim3(kRouteRecThreads), p.route_lds, stream, r);

@@ -59,6 +59,7 @@ struct ForwardPlan {
     int stream_lds;
     int route_block_items;  // items per route workgroup (their input rows in LDS)
     int route_lds;
+    bool route_rec_stage;  // the route records gathered in LDS before their stores
 };
 
 // Launch shape of the backward. General path, min-margin STE: the sort kernel
