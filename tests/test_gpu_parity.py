@@ -279,6 +279,7 @@ def test_c2_north_star_config():
         (48, 128, 12, 6, 2100, 0.1),
         (24, 200, 9, 6, 1500, 0.3),
         (20, 100, 6, 4, 40, 0.2),
+        (64, 300, 8, 5, 9000, 0.2),  # general path past 8192 items: the reduce kernel's direct record stores
     ],
 )
 def test_train_parity(i, o, t, c, b, thr_std):
