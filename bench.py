@@ -421,8 +421,8 @@ WINDOW_FLOORS = {"windows": 25, "steps": 100, "seconds": 0.2, "warmup_s": 0.3}
 
 def time_windows(window, steps: int, warmup: int, min_windows: int | None = None, min_steps: int | None = None,
                  min_seconds: float | None = None) -> dict:
-    """Device time per step, measured the way BASELINE.md plans it (the median
-    over >= 100 steps). window() issues one window of `steps` steps without
+    """Device time per step as the median over >= 100 steps (the benchmark
+    plan for c2). window() issues one window of `steps` steps without
     waiting for them. After >= `warmup` warmup windows and >= 0.3 s of them
     (the GPU clocks ramp up under sustained load), n windows are issued back
     to back with no host synchronisation between them and a HIP event
@@ -1025,8 +1025,8 @@ def bench_c4(args, dev) -> dict:
             step(ctr[0] % nb)
             ctr[0] += 1
 
-    # steps take milliseconds: at least 5 windows and 10 steps (BASELINE.md's
-    # >= 10 for c4), no time floor
+    # steps take milliseconds: at least 5 windows and 10 steps (the benchmark
+    # plan's >= 10 for c4), no time floor
     tw = time_windows(window, args.steps, 0, min_windows=5, min_steps=10, min_seconds=0.0)
     step_ms = tw["us_per_step"] * 1e-3
     # per-kernel durations over further steps, from events each kernel's own
