@@ -973,11 +973,19 @@ def test_retain_graph_backward_twice():
 
 
 @pytest.mark.parametrize(
-    "lut_dtype,t,o,c", [("f32", 64, 512, 8), ("f16", 128, 512, 8), ("f32", 256, 512, 6), ("f32", 1100, 128, 6)]
+    "lut_dtype,t,o,c,i",
+    [
+        ("f32", 64, 512, 8, 64),
+        ("f16", 128, 512, 8, 64),
+        ("f32", 256, 512, 6, 64),
+        ("f32", 1100, 128, 6, 64),
+        ("f16", 128, 512, 8, 37),  # input rows off 16-byte boundaries: the route kernel's 4-byte staging
+        ("f32", 64, 512, 8, 3000),  # 12 KB rows: 4 items per route workgroup
+    ],
 )
-def test_streamed_training_forward(lut_dtype, t, o, c):
+def test_streamed_training_forward(lut_dtype, t, o, c, i):
     """Large training shapes (>= 4096 items, rows of whole 64-byte chunks,
-    a LUT of >= 32 MiB: here exactly 32 MiB) take the streamed forward: a
+    a LUT of >= 32 MiB: here 32 MiB, 1100 tables 34 MiB) take the streamed forward: a
     route-record kernel, then per (item block, column chunk) workgroups that
     walk the tables with each table's LUT chunk in LDS. Its route debug
     tensors are bit-identical to the eval forward's (a kernel that routes and
@@ -989,7 +997,7 @@ def test_streamed_training_forward(lut_dtype, t, o, c):
     code reads them. The route kernel gathers a block's records in LDS when
     they fit beside its input rows (T * 8 items * 8 bytes); 1100 tables
     (70 KB of records) take its direct stores."""
-    i, b = 64, 4100
+    b = 4100
     ref, hip = make_pair(i, o, t, c, seed=1, thr_std=0.2, lut_dtype=lut_dtype)
     x = seeded((b, i), seed=3)
     g = seeded((b, 1, o), seed=4)
