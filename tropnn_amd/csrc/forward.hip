@@ -490,7 +490,7 @@ __global__ __launch_bounds__(kWaveThreads) void pairwise_forward_wave_kernel(Fwd
     // 2. route: lane = table (lanes past the last table idle), its C
     // comparisons in order, each read of an input giving all P items' values
     const bool tile0 = blockIdx.y == 0;
-    for (int t0 = 0; t0 < a.tables; t0 += kWave) {
+    auto route = [&](int t0) {
         const int t = t0 + lane;
         if (t < a.tables) {
             const int tblk = t / a.per_wave;
@@ -548,8 +548,13 @@ __global__ __launch_bounds__(kWaveThreads) void pairwise_forward_wave_kernel(Fwd
                 }
             }
         }
-    }
-    // LDS operations of one wave complete in order: its code lists are ready
+    };
+    // The first 64 tables are routed, then the gather's first blocks (every
+    // table of a block below 64: blocks hold at most kWaveBlock tables) are
+    // issued, and their rows are in flight while the other tables are
+    // routed. LDS operations of one wave complete in order: a block's codes
+    // are in the list before the block reads them.
+    route(0);
 
     // 3. gather
     const int g = lane >> lpr_log2, j = lane & ((1 << lpr_log2) - 1);
@@ -612,8 +617,10 @@ __global__ __launch_bounds__(kWaveThreads) void pairwise_forward_wave_kernel(Fwd
     // summed too (zeros), so that every wait counts exactly the loads issued
     // since (a conditional issue would merge two counts into the smaller).
     u32x4 w[K][kWaveBlock];
+    static_assert((K - 1) * kWaveBlock <= kWave, "the prefetched blocks lie in the first 64 tables");
 #pragma unroll
     for (int q = 0; q < K - 1; ++q) issue(q, w[q]);
+    for (int t0 = kWave; t0 < a.tables; t0 += kWave) route(t0);
     for (int b0 = 0; b0 < nblk; b0 += K) {
 #pragma unroll
         for (int q = 0; q < K; ++q) {
