@@ -130,3 +130,27 @@ def test_route_debug_attributes_are_settable():
     layer._last_indices = None
     layer._last_margins = None
     assert layer._last_indices is None and layer._last_margins is None and layer._last_codes is None
+
+
+def test_committed_counter_profiles_match_the_kernel_sources():
+    """bench.py takes each kernel's HBM bytes and L2 hit rate from the
+    committed rocprofv3 summaries (profiles/traffic*.json) only while the
+    kernel sources, comments aside, hash to the digest the profile was made
+    from; otherwise its roofline falls back to compulsory bytes. A kernel
+    change committed without new counter passes shows up here rather than as
+    a silently weaker bench line."""
+    root = Path(__file__).resolve().parents[1]
+    sys.path.insert(0, str(root))
+    import json
+
+    import bench
+
+    digest = bench.source_digest()
+    for name in ("traffic.json", "traffic_c1.json", "traffic_c3.json", "traffic_c4.json"):
+        rec = json.loads((root / "profiles" / name).read_text())
+        assert rec["source_digest"] == digest, f"profiles/{name} was made from other kernel sources"
+        assert rec["kernels"], name
+        for kernel, k in rec["kernels"].items():
+            assert k["fetch_bytes"] > 0 and k["write_bytes"] >= 0, (name, kernel)
+    for md in (root / "profiles").glob("c[1-5]_*.md"):
+        assert digest in md.read_text(), f"{md.name} names another digest of the kernel sources"
